@@ -1,0 +1,195 @@
+"""ctypes binding of libdlhip.so (the C ABI declared in include/dolittle_hip.h).
+
+The product path has no CPU fallback: if the HIP library is missing this
+module raises at import of the first entry point that needs it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "libdlhip.so")
+HEADER = os.path.join(HERE, "..", "include", "dolittle_hip.h")
+
+_lib = None
+
+u8p = C.POINTER(C.c_uint8)
+u16p = C.POINTER(C.c_uint16)
+u32p = C.POINTER(C.c_uint32)
+u64p = C.POINTER(C.c_uint64)
+vp = C.c_void_p
+vpp = C.POINTER(C.c_void_p)
+u64 = C.c_uint64
+u32 = C.c_uint32
+i32 = C.c_int32
+cint = C.c_int
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("arch", C.c_char * 64), ("compute_units", C.c_uint32),
+                ("reserved", C.c_uint32), ("total_bytes", C.c_uint64)]
+
+
+class Qwen3Config(C.Structure):
+    _fields_ = [("layers", C.c_uint32), ("hidden", C.c_uint32), ("q_heads", C.c_uint32),
+                ("kv_heads", C.c_uint32), ("head_dim", C.c_uint32), ("ffn", C.c_uint32),
+                ("vocab", C.c_uint32), ("tied_embeddings", C.c_uint32), ("rms_eps", C.c_float),
+                ("reserved", C.c_uint32), ("rope_theta", C.c_double)]
+
+
+class Sampling(C.Structure):
+    _fields_ = [("mode", C.c_uint32), ("top_k", C.c_uint32), ("temperature", C.c_double),
+                ("top_p", C.c_double)]
+
+
+class GenerationResult(C.Structure):
+    _fields_ = [("generated", C.c_uint32), ("reason", C.c_uint32), ("status", C.c_uint32),
+                ("reserved", C.c_uint32), ("position", C.c_uint64)]
+
+
+# name -> argument types (all return int status)
+SIGNATURES = {
+    "dl_device_open": [cint, vpp],
+    "dl_device_close": [vp],
+    "dl_device_info_get": [vp, C.POINTER(DeviceInfo)],
+    "dl_memory_snapshot": [vp, u64p, u64p],
+    "dl_buffer_alloc": [vp, u64, u64, vpp],
+    "dl_staging_alloc": [vp, u64, vpp],
+    "dl_buffer_free": [vp],
+    "dl_buffer_address": [vp, vpp],
+    "dl_buffer_size": [vp, u64p],
+    "dl_queue_create": [vp, vpp],
+    "dl_queue_destroy": [vp],
+    "dl_queue_upload": [vp, vp, u64, vp, u64, u64],
+    "dl_queue_download": [vp, vp, u64, vp, u64, u64],
+    "dl_queue_copy": [vp, vp, u64, vp, u64, u64],
+    "dl_queue_write": [vp, vp, u64, vp, u64],
+    "dl_queue_read": [vp, vp, vp, u64, u64],
+    "dl_queue_mark": [vp, u64p],
+    "dl_queue_wait": [vp, u64],
+    "dl_queue_drain": [vp],
+    "dl_event_create": [vp, vpp],
+    "dl_event_destroy": [vp],
+    "dl_event_record": [vp, vp],
+    "dl_event_elapsed_ms": [vp, vp, C.POINTER(C.c_float)],
+    "dl_projection": [vp, cint, vp, vp, vp, u64, u64, u64, vp],
+    "dl_rms_norm": [vp, cint, vp, vp, vp, u64, u64, C.c_float],
+    "dl_rotary": [vp, cint, vp, vp, u64, u64, u64, u64, C.c_double, vp, cint],
+    "dl_attention_scale": [vp, vp, u64],
+    "dl_attention": [vp, cint, vp, vp, vp, vp, u64, u64, u64, u64, u64, vp, u64, vp],
+    "dl_embedding": [vp, cint, vp, vp, vp, u64, u64, u64],
+    "dl_add": [vp, cint, vp, vp, vp, u64],
+    "dl_silu_multiply": [vp, cint, vp, vp, vp, u64],
+    "dl_gather_rows": [vp, vp, vp, u64, u64p, u64],
+    "dl_projection_packed_bytes": [u64, u64, u64p],
+    "dl_projection_pack": [vp, vp, vp, u64, u64],
+    "dl_projection_packed": [vp, vp, vp, vp, u64, u64, u64, vp],
+    "dl_qwen3_create": [vp, vp, C.POINTER(Qwen3Config), vpp],
+    "dl_qwen3_destroy": [vp],
+    "dl_qwen3_fill_synthetic": [vp, vp, u64, C.c_float],
+    "dl_qwen3_write_tensor": [vp, vp, cint, u32, u16p, u64],
+    "dl_qwen3_read_tensor": [vp, vp, cint, u32, u16p, u64],
+    "dl_qwen3_resident_bytes": [vp, u64p],
+    "dl_plan_create": [vp, vp, u32, u32, vpp],
+    "dl_plan_destroy": [vp],
+    "dl_plan_reset": [vp],
+    "dl_plan_position": [vp, u64p],
+    "dl_plan_write_cache": [vp, u32, u32, u64, u64, u16p, u16p],
+    "dl_plan_read_cache": [vp, u32, u32, u64, u64, u16p, u16p],
+    "dl_plan_seek": [vp, u64],
+    "dl_plan_read_hidden": [vp, u32, u16p],
+    "dl_plan_forward": [vp, u32p, u32],
+    "dl_plan_read_logits": [vp, u32, u16p],
+    "dl_plan_logits_address": [vp, u32, vpp],
+    "dl_plan_set_capture": [vp, i32],
+    "dl_plan_read_capture": [vp, u32, u64, u64, u16p],
+    "dl_plan_set_steering": [vp, u32, i32, C.POINTER(C.c_float)],
+    "dl_plan_set_embedding_override": [vp, u64, u16p, u32],
+    "dl_plan_generate": [vp, u32p, u32, u32, C.POINTER(Sampling), u64p, u32p, u32],
+    "dl_plan_prepare_generation": [vp, u32p, u32, u32, C.POINTER(Sampling), u64p, u32p, u32],
+    "dl_plan_decode_steps": [vp, u32],
+    "dl_plan_collect": [vp, u32p, u32, C.POINTER(GenerationResult)],
+    "dl_plan_request_stop": [vp],
+    "dl_sampler_create": [vp, vp, u64, cint, vpp],
+    "dl_sampler_destroy": [vp],
+    "dl_sampler_submit": [vp, vp, C.POINTER(Sampling), u64],
+    "dl_sampler_start": [vp, C.POINTER(Sampling), u64],
+    "dl_sampler_submit_next": [vp, vp],
+    "dl_sampler_result": [vp, u32p, u32p],
+}
+
+
+class DolittleError(RuntimeError):
+    """Base class; the subclass mirrors the reference exception type."""
+
+
+class InvalidArgument(DolittleError, ValueError):
+    pass
+
+
+class LengthError(DolittleError):
+    pass
+
+
+class DeviceError(DolittleError):
+    pass
+
+
+class Poisoned(DeviceError):
+    pass
+
+
+_STATUS = {1: InvalidArgument, 2: LengthError, 3: DeviceError, 4: Poisoned}
+
+
+def header_functions() -> list[str]:
+    """Every function declared by include/dolittle_hip.h."""
+    with open(HEADER) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:int|const char\*)\s+(dl_[a-z0-9_]+)\s*\(", text, flags=re.M)
+
+
+def load():
+    """Loads libdlhip.so; raises if the HIP extension is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIBRARY):
+        raise ImportError(f"libdlhip.so is not built ({LIBRARY}); run `python -m dolittle_amd.build`")
+    lib = C.CDLL(LIBRARY)
+    lib.dl_last_error.restype = C.c_char_p
+    lib.dl_last_error.argtypes = []
+    for name, args in SIGNATURES.items():
+        try:
+            fn = getattr(lib, name)
+        except AttributeError:
+            continue  # reported by missing_exports() and the ABI test
+        fn.argtypes = args
+        fn.restype = cint
+    _lib = lib
+    return lib
+
+
+def missing_exports() -> list[str]:
+    """Functions declared by the header but not exported by the library."""
+    lib = load()
+    missing = []
+    for name in header_functions():
+        try:
+            getattr(lib, name)
+        except AttributeError:
+            missing.append(name)
+    return missing
+
+
+def check(status: int) -> None:
+    if status != 0:
+        message = load().dl_last_error().decode(errors="replace")
+        raise _STATUS.get(status, DolittleError)(message or f"status {status}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args))

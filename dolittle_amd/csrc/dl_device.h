@@ -1,0 +1,48 @@
+// Device-side helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "dl_common.h"
+#include "dl_math.h"
+
+namespace dl {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Storage-typed element access: uint16_t holds BF16 bits, float is FP32.
+__device__ __forceinline__ float load_elem(const uint16_t* p, size_t i) { return dl_bf16_to_f32(p[i]); }
+__device__ __forceinline__ float load_elem(const float* p, size_t i) { return p[i]; }
+__device__ __forceinline__ void store_elem(uint16_t* p, size_t i, float v) { p[i] = dl_f32_to_bf16(v); }
+__device__ __forceinline__ void store_elem(float* p, size_t i, float v) { p[i] = v; }
+
+// One explicit storage-rounding point for storage type T.
+template <class T>
+__device__ __forceinline__ float storage_round(float v);
+template <>
+__device__ __forceinline__ float storage_round<uint16_t>(float v) {
+  return dl_round_bf16(v);
+}
+template <>
+__device__ __forceinline__ float storage_round<float>(float v) {
+  return v;
+}
+
+__device__ __forceinline__ float fma_rn(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+
+// Streaming 16-byte load that bypasses cache retention (weights are read once).
+__device__ __forceinline__ u32x4 load_stream(const u32x4* p) { return __builtin_nontemporal_load(p); }
+
+// 1/sqrt(x) from two correctly rounded IEEE operations (the reference's
+// native rsqrtf is unpinned; this build fixes the value on host and device).
+__device__ __forceinline__ float inverse_sqrt(float x) { return 1.0f / __builtin_sqrtf(x); }
+
+// Reads the device-owned position when one is bound, else the host value.
+__device__ __forceinline__ uint64_t position_or(const uint64_t* device_position, uint64_t host) {
+  return device_position ? *device_position : host;
+}
+
+}  // namespace dl

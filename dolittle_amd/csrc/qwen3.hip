@@ -1,0 +1,1555 @@
+// Qwen3 resident model, cached forward plan and device-owned token loop.
+//
+// Recipe (src/models/qwen3/model.cpp:343-409), per block:
+//   x = RMSNorm(h); q,k,v = x Wq, x Wk, x Wv; q,k = RoPE(RMSNorm_head(q,k));
+//   cache append; a = attention; h = h + a Wo; x = RMSNorm(h);
+//   h = h + (SiLU(x Wg) * (x Wu)) Wd
+// then final RMSNorm of the last row and the LM head.
+//
+// Kernel fusion (each fused kernel keeps every storage-rounding point of the
+// unfused operations, so results equal the reference operator sequence):
+//   k_step_begin   embedding lookup (or embedding override) into h
+//   k_qkv          RMSNorm prologue + packed Q|K|V GEMV; V stored straight into
+//                  the V cache (the reference's positioned output)
+//   k_attn_qk      per-head QK RMSNorm + RoPE prologue, K cache append, scores
+//   k_attn_softmax max, exp, 32-partial denominator, p = e / l
+//   k_attn_pv      the two ascending PV key ranges
+//   k_residual     packed O or down GEMV + residual add (+ steering, capture)
+//   k_gateup       RMSNorm prologue + packed gate|up GEMV + SiLU*up
+//   k_lm_head      final RMSNorm prologue + packed LM head + argmax partials
+//   k_step_end     greedy selection, token stream, position and stop latches
+// One decode step is captured once into a hipGraph and replayed; every kernel
+// reads the device-owned position and exits at once when the loop is
+// inactive, replacing the reference's conditional CUDA graph nodes
+// (src/kernels/cuda/decode.cu:103-194, 339-353), which HIP lacks.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <vector>
+
+#include "dl_device.h"
+#include "dl_internal.h"
+#include "dl_synth.h"
+#include "gemv.h"
+
+namespace dl {
+
+// Device-owned loop state (the reference's decode.cu State + Control).
+struct Control {
+  uint64_t position;        // absolute position consumed by the current step
+  uint32_t active;          // loop running
+  uint32_t prompt_length;   // positions [0, prompt_length) come from `tokens`
+  uint32_t generated;       // selections made so far (per sequence, lockstep)
+  uint32_t max_new;         // selection budget
+  uint32_t stop_pending;    // last selection made; the next step only consumes
+  uint32_t finished_mask;   // sequences that emitted a stop id
+  uint32_t all_mask;        // (1 << batch) - 1
+  uint32_t status;          // 0 ok, 1 NaN/+inf logit, 2 no finite logit, 4 bad token
+  uint32_t reason;          // 0 limit, 1 eos, 2 cancelled, 3 failure
+  uint32_t mode;            // 0 greedy, 1 categorical
+  uint32_t override_active;
+  uint32_t override_mask;
+  uint64_t override_position;
+  int32_t capture_layer;
+  int32_t steer_layer;
+  uint32_t steer_mask;
+  uint32_t select_row;      // 1 when the current step selects (set by k_step_begin)
+};
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kBlock = kWaves * 64;
+constexpr int kHeadDim = 128;
+
+__device__ __forceinline__ uint16_t bf16_bits(float v) { return dl_f32_to_bf16(v); }
+__device__ __forceinline__ float rbf(float v) { return dl_round_bf16(v); }
+
+// SiluMultiply on BF16-rounded operands (elementwise.cu:62-87).
+__device__ __forceinline__ float silu_times(float a, float b) {
+  const float e = dl_expf(a >= 0.0f ? -a : a);
+  const float sigmoid = a >= 0.0f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+  return rbf(a * sigmoid) * b;
+}
+
+// Step selects a token when the prompt is consumed and the budget is open.
+__device__ __forceinline__ bool selecting(const Control* c) { return c->select_row != 0; }
+
+// ------------------------------------------------------------ weight layout
+// Which packed matrix an element of a logical parameter belongs to.
+struct PackedView {
+  uint16_t* base;   // packed storage of the (possibly combined) matrix
+  int P;            // partials of the logical projection
+  uint64_t cols;    // input width
+  int combined;     // 0 plain, 1 gate rows, 2 up rows of the interleaved gate|up matrix
+};
+
+__host__ __device__ inline uint64_t view_index(const PackedView& v, uint64_t r, uint64_t k) {
+  uint64_t R = r;
+  if (v.combined == 1) R = 4 * (r / 2) + (r % 2);
+  if (v.combined == 2) R = 4 * (r / 2) + 2 + (r % 2);
+  return packed_index(R, k, v.P, v.cols);
+}
+
+// Seeded N(0, std) fill of a logical [rows, cols] matrix into its view.
+__global__ void k_fill_view(PackedView v, uint64_t rows, uint64_t seed, uint64_t stream, float scale) {
+  const uint64_t n = rows * v.cols;
+  const uint64_t step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step) {
+    const uint64_t r = i / v.cols, k = i % v.cols;
+    v.base[view_index(v, r, k)] = dl_normal_bf16(seed, stream, i, scale);
+  }
+}
+
+__global__ void k_fill_const(uint16_t* p, uint64_t n, uint16_t value) {
+  const uint64_t step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step) p[i] = value;
+}
+
+// Row-major <-> packed transfers of one logical matrix.
+__global__ void k_pack_view(PackedView v, uint64_t rows, const uint16_t* src, int unpack, uint16_t* dst) {
+  const uint64_t n = rows * v.cols;
+  const uint64_t step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step) {
+    const uint64_t r = i / v.cols, k = i % v.cols;
+    if (unpack)
+      dst[i] = v.base[view_index(v, r, k)];
+    else
+      v.base[view_index(v, r, k)] = src[i];
+  }
+}
+
+// RoPE cos/sin table rope[pos][i] = (round(cos a), round(sin a)) with
+// a = FP32(pos) * FP32(1/pow(theta, FP32(2i)/FP32(d))) (rotary.cu:84-126).
+__global__ void k_rope_table(float* rope, uint64_t positions, int width, double theta) {
+  const int half = width / 2;
+  const uint64_t n = positions * half;
+  const uint64_t step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step) {
+    const uint64_t pos = i / half;
+    const int pair = static_cast<int>(i % half);
+    const float exponent = static_cast<float>(2 * pair) / static_cast<float>(width);
+    const float inverse_frequency = static_cast<float>(1.0 / dl_pow_pos(theta, static_cast<double>(exponent)));
+    const float angle = static_cast<float>(pos) * inverse_frequency;
+    double s, c;
+    dl_sincos(static_cast<double>(angle), &s, &c);
+    rope[2 * i] = rbf(static_cast<float>(c));
+    rope[2 * i + 1] = rbf(static_cast<float>(s));
+  }
+}
+
+// ----------------------------------------------------------- control kernels
+struct InitArgs {
+  Control* ctl;
+  uint64_t position;
+  uint32_t prompt_length, max_new, batch, mode;
+  int32_t capture_layer, steer_layer;
+  uint32_t steer_mask, override_active, override_mask;
+  uint64_t override_position;
+};
+
+__global__ void k_init_control(InitArgs a) {
+  Control c{};
+  c.position = a.position;
+  c.active = 1;
+  c.prompt_length = a.prompt_length;
+  c.generated = 0;
+  c.max_new = a.max_new;
+  c.stop_pending = a.max_new == 0 ? 1u : 0u;
+  c.finished_mask = 0;
+  c.all_mask = a.batch >= 32 ? 0xffffffffu : ((1u << a.batch) - 1u);
+  c.status = 0;
+  c.reason = 0;
+  c.mode = a.mode;
+  c.override_active = a.override_active;
+  c.override_mask = a.override_mask;
+  c.override_position = a.override_position;
+  c.capture_layer = a.capture_layer;
+  c.steer_layer = a.steer_layer;
+  c.steer_mask = a.steer_mask;
+  c.select_row = 0;
+  *a.ctl = c;
+}
+
+struct BeginArgs {
+  Control* ctl;
+  const uint32_t* tokens;       // absolute-position token history [cap]
+  const uint32_t* selected;     // [B] last selection
+  uint16_t* h;                  // [B][D]
+  const uint16_t* lm_packed;    // tied: packed LM head (P = 16)
+  const uint16_t* embedding;    // untied: row-major [V][D]
+  const uint16_t* override_row; // [D]
+  const uint32_t* cancel;       // host-mapped cancel word
+  int D;
+  uint32_t V;
+  int tied;
+};
+
+// Embedding (embedding.cu:60-80), the embedding override, and the step's
+// selection decision.  Grid: one block per sequence.
+__global__ __launch_bounds__(kBlock) void k_step_begin(BeginArgs a) {
+  Control* c = a.ctl;
+  if (!c->active) return;
+  const uint64_t pos = c->position;
+  const int b = blockIdx.x;
+  if (b == 0 && threadIdx.x == 0) {
+    c->select_row = (pos + 1 >= c->prompt_length && !c->stop_pending) ? 1u : 0u;
+  }
+  const uint32_t token = pos < c->prompt_length ? a.tokens[pos] : a.selected[b];
+  uint16_t* out = a.h + static_cast<uint64_t>(b) * a.D;
+  const bool override_row = c->override_active && pos == c->override_position && ((c->override_mask >> b) & 1u);
+  if (override_row) {
+    for (int k = threadIdx.x; k < a.D; k += blockDim.x) out[k] = a.override_row[k];
+  } else if (token >= a.V) {
+    for (int k = threadIdx.x; k < a.D; k += blockDim.x) out[k] = 0;
+    if (threadIdx.x == 0) atomicOr(&c->status, 4u);
+  } else if (a.tied) {
+    for (int k = threadIdx.x; k < a.D; k += blockDim.x) out[k] = a.lm_packed[packed_index(token, k, 16, a.D)];
+  } else {
+    const uint16_t* row = a.embedding + static_cast<uint64_t>(token) * a.D;
+    for (int k = threadIdx.x; k < a.D; k += blockDim.x) out[k] = row[k];
+  }
+}
+
+// ------------------------------------------------------------- QKV GEMV
+struct QkvArgs {
+  const Control* ctl;
+  const uint16_t* h;
+  const uint16_t* norm;
+  const u32x4* w;            // packed Q (P=16) | K (P=32) | V (P=32)
+  uint16_t* q_out;           // [B][QW]
+  uint16_t* k_out;           // [B][KW]
+  uint16_t* v_cache;         // V^T of this layer, sequence 0: [KW][cap]
+  uint64_t cache_seq_stride; // elements
+  int D, QW, KW, cap;
+  float eps;
+};
+
+template <int B>
+__global__ __launch_bounds__(kBlock) void k_qkv(QkvArgs a) {
+  extern __shared__ float lds[];
+  float* xs16 = lds;
+  float* xs32 = xs16 + B * staged_floats(16, a.D);
+  __shared__ float scratch[40];
+  if (!a.ctl->active) return;
+  const uint64_t pos = a.ctl->position;
+  for (int b = 0; b < B; ++b) {
+    const uint16_t* hb = a.h + static_cast<uint64_t>(b) * a.D;
+    const float inverse = block_rms_inverse(hb, a.D, a.eps, scratch);
+    for (int i = threadIdx.x; i < a.D; i += blockDim.x) {
+      const float n = rbf(rbf(dl_bf16_to_f32(hb[i]) * inverse) * dl_bf16_to_f32(a.norm[i]));
+      stage_put<16>(xs16, a.D, b, i, n);
+      stage_put<32>(xs32, a.D, b, i, n);
+    }
+  }
+  __syncthreads();
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int q_tiles = a.QW / 4, k_tiles = a.KW / 2, total = q_tiles + 2 * k_tiles;
+  const uint64_t q_chunks = static_cast<uint64_t>(a.D / 128) * 64;
+  const uint64_t k_chunks = static_cast<uint64_t>(a.D / 256) * 64;
+  for (int tile = blockIdx.x * kWaves + wave; tile < total; tile += gridDim.x * kWaves) {
+    float acc[B];
+    if (tile < q_tiles) {
+      chain_tile<16, B>(a.w + tile * q_chunks, xs16, a.D, lane, acc);
+      if (lane % 16 == 0) {
+        const int row = tile * 4 + lane / 16;
+#pragma unroll
+        for (int b = 0; b < B; ++b) a.q_out[b * a.QW + row] = bf16_bits(acc[b]);
+      }
+    } else {
+      int kt = tile - q_tiles;
+      const bool is_v = kt >= k_tiles;
+      if (is_v) kt -= k_tiles;
+      chain_tile<32, B>(a.w + q_tiles * q_chunks + (is_v ? k_tiles : 0) * k_chunks + kt * k_chunks, xs32,
+                        a.D, lane, acc);
+      if (lane % 32 == 0) {
+        const int row = kt * 2 + lane / 32;
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+          if (is_v)
+            a.v_cache[b * a.cache_seq_stride + static_cast<uint64_t>(row) * a.cap + pos] = bf16_bits(acc[b]);
+          else
+            a.k_out[b * a.KW + row] = bf16_bits(acc[b]);
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- attention
+struct AttnArgs {
+  const Control* ctl;
+  const uint16_t* q_raw;     // [B][Hq*128]
+  const uint16_t* k_raw;     // [B][Hkv*128]
+  const uint16_t* q_norm;    // [128]
+  const uint16_t* k_norm;    // [128]
+  const float* rope;         // [cap][64][2]
+  uint16_t* k_cache;         // this layer, sequence 0: [Hkv][cap][128]
+  const uint16_t* v_cache;   // this layer, sequence 0: [Hkv*128][cap] (V^T)
+  uint64_t cache_seq_stride; // elements
+  float* scores;             // [B][Hq][cap]
+  float* probs;              // [B][Hq][cap]
+  uint16_t* att;             // [B][Hq*128]
+  int q_heads, kv_heads, cap;
+  float eps, scale;
+};
+
+// Per-head RMSNorm (width 128: lane t, component c holds feature t+32c;
+// normalization.cu:82-132) followed by RoPE (rotary.cu:84-126) for one head,
+// computed by one wavefront; lane i owns the RoPE pair (i, i+64).
+__device__ __forceinline__ void head_norm_rope(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gain,
+                                               const float* __restrict__ rope_pos, int lane, float eps,
+                                               float* out) {
+  const float xa = dl_bf16_to_f32(x[lane]);
+  const float xb = dl_bf16_to_f32(x[lane + 64]);
+  const float xa_hi = __shfl(xa, (lane + 32) & 63);
+  const float xb_hi = __shfl(xb, (lane + 32) & 63);
+  float s = ((xa * xa + xa_hi * xa_hi) + xb * xb) + xb_hi * xb_hi;
+#pragma unroll
+  for (int off = 1; off < 32; off *= 2) s = s + __shfl_down(s, off, 32);
+  const float total = __shfl(s, 0);
+  const float inverse = inverse_sqrt(total * (1.0f / 128.0f) + eps);
+  const float na = rbf(rbf(xa * inverse) * dl_bf16_to_f32(gain[lane]));
+  const float nb = rbf(rbf(xb * inverse) * dl_bf16_to_f32(gain[lane + 64]));
+  const float cosine = rope_pos[2 * lane], sine = rope_pos[2 * lane + 1];
+  out[lane] = rbf(rbf(na * cosine) - rbf(nb * sine));
+  out[lane + 64] = rbf(rbf(nb * cosine) + rbf(na * sine));
+}
+
+// Grid (kv head, 64-key tile, sequence); block 256 = 4 waves, one per query
+// head of the group.  Scores use 8 lanes per key, each an FMA chain over 16
+// contiguous features, merged at offsets 4,2,1 (attention.cu:231-300).
+__global__ __launch_bounds__(kBlock) void k_attn_qk(AttnArgs a) {
+  __shared__ float qs[4][kHeadDim];
+  __shared__ float ks[kHeadDim];
+  if (!a.ctl->active) return;
+  const uint64_t pos = a.ctl->position;
+  const int count = static_cast<int>(pos) + 1;
+  const int g = blockIdx.x, key0 = blockIdx.y * 64, b = blockIdx.z;
+  if (key0 >= count) return;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int group = a.q_heads / a.kv_heads;
+  const float* rope_pos = a.rope + pos * kHeadDim;
+  const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHeadDim, kw = static_cast<uint64_t>(a.kv_heads) * kHeadDim;
+  head_norm_rope(a.q_raw + b * qw + static_cast<uint64_t>(g * group + wave) * kHeadDim, a.q_norm, rope_pos, lane,
+                 a.eps, qs[wave]);
+  const bool has_new = pos >= static_cast<uint64_t>(key0) && pos < static_cast<uint64_t>(key0) + 64;
+  uint16_t* kc = a.k_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g) * a.cap * kHeadDim;
+  if (has_new && wave == 0) {
+    head_norm_rope(a.k_raw + b * kw + static_cast<uint64_t>(g) * kHeadDim, a.k_norm, rope_pos, lane, a.eps, ks);
+    kc[pos * kHeadDim + lane] = bf16_bits(ks[lane]);
+    kc[pos * kHeadDim + lane + 64] = bf16_bits(ks[lane + 64]);
+  }
+  __syncthreads();
+  const int kl = lane / 8, l = lane % 8;
+  float q[4][16];
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[h][i] = qs[h][16 * l + i];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int j = key0 + wave * 16 + it * 8 + kl;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (j < count) {
+      float kf[16];
+      if (static_cast<uint64_t>(j) == pos) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) kf[i] = ks[16 * l + i];
+      } else {
+        const u32x4* src = reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(j) * kHeadDim + 16 * l);
+        const u32x4 w0 = src[0], w1 = src[1];
+        kf[0] = dl_bf16_lo(w0.x); kf[1] = dl_bf16_hi(w0.x); kf[2] = dl_bf16_lo(w0.y); kf[3] = dl_bf16_hi(w0.y);
+        kf[4] = dl_bf16_lo(w0.z); kf[5] = dl_bf16_hi(w0.z); kf[6] = dl_bf16_lo(w0.w); kf[7] = dl_bf16_hi(w0.w);
+        kf[8] = dl_bf16_lo(w1.x); kf[9] = dl_bf16_hi(w1.x); kf[10] = dl_bf16_lo(w1.y); kf[11] = dl_bf16_hi(w1.y);
+        kf[12] = dl_bf16_lo(w1.z); kf[13] = dl_bf16_hi(w1.z); kf[14] = dl_bf16_lo(w1.w); kf[15] = dl_bf16_hi(w1.w);
+      }
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[h] = fma_rn(q[h][i], kf[i], acc[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int off = 4; off; off >>= 1) acc[h] = acc[h] + __shfl_down(acc[h], off, 8);
+    if (l == 0 && j < count) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        a.scores[(static_cast<uint64_t>(b) * a.q_heads + g * group + h) * a.cap + j] = acc[h] * a.scale;
+    }
+  }
+}
+
+// Grid (query head, sequence).  m = max, e = exp(s - m), denominator from 32
+// partials owning j mod 32 merged at offsets 16..1, p = e / l
+// (attention.cu:301-330).
+__global__ __launch_bounds__(kBlock) void k_attn_softmax(AttnArgs a) {
+  extern __shared__ float es[];
+  __shared__ float red[kBlock];
+  __shared__ float denominator_shared;
+  if (!a.ctl->active) return;
+  const int count = static_cast<int>(a.ctl->position) + 1;
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const uint64_t row = (static_cast<uint64_t>(b) * a.q_heads + h) * a.cap;
+  const float* sc = a.scores + row;
+  float m = sc[0];
+  for (int j = tid; j < count; j += kBlock) m = fmaxf(m, sc[j]);
+  red[tid] = m;
+  __syncthreads();
+  for (int off = kBlock / 2; off; off >>= 1) {
+    if (tid < off) red[tid] = fmaxf(red[tid], red[tid + off]);
+    __syncthreads();
+  }
+  m = red[0];
+  for (int j = tid; j < count; j += kBlock) es[j] = dl_expf(sc[j] - m);
+  __syncthreads();
+  if (tid < 32) {
+    float p = 0.0f;
+    for (int j = tid; j < count; j += 32) p = p + es[j];
+#pragma unroll
+    for (int off = 16; off; off >>= 1) p = p + __shfl_down(p, off, 32);
+    if (tid == 0) denominator_shared = p;
+  }
+  __syncthreads();
+  const float l = denominator_shared;
+  for (int j = tid; j < count; j += kBlock) a.probs[row + j] = es[j] / l;
+}
+
+// Grid (kv head * 16 feature blocks, sequence); one wavefront: lane =
+// (head in group, key half, feature).  Each output feature is
+// round(A + B), A and B ascending FMA chains over the first ceil(n/2) keys
+// and the rest (attention.cu:331-375).  V is stored transposed so a lane
+// reads 8 consecutive keys of its feature per 16-byte load.
+__global__ __launch_bounds__(64) void k_attn_pv(AttnArgs a) {
+  if (!a.ctl->active) return;
+  const int count = static_cast<int>(a.ctl->position) + 1;
+  const int split = (count - 1) / 2 + 1;
+  const int g = blockIdx.x / 16, fb = blockIdx.x % 16, b = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int hl = lane / 16, half = (lane / 8) % 2, fl = lane % 8;
+  const int group = a.q_heads / a.kv_heads;
+  const int h = g * group + hl, f = fb * 8 + fl;
+  const float* p = a.probs + (static_cast<uint64_t>(b) * a.q_heads + h) * a.cap;
+  const uint16_t* v = a.v_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g * kHeadDim + f) * a.cap;
+  const int begin = half ? split : 0, end = half ? count : split;
+  float acc = 0.0f;
+  int j = begin;
+  for (; j < end && (j & 7); ++j) acc = fma_rn(p[j], dl_bf16_to_f32(v[j]), acc);
+  for (; j + 8 <= end; j += 8) {
+    const u32x4 vv = *reinterpret_cast<const u32x4*>(v + j);
+    const float4 pa = *reinterpret_cast<const float4*>(p + j);
+    const float4 pb = *reinterpret_cast<const float4*>(p + j + 4);
+    acc = fma_rn(pa.x, dl_bf16_lo(vv.x), acc);
+    acc = fma_rn(pa.y, dl_bf16_hi(vv.x), acc);
+    acc = fma_rn(pa.z, dl_bf16_lo(vv.y), acc);
+    acc = fma_rn(pa.w, dl_bf16_hi(vv.y), acc);
+    acc = fma_rn(pb.x, dl_bf16_lo(vv.z), acc);
+    acc = fma_rn(pb.y, dl_bf16_hi(vv.z), acc);
+    acc = fma_rn(pb.z, dl_bf16_lo(vv.w), acc);
+    acc = fma_rn(pb.w, dl_bf16_hi(vv.w), acc);
+  }
+  for (; j < end; ++j) acc = fma_rn(p[j], dl_bf16_to_f32(v[j]), acc);
+  const float other = __shfl_down(acc, 8, 16);
+  if (half == 0) a.att[static_cast<uint64_t>(b) * a.q_heads * kHeadDim + h * kHeadDim + f] = bf16_bits(acc + other);
+}
+
+// ------------------------------------------------- residual GEMV (O, down)
+struct ResidualArgs {
+  const Control* ctl;
+  const uint16_t* x;     // [B][I]
+  const u32x4* w;        // packed [D][I]
+  uint16_t* h;           // [B][D], updated in place
+  uint16_t* capture;     // [B][cap][D] or null
+  const float* steer;    // [B][D] or null
+  int I, D, cap, layer;
+};
+
+// y = round(x W^T); h = round(h + y); optionally h = round(h + steer) and a
+// copy of h into the capture arena at the current position.
+template <int P, int B>
+__global__ __launch_bounds__(kBlock) void k_residual(ResidualArgs a) {
+  extern __shared__ float xs[];
+  if (!a.ctl->active) return;
+  const uint64_t pos = a.ctl->position;
+  for (int b = 0; b < B; ++b) {
+    const uint16_t* xb = a.x + static_cast<uint64_t>(b) * a.I;
+    for (int i = threadIdx.x; i < a.I; i += blockDim.x) stage_put<P>(xs, a.I, b, i, dl_bf16_to_f32(xb[i]));
+  }
+  __syncthreads();
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  constexpr int RW = 64 / P;
+  const int tiles = a.D / RW;
+  const uint64_t chunks = static_cast<uint64_t>(a.I / (8 * P)) * 64;
+  const bool steer = a.steer != nullptr && a.layer == a.ctl->steer_layer;
+  const bool capture = a.capture != nullptr && a.layer == a.ctl->capture_layer;
+  const uint32_t steer_mask = a.ctl->steer_mask;
+  for (int tile = blockIdx.x * kWaves + wave; tile < tiles; tile += gridDim.x * kWaves) {
+    float acc[B];
+    chain_tile<P, B>(a.w + tile * chunks, xs, a.I, lane, acc);
+    if (lane % P == 0) {
+      const int row = tile * RW + lane / P;
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const uint64_t at = static_cast<uint64_t>(b) * a.D + row;
+        float value = rbf(dl_bf16_to_f32(a.h[at]) + rbf(acc[b]));
+        if (steer && ((steer_mask >> b) & 1u)) value = rbf(value + a.steer[at]);
+        a.h[at] = bf16_bits(value);
+        if (capture) a.capture[(static_cast<uint64_t>(b) * a.cap + pos) * a.D + row] = bf16_bits(value);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ gate/up GEMV
+struct GateUpArgs {
+  const Control* ctl;
+  const uint16_t* h;
+  const uint16_t* norm;
+  const u32x4* w;        // packed interleaved rows [g 2j, g 2j+1, u 2j, u 2j+1]
+  uint16_t* act;         // [B][F]
+  int D, F;
+  float eps;
+};
+
+template <int B>
+__global__ __launch_bounds__(kBlock) void k_gateup(GateUpArgs a) {
+  extern __shared__ float xs[];
+  __shared__ float scratch[40];
+  if (!a.ctl->active) return;
+  for (int b = 0; b < B; ++b) {
+    const uint16_t* hb = a.h + static_cast<uint64_t>(b) * a.D;
+    const float inverse = block_rms_inverse(hb, a.D, a.eps, scratch);
+    for (int i = threadIdx.x; i < a.D; i += blockDim.x)
+      stage_put<16>(xs, a.D, b, i, rbf(rbf(dl_bf16_to_f32(hb[i]) * inverse) * dl_bf16_to_f32(a.norm[i])));
+  }
+  __syncthreads();
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int tiles = a.F / 2;
+  const uint64_t chunks = static_cast<uint64_t>(a.D / 128) * 64;
+  for (int tile = blockIdx.x * kWaves + wave; tile < tiles; tile += gridDim.x * kWaves) {
+    float acc[B];
+    chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc);
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const float up = __shfl_down(acc[b], 32, 64);
+      if (lane == 0 || lane == 16) {
+        const int o = tile * 2 + lane / 16;
+        a.act[static_cast<uint64_t>(b) * a.F + o] = bf16_bits(silu_times(rbf(acc[b]), rbf(up)));
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ LM head
+struct HeadArgs {
+  const Control* ctl;
+  const uint16_t* h;
+  const uint16_t* norm;
+  const u32x4* w;          // packed [V][D], P = 16
+  uint16_t* logits;        // [B][V]
+  uint64_t* partial_keys;  // [B][gridDim.x]
+  uint32_t* partial_flags; // [B][gridDim.x]
+  int D;
+  uint32_t V;
+  float eps;
+};
+
+// Orders BF16 logits: key = (ordered value << 32) | ~id, so the maximum key
+// is the largest value with the lowest id (categorical.cpp:168-173).
+// Flags: bit 0 NaN or +inf seen, bit 1 a finite candidate seen.
+__device__ __forceinline__ void logit_key(uint16_t bits, uint32_t id, uint64_t* key, uint32_t* flags) {
+  const uint32_t magnitude = bits & 0x7fffu;
+  if (magnitude > 0x7f80u || bits == 0x7f80u) {
+    *flags |= 1u;
+    return;
+  }
+  if (bits == 0xff80u) return;
+  *flags |= 2u;
+  const uint32_t canonical = bits == 0x8000u ? 0u : bits;
+  const uint32_t ordered = (canonical & 0x8000u) ? (~canonical & 0xffffu) : (canonical | 0x8000u);
+  const uint64_t k = (static_cast<uint64_t>(ordered) << 32) | (0xffffffffu - id);
+  if (k > *key) *key = k;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off; off >>= 1) {
+    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), off);
+    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), off);
+    const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+template <int B>
+__global__ __launch_bounds__(kBlock) void k_lm_head(HeadArgs a) {
+  extern __shared__ float xs[];
+  __shared__ float scratch[40];
+  __shared__ uint64_t wave_keys[kWaves][B];
+  __shared__ uint32_t wave_flags[kWaves][B];
+  if (!a.ctl->active || !selecting(a.ctl)) return;
+  for (int b = 0; b < B; ++b) {
+    const uint16_t* hb = a.h + static_cast<uint64_t>(b) * a.D;
+    const float inverse = block_rms_inverse(hb, a.D, a.eps, scratch);
+    for (int i = threadIdx.x; i < a.D; i += blockDim.x)
+      stage_put<16>(xs, a.D, b, i, rbf(rbf(dl_bf16_to_f32(hb[i]) * inverse) * dl_bf16_to_f32(a.norm[i])));
+  }
+  __syncthreads();
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int tiles = static_cast<int>(a.V / 4);
+  const uint64_t chunks = static_cast<uint64_t>(a.D / 128) * 64;
+  uint64_t best[B];
+  uint32_t flags[B];
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    best[b] = 0;
+    flags[b] = 0;
+  }
+  for (int tile = blockIdx.x * kWaves + wave; tile < tiles; tile += gridDim.x * kWaves) {
+    float acc[B];
+    chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc);
+    if (lane % 16 == 0) {
+      const uint32_t row = static_cast<uint32_t>(tile * 4 + lane / 16);
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const uint16_t bits = bf16_bits(acc[b]);
+        a.logits[static_cast<uint64_t>(b) * a.V + row] = bits;
+        logit_key(bits, row, &best[b], &flags[b]);
+      }
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    const uint64_t k = wave_max_u64(best[b]);
+    uint32_t f = flags[b];
+#pragma unroll
+    for (int off = 32; off; off >>= 1) f |= __shfl_xor(f, off);
+    if (lane == 0) {
+      wave_keys[wave][b] = k;
+      wave_flags[wave][b] = f;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < B) {
+    const int b = threadIdx.x;
+    uint64_t k = 0;
+    uint32_t f = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      k = wave_keys[w][b] > k ? wave_keys[w][b] : k;
+      f |= wave_flags[w][b];
+    }
+    a.partial_keys[static_cast<uint64_t>(b) * gridDim.x + blockIdx.x] = k;
+    a.partial_flags[static_cast<uint64_t>(b) * gridDim.x + blockIdx.x] = f;
+  }
+}
+
+// ---------------------------------------------------------------- step end
+struct EndArgs {
+  Control* ctl;
+  const uint64_t* partial_keys;
+  const uint32_t* partial_flags;
+  int partials;
+  uint32_t* selected;       // [B]
+  uint32_t* out_tokens;     // [B][out_capacity]
+  uint32_t out_capacity;
+  const uint8_t* stop_mask; // [V]
+  const uint32_t* cancel;   // host-mapped cancel word
+  int batch;
+};
+
+// Greedy selection from the argmax partials, token stream, stop latches
+// and position advance (decode.cu finish_selection / finish_consumption).
+__global__ __launch_bounds__(kBlock) void k_step_end(EndArgs a) {
+  __shared__ uint64_t keys[kBlock];
+  __shared__ uint32_t flags[kBlock];
+  Control* c = a.ctl;
+  if (!c->active) return;
+  const bool select = selecting(c);
+  if (select && c->mode == 0) {
+    for (int b = 0; b < a.batch; ++b) {
+      uint64_t k = 0;
+      uint32_t f = 0;
+      for (int i = threadIdx.x; i < a.partials; i += blockDim.x) {
+        const uint64_t v = a.partial_keys[static_cast<uint64_t>(b) * a.partials + i];
+        k = v > k ? v : k;
+        f |= a.partial_flags[static_cast<uint64_t>(b) * a.partials + i];
+      }
+      keys[threadIdx.x] = k;
+      flags[threadIdx.x] = f;
+      __syncthreads();
+      for (int off = kBlock / 2; off; off >>= 1) {
+        if (threadIdx.x < off) {
+          keys[threadIdx.x] = keys[threadIdx.x + off] > keys[threadIdx.x] ? keys[threadIdx.x + off] : keys[threadIdx.x];
+          flags[threadIdx.x] |= flags[threadIdx.x + off];
+        }
+        __syncthreads();
+      }
+      if (threadIdx.x == 0) {
+        if (flags[0] & 1u) {
+          c->status |= 1u;
+        } else if (!(flags[0] & 2u)) {
+          c->status |= 2u;
+        } else {
+          const uint32_t id = 0xffffffffu - static_cast<uint32_t>(keys[0] & 0xffffffffu);
+          a.selected[b] = id;
+          if (c->generated < a.out_capacity) a.out_tokens[static_cast<uint64_t>(b) * a.out_capacity + c->generated] = id;
+          if (a.stop_mask[id]) c->finished_mask |= 1u << b;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (threadIdx.x != 0) return;
+  if (select) {
+    c->generated += 1;
+    if (c->generated >= c->max_new || (c->finished_mask & c->all_mask) == c->all_mask) c->stop_pending = 1;
+  } else if (c->stop_pending && c->position + 1 >= c->prompt_length) {
+    // The final selection has now been consumed (decode.cu finish_consumption).
+    c->active = 0;
+    c->reason = (c->max_new > 0 && (c->finished_mask & c->all_mask) == c->all_mask) ? 1u : 0u;
+  }
+  if (c->status) {
+    c->active = 0;
+    c->reason = 3;
+  }
+  if (c->active && __hip_atomic_load(a.cancel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
+    c->active = 0;
+    c->reason = 2;
+  }
+  c->position += 1;
+}
+
+// Row-major seeded N(0, std) fill (untied embedding table).
+__global__ void k_fill_rowmajor(uint16_t* p, uint64_t n, uint64_t seed, uint64_t stream, float scale) {
+  const uint64_t step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step)
+    p[i] = dl_normal_bf16(seed, stream, i, scale);
+}
+
+// Partial count of the reference projection rule (projection.cu:277-318).
+int partials_for(uint64_t in_w, uint64_t out_w) { return (in_w <= 4096 && out_w > 1024) ? 16 : 32; }
+
+__global__ void k_seek(Control* c, uint64_t position) {
+  c->position = position;
+  c->active = 0;
+}
+
+// Reference-layout cache rows [count][Hkv][128] <-> the plan's layout:
+// K head-major [Hkv][cap][128], V transposed [Hkv*128][cap].
+__global__ void k_cache_rows(uint16_t* k_cache, uint16_t* v_cache, int cap, int kv_heads, uint64_t first,
+                             uint64_t count, uint16_t* keys, uint16_t* values, int read) {
+  const uint64_t n = count * kv_heads * kHeadDim;
+  const uint64_t step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step) {
+    const uint64_t j = first + i / (kv_heads * kHeadDim);
+    const uint64_t g = (i / kHeadDim) % kv_heads, f = i % kHeadDim;
+    uint16_t* kp = k_cache + (g * cap + j) * kHeadDim + f;
+    uint16_t* vp = v_cache + (g * kHeadDim + f) * cap + j;
+    if (read) {
+      keys[i] = *kp;
+      values[i] = *vp;
+    } else {
+      *kp = keys[i];
+      *vp = values[i];
+    }
+  }
+}
+
+}  // namespace
+}  // namespace dl
+
+// ===================================================================== host
+using dl::guard;
+using dl::require;
+
+struct dl_qwen3 {
+  dl_device* device = nullptr;
+  dl_qwen3_config cfg{};
+  int p_q = 16, p_kv = 32, p_o = 16, p_gu = 16, p_down = 32, p_lm = 16;
+  uint64_t qkv_elems = 0, o_elems = 0, gu_elems = 0, down_elems = 0;
+  std::vector<uint16_t*> qkv, o, gu, down, input_norm, post_norm, q_norm, k_norm;
+  uint16_t* final_norm = nullptr;
+  uint16_t* lm_head = nullptr;    // packed
+  uint16_t* embedding = nullptr;  // row-major, untied only
+  uint64_t resident = 0;
+  std::vector<void*> allocations;
+
+  uint16_t* alloc(uint64_t elements) {
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, elements * 2);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      dl::fail(DL_LENGTH_ERROR, std::string("model allocation failed: ") + hipGetErrorString(e));
+    }
+    allocations.push_back(p);
+    resident += elements * 2;
+    return static_cast<uint16_t*>(p);
+  }
+
+  // The view of one logical parameter inside the packed storage.
+  dl::PackedView view(int role, uint32_t layer, uint64_t* rows, uint64_t* cols) const {
+    const uint64_t D = cfg.hidden, QW = uint64_t(cfg.q_heads) * cfg.head_dim,
+                   KW = uint64_t(cfg.kv_heads) * cfg.head_dim, F = cfg.ffn;
+    switch (role) {
+      case DL_ROLE_Q: *rows = QW; *cols = D; return {qkv[layer], p_q, D, 0};
+      case DL_ROLE_K: *rows = KW; *cols = D; return {qkv[layer] + QW * D, p_kv, D, 0};
+      case DL_ROLE_V: *rows = KW; *cols = D; return {qkv[layer] + (QW + KW) * D, p_kv, D, 0};
+      case DL_ROLE_O: *rows = D; *cols = QW; return {o[layer], p_o, QW, 0};
+      case DL_ROLE_GATE: *rows = F; *cols = D; return {gu[layer], p_gu, D, 1};
+      case DL_ROLE_UP: *rows = F; *cols = D; return {gu[layer], p_gu, D, 2};
+      case DL_ROLE_DOWN: *rows = D; *cols = F; return {down[layer], p_down, F, 0};
+      case DL_ROLE_LM_HEAD: *rows = cfg.vocab; *cols = D; return {lm_head, p_lm, D, 0};
+      default: dl::fail(DL_INVALID_ARGUMENT, "role has no packed view");
+    }
+  }
+
+  // Row-major vectors and tables.
+  uint16_t* plain(int role, uint32_t layer, uint64_t* elements) const {
+    const uint64_t D = cfg.hidden;
+    switch (role) {
+      case DL_ROLE_FINAL_NORM: *elements = D; return final_norm;
+      case DL_ROLE_INPUT_NORM: *elements = D; return input_norm[layer];
+      case DL_ROLE_POST_NORM: *elements = D; return post_norm[layer];
+      case DL_ROLE_Q_NORM: *elements = cfg.head_dim; return q_norm[layer];
+      case DL_ROLE_K_NORM: *elements = cfg.head_dim; return k_norm[layer];
+      case DL_ROLE_EMBEDDING:
+        if (cfg.tied_embeddings) return nullptr;
+        *elements = uint64_t(cfg.vocab) * D;
+        return embedding;
+      default: return nullptr;
+    }
+  }
+
+  ~dl_qwen3() {
+    for (void* p : allocations) (void)hipFree(p);
+  }
+};
+
+namespace {
+void validate_config(const dl_qwen3_config& c) {
+  require(c.layers > 0 && c.hidden > 0 && c.q_heads > 0 && c.kv_heads > 0 && c.ffn > 0 && c.vocab > 0,
+          "empty Qwen3 dimension");
+  require(c.head_dim == 128, "this backend requires head_dim 128");
+  require(c.q_heads == 4 * c.kv_heads, "this backend requires 4 query heads per KV head");
+  require(c.hidden % 256 == 0 && c.ffn % 256 == 0, "hidden and ffn widths must be multiples of 256");
+  require(uint64_t(c.q_heads) * c.head_dim % 256 == 0, "query width must be a multiple of 256");
+  require(c.vocab % 4 == 0, "vocabulary must be a multiple of 4");
+  require(c.rms_eps > 0.0f, "rms epsilon must be positive");
+  require(c.rope_theta > 0.0 && std::isfinite(c.rope_theta), "rope theta must be positive");
+}
+
+unsigned fill_grid(uint64_t n) { return static_cast<unsigned>(std::min<uint64_t>(dl::ceil_div(n, 256), 65535)); }
+}  // namespace
+
+extern "C" {
+
+int dl_qwen3_create(dl_device* device, dl_queue* queue, const dl_qwen3_config* config, dl_qwen3** out) {
+  return guard([&] {
+    require(device && config && out, "null argument");
+    dl::enter(queue);
+    validate_config(*config);
+    auto m = std::make_unique<dl_qwen3>();
+    m->device = device;
+    m->cfg = *config;
+    const auto& c = m->cfg;
+    const uint64_t D = c.hidden, QW = uint64_t(c.q_heads) * c.head_dim, KW = uint64_t(c.kv_heads) * c.head_dim,
+                   F = c.ffn, V = c.vocab;
+    // P from the reference rule (projection.cu:277-318), per logical projection.
+    m->p_q = dl::partials_for(D, QW);
+    m->p_kv = dl::partials_for(D, KW);
+    m->p_o = dl::partials_for(QW, D);
+    m->p_gu = dl::partials_for(D, F);
+    m->p_down = dl::partials_for(F, D);
+    m->p_lm = dl::partials_for(D, V);
+    require(m->p_q == 16 && m->p_kv == 32 && m->p_o == 16 && m->p_gu == 16 && m->p_down == 32 && m->p_lm == 16,
+            "shape selects a partial count the fused kernels do not implement");
+    m->qkv_elems = (QW + 2 * KW) * D;
+    m->o_elems = D * QW;
+    m->gu_elems = 2 * F * D;
+    m->down_elems = D * F;
+    for (uint32_t l = 0; l < c.layers; ++l) {
+      m->qkv.push_back(m->alloc(m->qkv_elems));
+      m->o.push_back(m->alloc(m->o_elems));
+      m->gu.push_back(m->alloc(m->gu_elems));
+      m->down.push_back(m->alloc(m->down_elems));
+      m->input_norm.push_back(m->alloc(D));
+      m->post_norm.push_back(m->alloc(D));
+      m->q_norm.push_back(m->alloc(c.head_dim));
+      m->k_norm.push_back(m->alloc(c.head_dim));
+    }
+    m->final_norm = m->alloc(D);
+    m->lm_head = m->alloc(V * D);
+    if (!c.tied_embeddings) m->embedding = m->alloc(V * D);
+    *out = m.release();
+  });
+}
+
+int dl_qwen3_destroy(dl_qwen3* model) {
+  return guard([&] {
+    if (!model) return;
+    model->device->activate();
+    (void)hipDeviceSynchronize();
+    delete model;
+  });
+}
+
+int dl_qwen3_resident_bytes(dl_qwen3* model, uint64_t* bytes) {
+  return guard([&] {
+    require(model && bytes, "null argument");
+    *bytes = model->resident;
+  });
+}
+
+int dl_qwen3_fill_synthetic(dl_qwen3* model, dl_queue* queue, uint64_t seed, float weight_std) {
+  return guard([&] {
+    require(model != nullptr, "null model");
+    dl::enter(queue);
+    require(weight_std > 0.0f && std::isfinite(weight_std), "weight_std must be positive");
+    const auto& c = model->cfg;
+    hipStream_t s = queue->stream;
+    const int roles[] = {DL_ROLE_Q, DL_ROLE_K, DL_ROLE_V, DL_ROLE_O, DL_ROLE_GATE, DL_ROLE_UP, DL_ROLE_DOWN};
+    for (uint32_t l = 0; l < c.layers; ++l) {
+      for (int role : roles) {
+        uint64_t rows, cols;
+        const dl::PackedView v = model->view(role, l, &rows, &cols);
+        dl::k_fill_view<<<fill_grid(rows * cols), 256, 0, s>>>(v, rows, seed, uint64_t(l) * 16 + role, weight_std);
+      }
+      const int norms[] = {DL_ROLE_INPUT_NORM, DL_ROLE_POST_NORM, DL_ROLE_Q_NORM, DL_ROLE_K_NORM};
+      for (int role : norms) {
+        uint64_t n;
+        uint16_t* p = model->plain(role, l, &n);
+        dl::k_fill_const<<<fill_grid(n), 256, 0, s>>>(p, n, 0x3f80);
+      }
+    }
+    dl::k_fill_const<<<fill_grid(c.hidden), 256, 0, s>>>(model->final_norm, c.hidden, 0x3f80);
+    uint64_t rows, cols;
+    const dl::PackedView lm = model->view(DL_ROLE_LM_HEAD, 0, &rows, &cols);
+    // The tied table is the embedding (stream of role 0); the untied head uses role 1.
+    dl::k_fill_view<<<fill_grid(rows * cols), 256, 0, s>>>(lm, rows, seed,
+                                                            c.tied_embeddings ? DL_ROLE_EMBEDDING : DL_ROLE_LM_HEAD,
+                                                            weight_std);
+    if (!c.tied_embeddings) {
+      const uint64_t n = uint64_t(c.vocab) * c.hidden;
+      dl::k_fill_rowmajor<<<fill_grid(n), 256, 0, s>>>(model->embedding, n, seed, DL_ROLE_EMBEDDING, weight_std);
+    }
+    dl::check_launch(queue, "synthetic fill");
+  });
+}
+
+static int transfer_tensor(dl_qwen3* model, dl_queue* queue, int role, uint32_t layer, uint16_t* host,
+                           uint64_t elements, bool write) {
+  return guard([&] {
+    require(model != nullptr && host != nullptr, "null argument");
+    dl::enter(queue);
+    const auto& c = model->cfg;
+    const bool global = role == DL_ROLE_EMBEDDING || role == DL_ROLE_LM_HEAD || role == DL_ROLE_FINAL_NORM;
+    require(global || layer < c.layers, "layer out of range");
+    if (role == DL_ROLE_EMBEDDING && c.tied_embeddings) role = DL_ROLE_LM_HEAD;
+    uint64_t n = 0;
+    if (uint16_t* p = model->plain(role, layer, &n)) {
+      require(elements == n, "element count does not match the parameter", DL_LENGTH_ERROR);
+      dl::check_hip(hipMemcpyAsync(write ? static_cast<void*>(p) : static_cast<void*>(host),
+                                   write ? static_cast<const void*>(host) : static_cast<const void*>(p), n * 2,
+                                   write ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost, queue->stream),
+                    "tensor transfer");
+      dl::check_hip(hipStreamSynchronize(queue->stream), "tensor transfer wait");
+      return;
+    }
+    uint64_t rows, cols;
+    const dl::PackedView v = model->view(role, layer, &rows, &cols);
+    require(elements == rows * cols, "element count does not match the parameter", DL_LENGTH_ERROR);
+    void* tmp = nullptr;
+    dl::check_hip(hipMalloc(&tmp, elements * 2), "staging allocation");
+    hipError_t e = hipSuccess;
+    if (write) {
+      e = hipMemcpyAsync(tmp, host, elements * 2, hipMemcpyHostToDevice, queue->stream);
+      if (e == hipSuccess)
+        dl::k_pack_view<<<fill_grid(elements), 256, 0, queue->stream>>>(v, rows, static_cast<uint16_t*>(tmp), 0,
+                                                                          nullptr);
+    } else {
+      dl::k_pack_view<<<fill_grid(elements), 256, 0, queue->stream>>>(v, rows, nullptr, 1,
+                                                                        static_cast<uint16_t*>(tmp));
+      e = hipMemcpyAsync(host, tmp, elements * 2, hipMemcpyDeviceToHost, queue->stream);
+    }
+    const hipError_t w = hipStreamSynchronize(queue->stream);
+    (void)hipFree(tmp);
+    dl::check_hip(e, "tensor transfer");
+    dl::check_hip(w, "tensor transfer wait");
+  });
+}
+
+int dl_qwen3_write_tensor(dl_qwen3* model, dl_queue* queue, int role, uint32_t layer, const uint16_t* host,
+                          uint64_t elements) {
+  return transfer_tensor(model, queue, role, layer, const_cast<uint16_t*>(host), elements, true);
+}
+
+int dl_qwen3_read_tensor(dl_qwen3* model, dl_queue* queue, int role, uint32_t layer, uint16_t* host,
+                         uint64_t elements) {
+  return transfer_tensor(model, queue, role, layer, host, elements, false);
+}
+
+}  // extern "C"
+
+// ===================================================================== plan
+struct dl_plan {
+  dl_qwen3* model = nullptr;
+  dl_queue* queue = nullptr;
+  uint32_t batch = 1, capacity = 0, cap = 0;  // cap: padded to 64
+  int head_blocks = 1024;
+  std::vector<void*> allocations;
+  dl::Control* ctl = nullptr;
+  uint16_t *h = nullptr, *q_raw = nullptr, *k_raw = nullptr, *att = nullptr, *act = nullptr, *logits = nullptr;
+  uint16_t *k_cache = nullptr, *v_cache = nullptr, *capture = nullptr, *override_row = nullptr;
+  float *scores = nullptr, *probs = nullptr, *rope = nullptr, *steer = nullptr;
+  uint64_t* partial_keys = nullptr;
+  uint32_t *partial_flags = nullptr, *tokens = nullptr, *selected = nullptr, *out_tokens = nullptr;
+  uint8_t* stop_mask = nullptr;
+  uint32_t* cancel_host = nullptr;
+  uint32_t* cancel_device = nullptr;
+  uint64_t cache_seq_stride = 0, cache_layer_stride = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  // Host mirror of settings.
+  uint64_t position = 0;
+  int32_t capture_layer = -1;
+  int32_t steer_layer = -1;
+  uint32_t steer_mask = 0;
+  bool override_active = false;
+  uint32_t override_mask = 0;
+  uint64_t override_position = 0;
+  uint32_t max_new = 0;
+
+  template <class T>
+  T* alloc(uint64_t count) {
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, count * sizeof(T));
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      dl::fail(DL_LENGTH_ERROR, std::string("plan allocation failed: ") + hipGetErrorString(e));
+    }
+    allocations.push_back(p);
+    return static_cast<T*>(p);
+  }
+
+  ~dl_plan() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    for (void* p : allocations) (void)hipFree(p);
+    if (cancel_host) (void)hipHostFree(cancel_host);
+  }
+
+  void record_step(hipStream_t s);
+  void prepare_kernels();
+  void capture_step();
+};
+
+namespace {
+
+template <class K>
+void allow_lds(K kernel, size_t bytes) {
+  if (bytes > 64 * 1024)
+    dl::check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)),
+                  "hipFuncSetAttribute");
+}
+
+// Dynamic LDS above 64 KiB needs an explicit opt-in per kernel; this runs
+// before stream capture begins.
+template <int B>
+void prepare_kernels_b(dl_plan* p) {
+  using namespace dl;
+  const auto& c = p->model->cfg;
+  const int D = c.hidden, QW = c.q_heads * c.head_dim, F = c.ffn;
+  allow_lds(k_qkv<B>, size_t(B) * (staged_floats(16, D) + staged_floats(32, D)) * sizeof(float));
+  allow_lds(k_residual<16, B>, size_t(B) * staged_floats(16, QW) * sizeof(float));
+  allow_lds(k_gateup<B>, size_t(B) * staged_floats(16, D) * sizeof(float));
+  allow_lds(k_residual<32, B>, size_t(B) * staged_floats(32, F) * sizeof(float));
+  allow_lds(k_lm_head<B>, size_t(B) * staged_floats(16, D) * sizeof(float));
+  allow_lds(k_attn_softmax, size_t(p->cap) * sizeof(float));
+}
+
+template <int B>
+void record_step_b(dl_plan* p, hipStream_t s) {
+  using namespace dl;
+  const dl_qwen3* m = p->model;
+  const auto& c = m->cfg;
+  const int D = c.hidden, QW = c.q_heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
+  const uint32_t V = c.vocab;
+
+  BeginArgs begin{p->ctl, p->tokens, p->selected, p->h, m->lm_head, m->embedding, p->override_row,
+                  p->cancel_device, D, V, c.tied_embeddings ? 1 : 0};
+  k_step_begin<<<B, kBlock, 0, s>>>(begin);
+
+  const size_t qkv_lds = size_t(B) * (staged_floats(16, D) + staged_floats(32, D)) * sizeof(float);
+  const size_t o_lds = size_t(B) * staged_floats(16, QW) * sizeof(float);
+  const size_t gu_lds = size_t(B) * staged_floats(16, D) * sizeof(float);
+  const size_t down_lds = size_t(B) * staged_floats(32, F) * sizeof(float);
+  const size_t soft_lds = size_t(p->cap) * sizeof(float);
+  const unsigned qkv_grid = ceil_div(QW / 4 + KW, kWaves);
+  const unsigned o_grid = ceil_div(D / 4, kWaves);
+  const unsigned gu_grid = ceil_div(F / 2, kWaves);
+  const unsigned down_grid = ceil_div(D / 2, kWaves);
+  const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));
+
+  for (uint32_t l = 0; l < c.layers; ++l) {
+    uint16_t* kc = p->k_cache + uint64_t(l) * p->cache_layer_stride;
+    uint16_t* vc = p->v_cache + uint64_t(l) * p->cache_layer_stride;
+    QkvArgs qa{p->ctl, p->h, m->input_norm[l], reinterpret_cast<const u32x4*>(m->qkv[l]), p->q_raw, p->k_raw,
+               vc, p->cache_seq_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps};
+    k_qkv<B><<<qkv_grid, kBlock, qkv_lds, s>>>(qa);
+
+    AttnArgs aa{p->ctl, p->q_raw, p->k_raw, m->q_norm[l], m->k_norm[l], p->rope, kc, vc, p->cache_seq_stride,
+                p->scores, p->probs, p->att, static_cast<int>(c.q_heads), static_cast<int>(c.kv_heads),
+                static_cast<int>(p->cap), c.rms_eps, scale};
+    k_attn_qk<<<dim3(c.kv_heads, p->cap / 64, B), kBlock, 0, s>>>(aa);
+    k_attn_softmax<<<dim3(c.q_heads, B), kBlock, soft_lds, s>>>(aa);
+    k_attn_pv<<<dim3(c.kv_heads * 16, B), 64, 0, s>>>(aa);
+
+    ResidualArgs oa{p->ctl, p->att, reinterpret_cast<const u32x4*>(m->o[l]), p->h, nullptr, nullptr, QW, D,
+                    static_cast<int>(p->cap), static_cast<int>(l)};
+    k_residual<16, B><<<o_grid, kBlock, o_lds, s>>>(oa);
+
+    GateUpArgs ga{p->ctl, p->h, m->post_norm[l], reinterpret_cast<const u32x4*>(m->gu[l]), p->act, D, F, c.rms_eps};
+    k_gateup<B><<<gu_grid, kBlock, gu_lds, s>>>(ga);
+
+    ResidualArgs da{p->ctl, p->act, reinterpret_cast<const u32x4*>(m->down[l]), p->h, p->capture, p->steer, F, D,
+                    static_cast<int>(p->cap), static_cast<int>(l)};
+    k_residual<32, B><<<down_grid, kBlock, down_lds, s>>>(da);
+  }
+  HeadArgs ha{p->ctl, p->h, m->final_norm, reinterpret_cast<const u32x4*>(m->lm_head), p->logits, p->partial_keys,
+              p->partial_flags, D, V, c.rms_eps};
+  k_lm_head<B><<<p->head_blocks, kBlock, gu_lds, s>>>(ha);
+  EndArgs ea{p->ctl, p->partial_keys, p->partial_flags, p->head_blocks, p->selected, p->out_tokens, p->cap,
+             p->stop_mask, p->cancel_device, B};
+  k_step_end<<<1, kBlock, 0, s>>>(ea);
+}
+
+}  // namespace
+
+void dl_plan::record_step(hipStream_t s) {
+  switch (batch) {
+    case 1: record_step_b<1>(this, s); break;
+    case 2: record_step_b<2>(this, s); break;
+    default: dl::fail(DL_LENGTH_ERROR, "batch sizes above 2 are not supported yet");
+  }
+}
+
+void dl_plan::prepare_kernels() {
+  switch (batch) {
+    case 1: prepare_kernels_b<1>(this); break;
+    case 2: prepare_kernels_b<2>(this); break;
+    default: dl::fail(DL_LENGTH_ERROR, "batch sizes above 2 are not supported yet");
+  }
+}
+
+void dl_plan::capture_step() {
+  hipStream_t s = queue->stream;
+  if (exec) (void)hipGraphExecDestroy(exec);
+  if (graph) (void)hipGraphDestroy(graph);
+  exec = nullptr;
+  graph = nullptr;
+  prepare_kernels();
+  dl::check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture");
+  try {
+    record_step(s);
+  } catch (...) {
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(s, &g);
+    if (g) (void)hipGraphDestroy(g);
+    throw;
+  }
+  dl::check_hip(hipStreamEndCapture(s, &graph), "end capture");
+  dl::check_hip(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "graph instantiate");
+}
+
+namespace {
+void launch_steps(dl_plan* p, uint32_t steps) {
+  for (uint32_t i = 0; i < steps; ++i) dl::check_hip(hipGraphLaunch(p->exec, p->queue->stream), "hipGraphLaunch");
+}
+
+void init_control(dl_plan* p, uint64_t position, uint32_t prompt_length, uint32_t max_new, uint32_t mode) {
+  dl::InitArgs a{p->ctl, position, prompt_length, max_new, p->batch, mode, p->capture_layer, p->steer_layer,
+                 p->steer_mask, p->override_active ? 1u : 0u, p->override_mask, p->override_position};
+  dl::k_init_control<<<1, 1, 0, p->queue->stream>>>(a);
+  dl::check_launch(p->queue, "init control");
+}
+}  // namespace
+
+extern "C" {
+
+int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t capacity, dl_plan** out) {
+  return guard([&] {
+    require(model && out, "null argument");
+    dl::enter(queue);
+    require(batch >= 1 && batch <= 2, "batch must be 1 or 2", DL_LENGTH_ERROR);
+    require(capacity >= 1 && capacity <= 32768, "capacity must be in [1, 32768]", DL_LENGTH_ERROR);
+    auto p = std::make_unique<dl_plan>();
+    p->model = model;
+    p->queue = queue;
+    p->batch = batch;
+    p->capacity = capacity;
+    p->cap = static_cast<uint32_t>(dl::ceil_div(capacity, 64) * 64);
+    const auto& c = model->cfg;
+    const uint64_t B = batch, D = c.hidden, QW = uint64_t(c.q_heads) * c.head_dim,
+                   KW = uint64_t(c.kv_heads) * c.head_dim, F = c.ffn, V = c.vocab, L = c.layers, cap = p->cap;
+    p->ctl = p->alloc<dl::Control>(1);
+    p->h = p->alloc<uint16_t>(B * D);
+    p->q_raw = p->alloc<uint16_t>(B * QW);
+    p->k_raw = p->alloc<uint16_t>(B * KW);
+    p->att = p->alloc<uint16_t>(B * QW);
+    p->act = p->alloc<uint16_t>(B * F);
+    p->logits = p->alloc<uint16_t>(B * V);
+    p->cache_layer_stride = KW * cap;
+    p->cache_seq_stride = L * p->cache_layer_stride;
+    p->k_cache = p->alloc<uint16_t>(B * p->cache_seq_stride);
+    p->v_cache = p->alloc<uint16_t>(B * p->cache_seq_stride);
+    dl::check_hip(hipMemsetAsync(p->v_cache, 0, B * p->cache_seq_stride * 2, queue->stream), "cache clear");
+    dl::check_hip(hipMemsetAsync(p->k_cache, 0, B * p->cache_seq_stride * 2, queue->stream), "cache clear");
+    p->scores = p->alloc<float>(B * c.q_heads * cap);
+    p->probs = p->alloc<float>(B * c.q_heads * cap);
+    dl::check_hip(hipMemsetAsync(p->probs, 0, B * c.q_heads * cap * 4, queue->stream), "probs clear");
+    p->rope = p->alloc<float>(cap * c.head_dim);
+    p->partial_keys = p->alloc<uint64_t>(B * p->head_blocks);
+    p->partial_flags = p->alloc<uint32_t>(B * p->head_blocks);
+    p->tokens = p->alloc<uint32_t>(cap);
+    p->selected = p->alloc<uint32_t>(B);
+    p->out_tokens = p->alloc<uint32_t>(B * cap);
+    p->stop_mask = p->alloc<uint8_t>(V);
+    p->override_row = p->alloc<uint16_t>(D);
+    p->steer = p->alloc<float>(B * D);
+    dl::check_hip(hipMemsetAsync(p->stop_mask, 0, V, queue->stream), "stop mask clear");
+    dl::check_hip(hipMemsetAsync(p->selected, 0, B * 4, queue->stream), "selection clear");
+    dl::check_hip(hipMemsetAsync(p->tokens, 0, cap * 4, queue->stream), "token clear");
+    dl::check_hip(hipHostMalloc(reinterpret_cast<void**>(&p->cancel_host), 64, hipHostMallocMapped), "cancel word");
+    *p->cancel_host = 0;
+    dl::check_hip(hipHostGetDevicePointer(reinterpret_cast<void**>(&p->cancel_device), p->cancel_host, 0),
+                  "cancel word mapping");
+    dl::k_rope_table<<<fill_grid(cap * c.head_dim / 2), 256, 0, queue->stream>>>(p->rope, cap, c.head_dim,
+                                                                                  c.rope_theta);
+    dl::check_launch(queue, "rope table");
+    // Inactive control until a forward or generation starts.
+    dl::check_hip(hipMemsetAsync(p->ctl, 0, sizeof(dl::Control), queue->stream), "control clear");
+    dl::check_hip(hipStreamSynchronize(queue->stream), "plan setup");
+    // Capture one step into a graph.
+    p->capture_step();
+    *out = p.release();
+  });
+}
+
+int dl_plan_destroy(dl_plan* plan) {
+  return guard([&] {
+    if (!plan) return;
+    plan->queue->device->activate();
+    (void)hipStreamSynchronize(plan->queue->stream);
+    delete plan;
+  });
+}
+
+int dl_plan_reset(dl_plan* plan) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    dl::enter(plan->queue);
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "reset wait");
+    dl::check_hip(hipMemsetAsync(plan->ctl, 0, sizeof(dl::Control), plan->queue->stream), "control clear");
+    *plan->cancel_host = 0;
+    plan->position = 0;
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "reset");
+  });
+}
+
+int dl_plan_position(dl_plan* plan, uint64_t* position) {
+  return guard([&] {
+    require(plan && position, "null argument");
+    dl::enter(plan->queue);
+    dl::Control c;
+    dl::check_hip(hipMemcpyAsync(&c, plan->ctl, sizeof c, hipMemcpyDeviceToHost, plan->queue->stream), "read control");
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "read control wait");
+    *position = c.position;
+  });
+}
+
+int dl_plan_forward(dl_plan* plan, const uint32_t* tokens, uint32_t rows) {
+  return guard([&] {
+    require(plan && tokens, "null argument");
+    dl::enter(plan->queue);
+    require(rows > 0, "empty forward");
+    dl::Control c;
+    hipStream_t s = plan->queue->stream;
+    dl::check_hip(hipMemcpyAsync(&c, plan->ctl, sizeof c, hipMemcpyDeviceToHost, s), "read control");
+    dl::check_hip(hipStreamSynchronize(s), "read control wait");
+    const uint64_t pos = c.position;
+    require(pos + rows <= plan->capacity, "forward exceeds the cache capacity", DL_LENGTH_ERROR);
+    // All sequences consume the same rows in this diagnostic path.
+    dl::check_hip(hipMemcpyAsync(plan->tokens + pos, tokens, rows * 4, hipMemcpyHostToDevice, s), "token upload");
+    plan->max_new = 1;
+    init_control(plan, pos, static_cast<uint32_t>(pos + rows), 1, 0);
+    launch_steps(plan, rows);
+    dl::check_hip(hipStreamSynchronize(s), "forward");
+  });
+}
+
+int dl_plan_read_logits(dl_plan* plan, uint32_t seq, uint16_t* host) {
+  return guard([&] {
+    require(plan && host, "null argument");
+    require(seq < plan->batch, "sequence out of range");
+    dl::enter(plan->queue);
+    const uint64_t V = plan->model->cfg.vocab;
+    dl::check_hip(hipMemcpyAsync(host, plan->logits + uint64_t(seq) * V, V * 2, hipMemcpyDeviceToHost,
+                                 plan->queue->stream),
+                  "read logits");
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "read logits wait");
+  });
+}
+
+int dl_plan_logits_address(dl_plan* plan, uint32_t seq, void** out) {
+  return guard([&] {
+    require(plan && out, "null argument");
+    require(seq < plan->batch, "sequence out of range");
+    *out = plan->logits + uint64_t(seq) * plan->model->cfg.vocab;
+  });
+}
+
+int dl_plan_set_capture(dl_plan* plan, int32_t layer) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    dl::enter(plan->queue);
+    require(layer < static_cast<int32_t>(plan->model->cfg.layers), "capture layer out of range");
+    if (layer >= 0 && !plan->capture) {
+      plan->capture = plan->alloc<uint16_t>(uint64_t(plan->batch) * plan->cap * plan->model->cfg.hidden);
+      // The recorded graph holds the capture pointer: record it again.
+      dl::check_hip(hipStreamSynchronize(plan->queue->stream), "capture setup");
+      plan->capture_step();
+    }
+    plan->capture_layer = layer;
+  });
+}
+
+int dl_plan_read_capture(dl_plan* plan, uint32_t seq, uint64_t first_position, uint64_t count, uint16_t* host) {
+  return guard([&] {
+    require(plan && host, "null argument");
+    require(plan->capture != nullptr, "capture is not enabled");
+    require(seq < plan->batch, "sequence out of range");
+    require(first_position + count <= plan->cap, "capture range outside the cache", DL_LENGTH_ERROR);
+    dl::enter(plan->queue);
+    const uint64_t D = plan->model->cfg.hidden;
+    dl::check_hip(hipMemcpyAsync(host, plan->capture + (uint64_t(seq) * plan->cap + first_position) * D,
+                                 count * D * 2, hipMemcpyDeviceToHost, plan->queue->stream),
+                  "read capture");
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "read capture wait");
+  });
+}
+
+int dl_plan_set_steering(dl_plan* plan, uint32_t seq, int32_t layer, const float* vector) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    require(seq < plan->batch, "sequence out of range");
+    dl::enter(plan->queue);
+    const auto& c = plan->model->cfg;
+    if (!vector) {
+      plan->steer_mask &= ~(1u << seq);
+      return;
+    }
+    require(layer >= 0 && layer < static_cast<int32_t>(c.layers), "steering layer out of range");
+    require(plan->steer_layer < 0 || plan->steer_layer == layer || plan->steer_mask == 0,
+            "all steered sequences must use one layer");
+    for (uint32_t i = 0; i < c.hidden; ++i) require(std::isfinite(vector[i]), "steering vector must be finite");
+    dl::check_hip(hipMemcpyAsync(plan->steer + uint64_t(seq) * c.hidden, vector, c.hidden * 4, hipMemcpyHostToDevice,
+                                 plan->queue->stream),
+                  "steering upload");
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "steering upload wait");
+    plan->steer_layer = layer;
+    plan->steer_mask |= 1u << seq;
+  });
+}
+
+int dl_plan_set_embedding_override(dl_plan* plan, uint64_t position, const uint16_t* row, uint32_t seq_mask) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    dl::enter(plan->queue);
+    if (!row || seq_mask == 0) {
+      plan->override_active = false;
+      return;
+    }
+    require(position < plan->capacity, "override position outside the cache", DL_LENGTH_ERROR);
+    dl::check_hip(hipMemcpyAsync(plan->override_row, row, plan->model->cfg.hidden * 2, hipMemcpyHostToDevice,
+                                 plan->queue->stream),
+                  "override upload");
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "override upload wait");
+    plan->override_active = true;
+    plan->override_position = position;
+    plan->override_mask = seq_mask;
+  });
+}
+
+static int cache_transfer(dl_plan* plan, uint32_t seq, uint32_t layer, uint64_t first, uint64_t count,
+                          uint16_t* keys, uint16_t* values, bool read) {
+  return guard([&] {
+    require(plan && keys && values, "null argument");
+    dl::enter(plan->queue);
+    const auto& c = plan->model->cfg;
+    require(seq < plan->batch && layer < c.layers, "sequence or layer out of range");
+    require(count > 0 && first + count <= plan->capacity, "cache rows outside the capacity", DL_LENGTH_ERROR);
+    const uint64_t elements = count * c.kv_heads * c.head_dim;
+    void* tk = nullptr;
+    void* tv = nullptr;
+    dl::check_hip(hipMalloc(&tk, elements * 2), "cache staging");
+    if (hipMalloc(&tv, elements * 2) != hipSuccess) {
+      (void)hipFree(tk);
+      dl::fail(DL_LENGTH_ERROR, "cache staging allocation failed");
+    }
+    hipStream_t s = plan->queue->stream;
+    const uint64_t base = seq * plan->cache_seq_stride + uint64_t(layer) * plan->cache_layer_stride;
+    hipError_t e = hipSuccess;
+    if (!read) {
+      e = hipMemcpyAsync(tk, keys, elements * 2, hipMemcpyHostToDevice, s);
+      if (e == hipSuccess) e = hipMemcpyAsync(tv, values, elements * 2, hipMemcpyHostToDevice, s);
+    }
+    if (e == hipSuccess)
+      dl::k_cache_rows<<<fill_grid(elements), 256, 0, s>>>(plan->k_cache + base, plan->v_cache + base,
+                                                           static_cast<int>(plan->cap), c.kv_heads, first, count,
+                                                           static_cast<uint16_t*>(tk), static_cast<uint16_t*>(tv),
+                                                           read ? 1 : 0);
+    if (e == hipSuccess && read) {
+      e = hipMemcpyAsync(keys, tk, elements * 2, hipMemcpyDeviceToHost, s);
+      if (e == hipSuccess) e = hipMemcpyAsync(values, tv, elements * 2, hipMemcpyDeviceToHost, s);
+    }
+    const hipError_t w = hipStreamSynchronize(s);
+    (void)hipFree(tk);
+    (void)hipFree(tv);
+    dl::check_hip(e, "cache transfer");
+    dl::check_hip(w, "cache transfer wait");
+  });
+}
+
+int dl_plan_write_cache(dl_plan* plan, uint32_t seq, uint32_t layer, uint64_t first_position, uint64_t count,
+                        const uint16_t* keys, const uint16_t* values) {
+  return cache_transfer(plan, seq, layer, first_position, count, const_cast<uint16_t*>(keys),
+                        const_cast<uint16_t*>(values), false);
+}
+
+int dl_plan_read_cache(dl_plan* plan, uint32_t seq, uint32_t layer, uint64_t first_position, uint64_t count,
+                       uint16_t* keys, uint16_t* values) {
+  return cache_transfer(plan, seq, layer, first_position, count, keys, values, true);
+}
+
+int dl_plan_seek(dl_plan* plan, uint64_t position) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    dl::enter(plan->queue);
+    require(position < plan->capacity, "position outside the capacity", DL_LENGTH_ERROR);
+    dl::k_seek<<<1, 1, 0, plan->queue->stream>>>(plan->ctl, position);
+    dl::check_launch(plan->queue, "seek");
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "seek wait");
+  });
+}
+
+int dl_plan_read_hidden(dl_plan* plan, uint32_t seq, uint16_t* host) {
+  return guard([&] {
+    require(plan && host, "null argument");
+    require(seq < plan->batch, "sequence out of range");
+    dl::enter(plan->queue);
+    const uint64_t D = plan->model->cfg.hidden;
+    dl::check_hip(hipMemcpyAsync(host, plan->h + uint64_t(seq) * D, D * 2, hipMemcpyDeviceToHost, plan->queue->stream),
+                  "read hidden");
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "read hidden wait");
+  });
+}
+
+int dl_plan_generate(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length, uint32_t max_new,
+                     const dl_sampling* sampling, const uint64_t* seeds, const uint32_t* stop_ids,
+                     uint32_t stop_count) {
+  const int status =
+      dl_plan_prepare_generation(plan, prompt, prompt_length, max_new, sampling, seeds, stop_ids, stop_count);
+  if (status != DL_OK) return status;
+  return dl_plan_decode_steps(plan, prompt_length + max_new);
+}
+
+int dl_plan_prepare_generation(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length, uint32_t max_new,
+                               const dl_sampling* sampling, const uint64_t* seeds, const uint32_t* stop_ids,
+                               uint32_t stop_count) {
+  return guard([&] {
+    require(plan && prompt, "null argument");
+    dl::enter(plan->queue);
+    require(prompt_length > 0, "empty prompt");
+    require(uint64_t(prompt_length) + max_new <= plan->capacity, "generation exceeds the cache capacity",
+            DL_LENGTH_ERROR);
+    (void)seeds;
+    uint32_t mode = 0;
+    if (sampling) {
+      require(sampling->mode == 0 || sampling->mode == 1, "invalid sampling mode");
+      require(std::isfinite(sampling->temperature) && sampling->temperature > 0, "invalid temperature");
+      require(std::isfinite(sampling->top_p) && sampling->top_p > 0 && sampling->top_p <= 1, "invalid top_p");
+      if (sampling->mode == 0)
+        require(sampling->temperature == 1 && sampling->top_k == 0 && sampling->top_p == 1,
+                "greedy selection takes temperature 1, top_k 0, top_p 1");
+      mode = sampling->mode;
+    }
+    require(mode == 0, "categorical sampling inside the device loop is not available yet");
+    const uint32_t V = plan->model->cfg.vocab;
+    for (uint32_t i = 0; i < prompt_length; ++i) require(prompt[i] < V, "prompt id outside the vocabulary");
+    for (uint32_t i = 0; i < stop_count; ++i) require(stop_ids && stop_ids[i] < V, "stop id outside the vocabulary");
+    hipStream_t s = plan->queue->stream;
+    dl::check_hip(hipStreamSynchronize(s), "generate wait");
+    *plan->cancel_host = 0;
+    dl::check_hip(hipMemcpyAsync(plan->tokens, prompt, prompt_length * 4ull, hipMemcpyHostToDevice, s), "prompt");
+    dl::check_hip(hipMemsetAsync(plan->stop_mask, 0, V, s), "stop mask");
+    if (stop_count) {
+      std::vector<uint8_t> mask(V, 0);
+      for (uint32_t i = 0; i < stop_count; ++i) mask[stop_ids[i]] = 1;
+      dl::check_hip(hipMemcpyAsync(plan->stop_mask, mask.data(), V, hipMemcpyHostToDevice, s), "stop mask");
+      dl::check_hip(hipStreamSynchronize(s), "stop mask wait");
+    }
+    plan->max_new = max_new;
+    init_control(plan, 0, prompt_length, max_new, mode);
+  });
+}
+
+int dl_plan_decode_steps(dl_plan* plan, uint32_t steps) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    dl::enter(plan->queue);
+    launch_steps(plan, steps);
+  });
+}
+
+int dl_plan_collect(dl_plan* plan, uint32_t* tokens, uint32_t max_new, dl_generation_result* results) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    dl::enter(plan->queue);
+    hipStream_t s = plan->queue->stream;
+    const hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+      plan->queue->device->poisoned = true;
+      dl::check_hip(e, "generation");
+    }
+    dl::Control c;
+    dl::check_hip(hipMemcpy(&c, plan->ctl, sizeof c, hipMemcpyDeviceToHost), "read control");
+    const uint32_t n = std::min(c.generated, max_new);
+    for (uint32_t b = 0; b < plan->batch; ++b) {
+      if (tokens && n)
+        dl::check_hip(hipMemcpy(tokens + uint64_t(b) * max_new, plan->out_tokens + uint64_t(b) * plan->cap, n * 4ull,
+                                hipMemcpyDeviceToHost),
+                      "read tokens");
+      if (results) {
+        results[b].generated = c.generated;
+        results[b].reason = c.active ? 0u : c.reason;
+        if (!c.active && c.reason == 0 && ((c.finished_mask >> b) & 1u)) results[b].reason = 1;
+        results[b].status = c.status;
+        results[b].reserved = c.active;
+        results[b].position = c.position;
+      }
+    }
+  });
+}
+
+int dl_plan_request_stop(dl_plan* plan) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    __atomic_store_n(plan->cancel_host, 1u, __ATOMIC_RELEASE);
+  });
+}
+
+}  // extern "C"

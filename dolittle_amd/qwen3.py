@@ -1,0 +1,226 @@
+"""Qwen3 resident model and cached forward plan over libdlhip.so.
+
+Mirrors the reference's load_resident_model / prepare_cached_forward /
+generate flow (src/inference/executor.h:242-342,
+src/inference/generation.h:129-138) for the Qwen3-8B recipe
+(src/models/qwen3/model.cpp:343-409).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _lib
+from .runtime import Device, Queue
+
+ROLE = {
+    "embedding": 0, "lm_head": 1, "final_norm": 2, "input_norm": 3, "q": 4, "k": 5, "v": 6,
+    "q_norm": 7, "k_norm": 8, "o": 9, "post_norm": 10, "gate": 11, "up": 12, "down": 13,
+}
+REASON = {0: "limit", 1: "eos", 2: "cancelled", 3: "failure"}
+
+
+@dataclass
+class Qwen3Config:
+    """src/models/qwen3/model.h:125-137; defaults are Qwen3-8B."""
+    layers: int = 36
+    hidden: int = 4096
+    q_heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    ffn: int = 12288
+    vocab: int = 151936
+    tied_embeddings: bool = True
+    rms_eps: float = 1e-6
+    rope_theta: float = 1e6
+
+    def ctype(self) -> _lib.Qwen3Config:
+        return _lib.Qwen3Config(self.layers, self.hidden, self.q_heads, self.kv_heads, self.head_dim, self.ffn,
+                                self.vocab, 1 if self.tied_embeddings else 0, self.rms_eps, 0, self.rope_theta)
+
+    def shape(self, role: str) -> tuple:
+        D, QW, KW = self.hidden, self.q_heads * self.head_dim, self.kv_heads * self.head_dim
+        return {
+            "embedding": (self.vocab, D), "lm_head": (self.vocab, D), "final_norm": (D,),
+            "input_norm": (D,), "post_norm": (D,), "q_norm": (self.head_dim,), "k_norm": (self.head_dim,),
+            "q": (QW, D), "k": (KW, D), "v": (KW, D), "o": (D, QW), "gate": (self.ffn, D),
+            "up": (self.ffn, D), "down": (D, self.ffn),
+        }[role]
+
+    def projection_bytes_per_token(self) -> int:
+        """BF16 projection weight bytes read per decoded token (incl. LM head)."""
+        D, QW, KW, F = self.hidden, self.q_heads * self.head_dim, self.kv_heads * self.head_dim, self.ffn
+        per_block = (QW * D + 2 * KW * D + D * QW + 2 * F * D + D * F) * 2
+        return self.layers * per_block + self.vocab * D * 2
+
+
+@dataclass
+class SamplingSettings:
+    """src/inference/sampling/sampler.h:45-55."""
+    mode: str = "greedy"
+    temperature: float = 1.0
+    top_k: int = 0
+    top_p: float = 1.0
+
+    def ctype(self) -> _lib.Sampling:
+        return _lib.Sampling(0 if self.mode == "greedy" else 1, self.top_k, self.temperature, self.top_p)
+
+
+class Qwen3Model:
+    """Resident parameters in the backend's packed layout."""
+
+    def __init__(self, device: Device, queue: Queue, config: Qwen3Config):
+        self.device, self.queue, self.config = device, queue, config
+        cfg = config.ctype()
+        handle = C.c_void_p()
+        _lib.call("dl_qwen3_create", device.handle, queue.handle, C.byref(cfg), C.byref(handle))
+        self.handle = handle
+
+    def fill_synthetic(self, seed: int, weight_std: float = 0.02) -> None:
+        _lib.call("dl_qwen3_fill_synthetic", self.handle, self.queue.handle, seed, C.c_float(weight_std))
+
+    def write(self, role: str, layer: int, array: np.ndarray) -> None:
+        a = np.ascontiguousarray(array, dtype=np.uint16).reshape(-1)
+        _lib.call("dl_qwen3_write_tensor", self.handle, self.queue.handle, ROLE[role], layer,
+                  a.ctypes.data_as(_lib.u16p), a.size)
+
+    def read(self, role: str, layer: int = 0) -> np.ndarray:
+        shape = self.config.shape(role)
+        out = np.empty(int(np.prod(shape)), dtype=np.uint16)
+        _lib.call("dl_qwen3_read_tensor", self.handle, self.queue.handle, ROLE[role], layer,
+                  out.ctypes.data_as(_lib.u16p), out.size)
+        return out.reshape(shape)
+
+    def resident_bytes(self) -> int:
+        n = C.c_uint64()
+        _lib.call("dl_qwen3_resident_bytes", self.handle, C.byref(n))
+        return n.value
+
+    def __del__(self):
+        try:
+            _lib.call("dl_qwen3_destroy", self.handle)
+        except Exception:
+            pass
+
+
+class Plan:
+    """Cached forward plan for `batch` sequences with `capacity` positions."""
+
+    def __init__(self, model: Qwen3Model, batch: int = 1, capacity: int = 8192):
+        self.model, self.batch, self.capacity = model, batch, capacity
+        handle = C.c_void_p()
+        _lib.call("dl_plan_create", model.handle, model.queue.handle, batch, capacity, C.byref(handle))
+        self.handle = handle
+        self.max_new = 0
+
+    # -- diagnostic chunk path
+    def forward(self, tokens: Sequence[int]) -> None:
+        a = np.ascontiguousarray(tokens, dtype=np.uint32)
+        _lib.call("dl_plan_forward", self.handle, a.ctypes.data_as(_lib.u32p), a.size)
+
+    def seek(self, position: int) -> None:
+        _lib.call("dl_plan_seek", self.handle, position)
+
+    def position(self) -> int:
+        p = C.c_uint64()
+        _lib.call("dl_plan_position", self.handle, C.byref(p))
+        return p.value
+
+    def reset(self) -> None:
+        _lib.call("dl_plan_reset", self.handle)
+
+    def logits(self, seq: int = 0) -> np.ndarray:
+        out = np.empty(self.model.config.vocab, dtype=np.uint16)
+        _lib.call("dl_plan_read_logits", self.handle, seq, out.ctypes.data_as(_lib.u16p))
+        return out
+
+    def hidden(self, seq: int = 0) -> np.ndarray:
+        out = np.empty(self.model.config.hidden, dtype=np.uint16)
+        _lib.call("dl_plan_read_hidden", self.handle, seq, out.ctypes.data_as(_lib.u16p))
+        return out
+
+    def write_cache(self, layer: int, first: int, keys: np.ndarray, values: np.ndarray, seq: int = 0) -> None:
+        k = np.ascontiguousarray(keys, dtype=np.uint16).reshape(-1)
+        v = np.ascontiguousarray(values, dtype=np.uint16).reshape(-1)
+        per_row = self.model.config.kv_heads * self.model.config.head_dim
+        _lib.call("dl_plan_write_cache", self.handle, seq, layer, first, k.size // per_row,
+                  k.ctypes.data_as(_lib.u16p), v.ctypes.data_as(_lib.u16p))
+
+    def read_cache(self, layer: int, first: int, count: int, seq: int = 0) -> tuple[np.ndarray, np.ndarray]:
+        per_row = self.model.config.kv_heads * self.model.config.head_dim
+        k = np.empty(count * per_row, dtype=np.uint16)
+        v = np.empty(count * per_row, dtype=np.uint16)
+        _lib.call("dl_plan_read_cache", self.handle, seq, layer, first, count, k.ctypes.data_as(_lib.u16p),
+                  v.ctypes.data_as(_lib.u16p))
+        return k, v
+
+    # -- hooks
+    def set_capture(self, layer: int) -> None:
+        _lib.call("dl_plan_set_capture", self.handle, layer)
+
+    def read_capture(self, seq: int, first: int, count: int) -> np.ndarray:
+        out = np.empty(count * self.model.config.hidden, dtype=np.uint16)
+        _lib.call("dl_plan_read_capture", self.handle, seq, first, count, out.ctypes.data_as(_lib.u16p))
+        return out.reshape(count, self.model.config.hidden)
+
+    def set_steering(self, seq: int, layer: int, vector: Optional[np.ndarray]) -> None:
+        if vector is None:
+            _lib.call("dl_plan_set_steering", self.handle, seq, layer, None)
+            return
+        v = np.ascontiguousarray(vector, dtype=np.float32)
+        _lib.call("dl_plan_set_steering", self.handle, seq, layer, v.ctypes.data_as(C.POINTER(C.c_float)))
+
+    def set_embedding_override(self, position: int, row: Optional[np.ndarray], seq_mask: int) -> None:
+        if row is None:
+            _lib.call("dl_plan_set_embedding_override", self.handle, 0, None, 0)
+            return
+        r = np.ascontiguousarray(row, dtype=np.uint16)
+        _lib.call("dl_plan_set_embedding_override", self.handle, position, r.ctypes.data_as(_lib.u16p), seq_mask)
+
+    # -- device-owned loop
+    def _args(self, prompt, sampling, seeds, stop_ids):
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        s = (sampling or SamplingSettings()).ctype()
+        seeds_a = np.ascontiguousarray(seeds if seeds is not None else [0] * self.batch, dtype=np.uint64)
+        stops = np.ascontiguousarray(stop_ids if stop_ids else [0], dtype=np.uint32)
+        return p, s, seeds_a, stops, (len(stop_ids) if stop_ids else 0)
+
+    def generate(self, prompt, max_new: int, sampling: Optional[SamplingSettings] = None, seeds=None,
+                 stop_ids: Optional[Sequence[int]] = None) -> None:
+        p, s, seeds_a, stops, n = self._args(prompt, sampling, seeds, stop_ids)
+        _lib.call("dl_plan_generate", self.handle, p.ctypes.data_as(_lib.u32p), p.size, max_new, C.byref(s),
+                  seeds_a.ctypes.data_as(_lib.u64p), stops.ctypes.data_as(_lib.u32p), n)
+        self.max_new = max_new
+
+    def prepare_generation(self, prompt, max_new: int, sampling: Optional[SamplingSettings] = None, seeds=None,
+                           stop_ids: Optional[Sequence[int]] = None) -> None:
+        p, s, seeds_a, stops, n = self._args(prompt, sampling, seeds, stop_ids)
+        _lib.call("dl_plan_prepare_generation", self.handle, p.ctypes.data_as(_lib.u32p), p.size, max_new,
+                  C.byref(s), seeds_a.ctypes.data_as(_lib.u64p), stops.ctypes.data_as(_lib.u32p), n)
+        self.max_new = max_new
+
+    def decode_steps(self, steps: int) -> None:
+        _lib.call("dl_plan_decode_steps", self.handle, steps)
+
+    def collect(self) -> tuple[np.ndarray, list[dict]]:
+        n = max(self.max_new, 1)
+        tokens = np.zeros(self.batch * n, dtype=np.uint32)
+        results = (_lib.GenerationResult * self.batch)()
+        _lib.call("dl_plan_collect", self.handle, tokens.ctypes.data_as(_lib.u32p), n, results)
+        out = []
+        for r in results:
+            out.append({"generated": r.generated, "reason": REASON.get(r.reason, r.reason), "status": r.status,
+                        "active": bool(r.reserved), "position": r.position})
+        return tokens.reshape(self.batch, n), out
+
+    def request_stop(self) -> None:
+        _lib.call("dl_plan_request_stop", self.handle)
+
+    def __del__(self):
+        try:
+            _lib.call("dl_plan_destroy", self.handle)
+        except Exception:
+            pass

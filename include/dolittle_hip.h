@@ -1,0 +1,342 @@
+/*
+ * dolittle_hip.h -- C ABI of libdlhip.so, the MI355X (gfx950) backend for
+ * Dolittle's Qwen3-8B token loop.
+ *
+ * This is the seam a Dolittle host binds in place of its CUDA backend.  Every
+ * entry point is extern "C", takes plain pointers and sizes, and returns an
+ * int status (DL_OK or one of the dl_status codes); the message of the last
+ * failure on the calling thread is available from dl_last_error().  No HIP,
+ * torch or C++ types cross the boundary.
+ *
+ * Reference interfaces replaced (paths relative to the Dolittle tree):
+ *   runtime     gpu::Device / gpu::Queue / buffers      src/gpu/device.h:73-184,
+ *               gpu::query_memory                       src/gpu/memory.h:49-56,
+ *               gpu::cuda::open_device                  src/gpu/cuda/device.h:29
+ *   operations  kernels::cuda::launch_*                 src/kernels/cuda/launch.h:79-109
+ *               (the eight-operation catalog of src/kernels/operations.h:169-271)
+ *   plan/loop   CachedForwardPlan + DeviceSequence       src/inference/executor.h:242-342,
+ *                                                       src/inference/decoding/device.h:84-137
+ *   sampling    DeviceCategorical                       src/inference/sampling/device.h:58-85
+ *   steering    DeviceIntervention (all-position form)  src/inference/steering/device.h:30-68
+ *   capture     DeviceSequence::capture                 src/inference/decoding/device.h:112
+ *   injection   EmbeddingOverride                       src/inference/executor.h:129-135
+ *
+ * Conventions kept from the reference (src/gpu/device.h:18-25,
+ * src/kernels/cuda/launch.h:10-14): launches only enqueue work; they allocate
+ * nothing and never wait on the host.  Buffers are borrowed until the queue
+ * reaches a later completion point.  Asynchronous device errors surface at
+ * the next wait.  Host calls on one device are serialised by the caller.
+ */
+#ifndef DOLITTLE_HIP_H
+#define DOLITTLE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ status */
+/* Mirrors the reference's exception classes (src/gpu/device.h:23-25,
+ * src/kernels/operations.h:5-10): invalid_argument, length_error,
+ * runtime_error, and a poisoned device after an unrecoverable failure. */
+typedef enum dl_status {
+  DL_OK = 0,
+  DL_INVALID_ARGUMENT = 1,
+  DL_LENGTH_ERROR = 2,
+  DL_RUNTIME_ERROR = 3,
+  DL_POISONED = 4
+} dl_status;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* dl_last_error(void);
+
+/* Storage element types (src/tensors/representations/representation.h). */
+typedef enum dl_dtype { DL_BF16 = 1, DL_F32 = 2 } dl_dtype;
+
+/* ----------------------------------------------------------------- runtime */
+typedef struct dl_device dl_device;
+typedef struct dl_queue dl_queue;
+typedef struct dl_buffer dl_buffer;
+typedef struct dl_event dl_event;
+
+typedef struct dl_device_info {
+  char name[64];
+  char arch[64];
+  uint32_t compute_units;
+  uint32_t reserved;
+  uint64_t total_bytes;
+} dl_device_info;
+
+/* gpu::cuda::open_device (src/gpu/cuda/device.h:29). */
+int dl_device_open(int ordinal, dl_device** out);
+int dl_device_close(dl_device* device);
+/* gpu::Device::info (src/gpu/device.h:138-150). */
+int dl_device_info_get(dl_device* device, dl_device_info* out);
+/* gpu::query_memory (src/gpu/memory.h:49-56). */
+int dl_memory_snapshot(dl_device* device, uint64_t* free_bytes, uint64_t* total_bytes);
+
+/* gpu::Device::allocate (device memory) and allocate_staging (pinned,
+ * host-mapped memory) (src/gpu/device.h:150-160). */
+int dl_buffer_alloc(dl_device* device, uint64_t bytes, uint64_t alignment, dl_buffer** out);
+int dl_staging_alloc(dl_device* device, uint64_t bytes, dl_buffer** out);
+int dl_buffer_free(dl_buffer* buffer);
+/* Address of the buffer: a device address for device buffers (valid as an
+ * operand of the dl_* operations), a host address for staging buffers. */
+int dl_buffer_address(dl_buffer* buffer, void** out);
+int dl_buffer_size(dl_buffer* buffer, uint64_t* out);
+
+/* gpu::Device::create_queue and gpu::Queue (src/gpu/device.h:160-184). */
+int dl_queue_create(dl_device* device, dl_queue** out);
+int dl_queue_destroy(dl_queue* queue);
+int dl_queue_upload(dl_queue* queue, dl_buffer* dst, uint64_t dst_offset, dl_buffer* src_staging,
+                    uint64_t src_offset, uint64_t bytes);
+int dl_queue_download(dl_queue* queue, dl_buffer* dst_staging, uint64_t dst_offset, dl_buffer* src,
+                      uint64_t src_offset, uint64_t bytes);
+int dl_queue_copy(dl_queue* queue, dl_buffer* dst, uint64_t dst_offset, dl_buffer* src,
+                  uint64_t src_offset, uint64_t bytes);
+/* Convenience transfers from/to pageable host memory; both complete before
+ * returning (they wait on the queue). */
+int dl_queue_write(dl_queue* queue, dl_buffer* dst, uint64_t dst_offset, const void* host,
+                   uint64_t bytes);
+int dl_queue_read(dl_queue* queue, void* host, dl_buffer* src, uint64_t src_offset, uint64_t bytes);
+/* Completion points: mark returns a monotonically increasing point; wait
+ * blocks until the queue reaches it and reports asynchronous failures. */
+int dl_queue_mark(dl_queue* queue, uint64_t* point);
+int dl_queue_wait(dl_queue* queue, uint64_t point);
+int dl_queue_drain(dl_queue* queue);
+
+/* Timing events recorded on a queue (for measurement only). */
+int dl_event_create(dl_device* device, dl_event** out);
+int dl_event_destroy(dl_event* event);
+int dl_event_record(dl_event* event, dl_queue* queue);
+int dl_event_elapsed_ms(dl_event* start, dl_event* stop, float* ms);
+
+/* ----------------------------------------------------- operation catalog */
+/* The eight operations of src/kernels/operations.h:169-202, with the launch
+ * signatures of src/kernels/cuda/launch.h:79-109.  Operands are device
+ * addresses (dl_buffer_address) in the reference's row-major layouts; every
+ * result is bit-exact with the reference's numerical contract
+ * (docs/architecture/transformer-execution.md:115-170), with this build's
+ * deterministic exp/sin/cos/sqrt in place of the unpinned native ones.
+ * `device_position`, when non-null, points at a uint64 position in device
+ * memory that replaces the host first_position (operations.h:234-239). */
+
+/* launch_projection: Y[R,O] = X[R,I] W[O,I]^T (launch.h:79-82). */
+int dl_projection(dl_queue* queue, int dtype, const void* input, const void* weight, void* output,
+                  uint64_t rows, uint64_t input_width, uint64_t output_width,
+                  const uint64_t* output_position);
+/* launch_rms_norm (launch.h:83-85). */
+int dl_rms_norm(dl_queue* queue, int dtype, const void* input, const void* weight, void* output,
+                uint64_t rows, uint64_t width, float epsilon);
+/* launch_rotary (launch.h:86-91). */
+int dl_rotary(dl_queue* queue, int dtype, const void* input, void* output, uint64_t positions,
+              uint64_t heads, uint64_t width, uint64_t first_position, double theta,
+              const uint64_t* device_position, int positioned_output);
+/* launch_attention_scale: *output = FP32(1/sqrt(width)) (launch.h:92-93). */
+int dl_attention_scale(dl_queue* queue, float* output, uint64_t width);
+/* launch_attention (launch.h:94-100): K/V rows [capacity, kv_heads, width]. */
+int dl_attention(dl_queue* queue, int dtype, const void* query, const void* key, const void* value,
+                 void* output, uint64_t positions, uint64_t query_heads, uint64_t kv_heads,
+                 uint64_t width, uint64_t first_position, const uint64_t* device_position,
+                 uint64_t capacity, const float* scale);
+/* launch_embedding (launch.h:101-103).  `vocabulary` bounds the table: a
+ * token id outside it yields a zero row instead of an out-of-bounds read. */
+int dl_embedding(dl_queue* queue, int dtype, const uint32_t* tokens, const void* weight,
+                 void* output, uint64_t rows, uint64_t width, uint64_t vocabulary);
+/* launch_add, launch_silu_multiply (launch.h:104-109). */
+int dl_add(dl_queue* queue, int dtype, const void* left, const void* right, void* output,
+           uint64_t count);
+int dl_silu_multiply(dl_queue* queue, int dtype, const void* gate, const void* up, void* output,
+                     uint64_t count);
+/* GatherRows (src/kernels/cuda/operations.cpp:544-572): copies the listed
+ * rows (host array) of `input` into consecutive rows of `output`. */
+int dl_gather_rows(dl_queue* queue, const void* input, void* output, uint64_t row_bytes,
+                   const uint64_t* rows, uint64_t count);
+
+/* ------------------------------------------- packed projection fast path */
+/* Weight layout is an implementation choice of the backend
+ * (docs/architecture/transformer-execution.md:47-48).  The packed layout
+ * stores each lane's reduction chain contiguously so that every wavefront
+ * load is a contiguous 1 KiB while the reference's partial ownership and
+ * merge tree are preserved bit for bit.  Requires BF16, output_width a
+ * multiple of 64/P and input_width a multiple of 8P (P from the reference's
+ * rule).  The row-major weight is not modified. */
+int dl_projection_packed_bytes(uint64_t output_width, uint64_t input_width, uint64_t* bytes);
+int dl_projection_pack(dl_queue* queue, const void* weight, void* packed, uint64_t output_width,
+                       uint64_t input_width);
+int dl_projection_packed(dl_queue* queue, const void* input, const void* packed, void* output,
+                         uint64_t rows, uint64_t input_width, uint64_t output_width,
+                         const uint64_t* output_position);
+
+/* -------------------------------------------------------------- Qwen3 model */
+typedef struct dl_qwen3 dl_qwen3;
+
+typedef struct dl_qwen3_config {
+  uint32_t layers;          /* 36 */
+  uint32_t hidden;          /* 4096 */
+  uint32_t q_heads;         /* 32 */
+  uint32_t kv_heads;        /* 8 */
+  uint32_t head_dim;        /* 128 */
+  uint32_t ffn;             /* 12288 */
+  uint32_t vocab;           /* 151936 */
+  uint32_t tied_embeddings; /* 1: the LM head and the embedding share storage */
+  float rms_eps;            /* 1e-6 */
+  uint32_t reserved;
+  double rope_theta;        /* 1e6 */
+} dl_qwen3_config;
+
+/* Parameter roles (src/models/qwen3/checkpoint.cpp:113-149 naming). */
+typedef enum dl_qwen3_role {
+  DL_ROLE_EMBEDDING = 0,
+  DL_ROLE_LM_HEAD = 1,
+  DL_ROLE_FINAL_NORM = 2,
+  DL_ROLE_INPUT_NORM = 3,
+  DL_ROLE_Q = 4,
+  DL_ROLE_K = 5,
+  DL_ROLE_V = 6,
+  DL_ROLE_Q_NORM = 7,
+  DL_ROLE_K_NORM = 8,
+  DL_ROLE_O = 9,
+  DL_ROLE_POST_NORM = 10,
+  DL_ROLE_GATE = 11,
+  DL_ROLE_UP = 12,
+  DL_ROLE_DOWN = 13
+} dl_qwen3_role;
+
+/* Allocates resident (packed) storage for every parameter
+ * (load_resident_model, src/inference/executor.cpp:772-833). */
+int dl_qwen3_create(dl_device* device, dl_queue* queue, const dl_qwen3_config* config,
+                    dl_qwen3** out);
+int dl_qwen3_destroy(dl_qwen3* model);
+/* Seeded synthetic parameters generated on the device: every projection
+ * and the embedding ~N(0, weight_std) in BF16, every norm gain 1.0.  Stream
+ * ids and the generator are documented in dl_synth.h; element i of the
+ * tensor (role, layer) in row-major order uses stream layer*16 + role. */
+int dl_qwen3_fill_synthetic(dl_qwen3* model, dl_queue* queue, uint64_t seed, float weight_std);
+/* Row-major BF16 transfer of one parameter (packing handled internally). */
+int dl_qwen3_write_tensor(dl_qwen3* model, dl_queue* queue, int role, uint32_t layer,
+                          const uint16_t* host, uint64_t elements);
+int dl_qwen3_read_tensor(dl_qwen3* model, dl_queue* queue, int role, uint32_t layer,
+                         uint16_t* host, uint64_t elements);
+/* Bytes of resident parameter storage. */
+int dl_qwen3_resident_bytes(dl_qwen3* model, uint64_t* bytes);
+
+/* ---------------------------------------------------------------- the plan */
+/* A cached forward plan for `batch` independent sequences sharing the
+ * model, each with a contiguous KV cache of `capacity` positions. */
+typedef struct dl_plan dl_plan;
+
+typedef struct dl_sampling {
+  uint32_t mode;      /* 0 greedy, 1 categorical (sampler.h:45-55) */
+  uint32_t top_k;     /* 0 disables */
+  double temperature; /* > 0 */
+  double top_p;       /* (0, 1] */
+} dl_sampling;
+
+typedef struct dl_generation_result {
+  uint32_t generated; /* tokens produced */
+  uint32_t reason;    /* 0 limit, 1 eos/stop id, 2 cancelled, 3 failure (device.h:93) */
+  uint32_t status;    /* sampler status latch: 0 ok, 1 NaN/+inf logit, 2 no finite logit */
+  uint32_t reserved;
+  uint64_t position;  /* next position */
+} dl_generation_result;
+
+int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t capacity,
+                   dl_plan** out);
+int dl_plan_destroy(dl_plan* plan);
+/* Clears positions and generation state (KV contents are overwritten). */
+int dl_plan_reset(dl_plan* plan);
+int dl_plan_position(dl_plan* plan, uint64_t* position);
+
+/* Writes cache rows [first_position, first_position + count) of one layer
+ * of one sequence from the reference layout [count, kv_heads, head_dim]
+ * (keys post-RoPE, values raw), as DeviceSequence cache appends would. */
+int dl_plan_write_cache(dl_plan* plan, uint32_t seq, uint32_t layer, uint64_t first_position,
+                        uint64_t count, const uint16_t* keys, const uint16_t* values);
+/* Reads the same rows back in the reference layout. */
+int dl_plan_read_cache(dl_plan* plan, uint32_t seq, uint32_t layer, uint64_t first_position,
+                       uint64_t count, uint16_t* keys, uint16_t* values);
+/* Moves the plan to `position`: rows below it are treated as cached. */
+int dl_plan_seek(dl_plan* plan, uint64_t position);
+/* Residual row of sequence `seq` after the last consumed position (the
+ * final block output, before the final RMSNorm). */
+int dl_plan_read_hidden(dl_plan* plan, uint32_t seq, uint16_t* host);
+
+/* Cached forward of `rows` tokens per sequence at the plan's position
+ * (tokens[seq * rows + i]); computes the logits of each sequence's last row.
+ * This is the diagnostic chunk path (executor.cpp:932-1031). */
+int dl_plan_forward(dl_plan* plan, const uint32_t* tokens, uint32_t rows);
+/* BF16 logits [vocab] of sequence `seq` from the last forward or step. */
+int dl_plan_read_logits(dl_plan* plan, uint32_t seq, uint16_t* host);
+/* Device address of sequence `seq`'s logits row (for dl_sampler_* use). */
+int dl_plan_logits_address(dl_plan* plan, uint32_t seq, void** out);
+
+/* Block-output capture (DeviceSequence::capture): after block `layer`'s
+ * second residual addition every consumed position's row is copied to
+ * capture[seq][position][hidden] (BF16).  layer < 0 disables. */
+int dl_plan_set_capture(dl_plan* plan, int32_t layer);
+int dl_plan_read_capture(dl_plan* plan, uint32_t seq, uint64_t first_position, uint64_t count,
+                         uint16_t* host);
+/* All-position residual steering of one sequence: after block `layer`'s
+ * output, h <- BF16(FP32(h) + vector[i]) for every position (FP32 vector of
+ * `hidden` values).  The capture of that block sees the steered row.  A null
+ * vector disables steering for the sequence. */
+int dl_plan_set_steering(dl_plan* plan, uint32_t seq, int32_t layer, const float* vector);
+/* Embedding override (EmbeddingOverride, executor.h:129-135): the embedding
+ * row of absolute prompt position `position` is replaced by `row` (BF16
+ * bits) for the sequences in `seq_mask` (bit i = sequence i). */
+int dl_plan_set_embedding_override(dl_plan* plan, uint64_t position, const uint16_t* row,
+                                   uint32_t seq_mask);
+
+/* Device-owned token loop.  Consumes the prompt (shared by all sequences),
+ * then generates up to max_new tokens per sequence with the sampling law of
+ * src/inference/sampling/categorical.cpp:146-201 and per-sequence
+ * MT19937-64 streams seeded seeds[seq] (null: seed 0).  Stop ids end a
+ * sequence after the stop token is emitted.  Work is only enqueued; use
+ * dl_plan_collect to wait for and read the results. */
+int dl_plan_generate(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length,
+                     uint32_t max_new, const dl_sampling* sampling, const uint64_t* seeds,
+                     const uint32_t* stop_ids, uint32_t stop_count);
+/* Same as dl_plan_generate but enqueues no step: the caller drives the loop
+ * with dl_plan_decode_steps (prompt_length + max_new steps complete it). */
+int dl_plan_prepare_generation(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length,
+                               uint32_t max_new, const dl_sampling* sampling,
+                               const uint64_t* seeds, const uint32_t* stop_ids,
+                               uint32_t stop_count);
+/* Enqueues `steps` further decode steps of an active generation (no host
+ * wait); used by the benchmark to time steady-state decoding. */
+int dl_plan_decode_steps(dl_plan* plan, uint32_t steps);
+/* Waits for the enqueued loop and copies each sequence's generated ids
+ * (tokens[seq * max_new + i]) and results. */
+int dl_plan_collect(dl_plan* plan, uint32_t* tokens, uint32_t max_new,
+                    dl_generation_result* results);
+/* Requests cancellation of the running loop (may be called from another
+ * thread; DeviceSequence::request_stop, decoding/device.h:126). */
+int dl_plan_request_stop(dl_plan* plan);
+
+/* ------------------------------------------------------- device sampler */
+/* DeviceCategorical (src/inference/sampling/device.h:58-85) over one BF16
+ * or FP32 logits row in device memory. */
+typedef struct dl_sampler dl_sampler;
+int dl_sampler_create(dl_device* device, dl_queue* queue, uint64_t vocabulary, int dtype,
+                      dl_sampler** out);
+int dl_sampler_destroy(dl_sampler* sampler);
+/* One selection with explicit 64-bit draw bits (DeviceCategorical::submit).
+ * Result pair {token, status} is written to *result_device (device memory,
+ * 8 bytes) when non-null and returned by dl_sampler_result. */
+int dl_sampler_submit(dl_sampler* sampler, const void* logits, const dl_sampling* settings,
+                      uint64_t draw_bits);
+/* Seeds the device MT19937-64 stream (DeviceCategorical::start). */
+int dl_sampler_start(dl_sampler* sampler, const dl_sampling* settings, uint64_t seed);
+/* One selection drawing from the device stream (submit_next). */
+int dl_sampler_submit_next(dl_sampler* sampler, const void* logits);
+/* Waits for the queue and returns {token, status}. */
+int dl_sampler_result(dl_sampler* sampler, uint32_t* token, uint32_t* status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DOLITTLE_HIP_H */
