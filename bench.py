@@ -1,0 +1,243 @@
+#!/usr/bin/env python3
+"""Qwen3-8B batch-1 decode tokens/s on one MI355X.
+
+Workload: the full Qwen3-8B architecture (36 blocks, tied 151,936-row LM
+head) with seeded random BF16 weights ~N(0, 0.02) generated on the device,
+a prompt of 128 seeded uniform-random token ids, fresh KV cache, greedy
+decoding of 256 tokens through the device-owned token loop.  One "step" is
+one decode token (one full forward of the last token + LM head + greedy
+selection).  The first token comes from the prompt pass; `--warmup` more
+steps run untimed; exactly `--steps` steps are timed with HIP events on the
+plan's stream.  Inputs are resident in HBM for the whole timed region.
+
+Also reported: prefill tokens/s of the 128-token prompt, the whole-step HBM
+roofline fraction, a live HIP-event roofline of the dominant kernel (the
+fused RMSNorm + gate/up GEMV + SiLU), and the CPU baseline: the CPU contract
+restatement (oracle/) timed on this host's cores on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Qwen3-8B batch-1 decode tokens/s on 1 MI355X; % HBM roofline; prefill tok/s"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def kernel_bytes(cfg, which):
+    """Algorithmic bytes of one launch of a decode-step kernel at batch 1."""
+    D, QW, KW, F, V = cfg.hidden, cfg.q_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim, cfg.ffn, cfg.vocab
+    return {
+        0: (QW + 2 * KW) * D * 2 + 2 * D * 2 + QW * 2 + KW * 2 + KW * 2,  # weights, norm+h, q/k out, v append
+        4: D * QW * 2 + QW * 2 + 2 * D * 2,                                 # weights, att in, h in/out
+        5: 2 * F * D * 2 + 2 * D * 2 + F * 2,                               # weights, norm+h, act out
+        6: D * F * 2 + F * 2 + 2 * D * 2,                                   # weights, act in, h in/out
+        7: V * D * 2 + 2 * D * 2 + V * 2,                                   # weights, norm+h, logits out
+    }[which]
+
+
+def step_bytes(cfg, context):
+    """SURVEY 8(d) algorithmic bytes of one batch-1 decode step with `context`
+    visible keys: projection weights incl. LM head, norm gains, embedding
+    row, KV read and append, BF16 logits."""
+    return (cfg.projection_bytes_per_token() + (cfg.layers * (2 * cfg.hidden + 2 * cfg.head_dim) + cfg.hidden) * 2
+            + cfg.hidden * 2 + cfg.layers * 2 * cfg.kv_heads * cfg.head_dim * 2 * (context + 1) + cfg.vocab * 2)
+
+
+def cpu_baseline(model, plan, context, threads):
+    """Times the CPU contract restatement on a bounded sample: one Qwen3-8B
+    block at `context` keys (layer 0 weights and KV rows copied from the
+    device) for a few positions, plus the final norm + LM head once; the
+    per-token time is extrapolated as layers * t_block + t_head."""
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle"))
+    import oracle as o
+    lib = o.lib()
+    lib.or_set_threads(threads)
+    cfg = model.config
+    dims = o.Dims(cfg.hidden, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.ffn, cfg.vocab, cfg.rms_eps,
+                  cfg.rope_theta)
+    roles = (("input_norm", "input_norm"), ("wq", "q"), ("wk", "k"), ("wv", "v"), ("q_norm", "q_norm"),
+             ("k_norm", "k_norm"), ("wo", "o"), ("post_norm", "post_norm"), ("wg", "gate"), ("wu", "up"),
+             ("wd", "down"))
+    block = {name: np.ascontiguousarray(model.read(role, 0).reshape(-1)) for name, role in roles}
+    lm = np.ascontiguousarray(model.read("lm_head").reshape(-1))
+    weights = o.Qwen3Weights(dims, [block], np.ascontiguousarray(model.read("final_norm")), lm, lm)
+    kw = cfg.kv_heads * cfg.head_dim
+    reps = 3
+    capacity = context + reps + 1
+    k = np.zeros(capacity * kw, np.uint16)
+    v = np.zeros(capacity * kw, np.uint16)
+    keys, values = plan.read_cache(0, 0, context)
+    k[: context * kw] = keys
+    v[: context * kw] = values
+    h = np.ascontiguousarray(plan.hidden(0))
+    t0 = time.perf_counter()
+    for r in range(reps):
+        o.block_forward(weights, 0, h, 1, context + r, k, v)
+    t_block = (time.perf_counter() - t0) / reps
+    t0 = time.perf_counter()
+    o.logits(weights, h)
+    t_head = time.perf_counter() - t0
+    per_token = cfg.layers * t_block + t_head
+    return {
+        "value": round(1.0 / per_token, 4),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"CPU contract restatement (oracle/, C, -O3, {threads} OpenMP threads): one Qwen3-8B block "
+                   f"timed over {reps} decode positions at {context} cached keys ({t_block * 1e3:.1f} ms/block) "
+                   f"plus final norm + LM head once ({t_head * 1e3:.1f} ms); per token extrapolated as "
+                   f"{cfg.layers} x block + head"),
+    }
+
+
+def load_traffic():
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_gateup.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        data = json.load(f)
+    return data.get("hbm_bytes_per_launch")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=250)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--prompt", type=int, default=128)
+    ap.add_argument("--seed", type=int, default=20261201)
+    ap.add_argument("--kernel-iters", type=int, default=72)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="also run one device-to-device copy of this many MiB (PMC scaling reference)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one MI355X: this backend has no multi-GPU path; run with --gpus 1",
+              file=sys.stderr)
+        return 2
+
+    from dolittle_amd import Device, Event, _lib
+    from dolittle_amd.qwen3 import Plan, Qwen3Config, Qwen3Model
+
+    device = Device(0)
+    queue = device.create_queue()
+    cfg = Qwen3Config()
+    t0 = time.perf_counter()
+    model = Qwen3Model(device, queue, cfg)
+    model.fill_synthetic(args.seed, 0.02)
+    queue.drain()
+    log(f"model resident: {model.resident_bytes() / 2**30:.2f} GiB in {time.perf_counter() - t0:.1f}s")
+    max_new = 1 + args.warmup + args.steps
+    capacity = args.prompt + max_new + 1
+    plan = Plan(model, batch=1, capacity=capacity)
+    prompt = np.random.default_rng(args.seed).integers(0, cfg.vocab, args.prompt).astype(np.uint32)
+    plan.prepare_generation(prompt, max_new)
+    e_p0, e_p1, e_a, e_b = Event(device), Event(device), Event(device), Event(device)
+    e_p0.record(queue)
+    plan.decode_steps(args.prompt)  # consumes the prompt, selects token 1
+    e_p1.record(queue)
+    plan.decode_steps(args.warmup)
+    queue.drain()
+    e_a.record(queue)
+    plan.decode_steps(args.steps)
+    e_b.record(queue)
+    queue.drain()
+    plan.decode_steps(1)  # consumes the last selection (completes the loop)
+    tokens, results = plan.collect()
+    prefill_ms = e_p0.elapsed_ms(e_p1)
+    decode_ms = e_a.elapsed_ms(e_b)
+    ms_per_step = decode_ms / args.steps
+    tok_s = 1000.0 / ms_per_step
+    assert results[0]["generated"] == max_new, results
+    first_ctx = args.prompt + 1 + args.warmup
+    mean_context = first_ctx + (args.steps - 1) / 2.0
+    bytes_step = step_bytes(cfg, mean_context)
+    step_gbs = bytes_step / (ms_per_step * 1e-3) / 1e9
+    log(f"prefill {args.prompt} tok in {prefill_ms:.2f} ms; decode {ms_per_step * 1e3:.1f} us/token "
+        f"= {tok_s:.1f} tok/s; step {step_gbs:.0f} GB/s ({step_gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+
+    # Live per-kernel timing on the plan's stream, cycling layers so every
+    # launch streams distinct weights.
+    _lib.call("dl_plan_bench_prepare", plan.handle)
+    kernels = {}
+    names = {0: "k_qkv", 4: "k_residual<16> (O)", 5: "k_gateup", 6: "k_residual<32> (down)", 7: "k_lm_head"}
+    for which in (5, 7, 0, 6, 4):
+        iters = args.kernel_iters if which != 7 else max(8, args.kernel_iters // 8)
+        _lib.call("dl_plan_launch_kernel", plan.handle, which, 0, 2)  # warm
+        ea, eb = Event(device), Event(device)
+        queue.drain()
+        ea.record(queue)
+        _lib.call("dl_plan_launch_kernel", plan.handle, which, 0, iters)
+        eb.record(queue)
+        us = ea.elapsed_ms(eb) * 1e3 / iters
+        gbs = kernel_bytes(cfg, which) / (us * 1e-6) / 1e9
+        kernels[names[which]] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"  {names[which]:<24} {us:8.2f} us  {gbs:7.0f} GB/s  {gbs / HBM_PEAK_GBS:.1%}")
+    dominant = kernels["k_gateup"]
+
+    if args.copy_calibration_mib:
+        n = args.copy_calibration_mib << 20
+        a, b = device.allocate(n), device.allocate(n)
+        queue.copy(b, a, n)
+        queue.drain()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(model, plan, int(mean_context), threads)
+        log(f"cpu baseline: {cpu['value']} tok/s ({time.perf_counter() - t0:.1f}s)")
+
+    gateup_bytes = kernel_bytes(cfg, 5)
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) BF16 weights generated on device, seeded uniform prompt ids)",
+        "config": {
+            "workload": "BASELINE config 2: Qwen3-8B, 36 blocks, tied 151936-row LM head, batch 1, "
+                        f"{args.prompt}-id prompt, greedy decode of {max_new} tokens",
+            "timed_decode_positions": [first_ctx, first_ctx + args.steps - 1],
+            "parallelism": "single-gpu",
+        },
+        "prefill_tokens_per_s": round(args.prompt / (prefill_ms * 1e-3), 1),
+        "hbm_roofline_step": {"bytes_per_step": int(bytes_step), "achieved_GBs": round(step_gbs, 1),
+                              "peak_GBs": HBM_PEAK_GBS, "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
+        "roofline": {
+            "kernel": "k_gateup (RMSNorm + gate/up GEMV + SiLU*up, one block)",
+            "bound": "hbm",
+            "achieved": dominant["GB/s"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": dominant["frac"],
+            "traffic": load_traffic(),
+            "algorithmic_bytes_per_launch": gateup_bytes,
+            "avg_launch_us": dominant["us"],
+        },
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -111,6 +111,9 @@ SIGNATURES = {
     "dl_plan_prepare_generation": [vp, u32p, u32, u32, C.POINTER(Sampling), u64p, u32p, u32],
     "dl_plan_decode_steps": [vp, u32],
     "dl_plan_collect": [vp, u32p, u32, C.POINTER(GenerationResult)],
+    "dl_plan_bench_prepare": [vp],
+    "dl_plan_launch_kernel": [vp, u32, u32, u32],
+    "dl_plan_set_grid": [vp, u32, u32],
     "dl_plan_request_stop": [vp],
     "dl_sampler_create": [vp, vp, u64, cint, vpp],
     "dl_sampler_destroy": [vp],

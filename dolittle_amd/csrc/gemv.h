@@ -57,6 +57,36 @@ __device__ __forceinline__ void stage_put(float* xs, int I, int b, int i, float 
 // One wavefront computes RW output rows for B input rows.  `tile` points at
 // the tile's first 16-byte chunk; on return lane (row, 0) of each P-lane
 // segment holds the merged FP32 sum of that row for every b.
+//
+// Loads are issued in batches of kBatch independent 16-byte chunks held in
+// distinct registers before any of them is consumed, so each wavefront keeps
+// kBatch KiB in flight instead of serialising on one load-use chain.
+constexpr int kBatch = 8;
+
+// One step of every lane's chain: 8 consecutive chain elements of weights w
+// against the staged inputs at step s, for each of the B rows.
+template <int B>
+__device__ __forceinline__ void chain_step(const u32x4 w, const float* __restrict__ xt, int bstride, int s,
+                                           float (&acc)[B]) {
+  const float w0 = dl_bf16_lo(w.x), w1 = dl_bf16_hi(w.x), w2 = dl_bf16_lo(w.y), w3 = dl_bf16_hi(w.y);
+  const float w4 = dl_bf16_lo(w.z), w5 = dl_bf16_hi(w.z), w6 = dl_bf16_lo(w.w), w7 = dl_bf16_hi(w.w);
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    const float4 xa = *reinterpret_cast<const float4*>(xt + b * bstride + 8 * s);
+    const float4 xb = *reinterpret_cast<const float4*>(xt + b * bstride + 8 * s + 4);
+    float a = acc[b];
+    a = fma_rn(xa.x, w0, a);
+    a = fma_rn(xa.y, w1, a);
+    a = fma_rn(xa.z, w2, a);
+    a = fma_rn(xa.w, w3, a);
+    a = fma_rn(xb.x, w4, a);
+    a = fma_rn(xb.y, w5, a);
+    a = fma_rn(xb.z, w6, a);
+    a = fma_rn(xb.w, w7, a);
+    acc[b] = a;
+  }
+}
+
 template <int P, int B>
 __device__ __forceinline__ void chain_tile(const u32x4* __restrict__ tile, const float* __restrict__ xs,
                                            int I, int lane, float (&acc)[B]) {
@@ -65,27 +95,15 @@ __device__ __forceinline__ void chain_tile(const u32x4* __restrict__ tile, const
   const u32x4* src = tile + lane;
 #pragma unroll
   for (int b = 0; b < B; ++b) acc[b] = 0.0f;
-#pragma unroll 8
-  for (int s = 0; s < S; ++s) {
-    const u32x4 w = load_stream(src + s * 64);
-    const float w0 = dl_bf16_lo(w.x), w1 = dl_bf16_hi(w.x), w2 = dl_bf16_lo(w.y), w3 = dl_bf16_hi(w.y);
-    const float w4 = dl_bf16_lo(w.z), w5 = dl_bf16_hi(w.z), w6 = dl_bf16_lo(w.w), w7 = dl_bf16_hi(w.w);
+  int s0 = 0;
+  for (; s0 + kBatch <= S; s0 += kBatch) {
+    u32x4 w[kBatch];
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const float4 xa = *reinterpret_cast<const float4*>(xt + b * bstride + 8 * s);
-      const float4 xb = *reinterpret_cast<const float4*>(xt + b * bstride + 8 * s + 4);
-      float a = acc[b];
-      a = fma_rn(xa.x, w0, a);
-      a = fma_rn(xa.y, w1, a);
-      a = fma_rn(xa.z, w2, a);
-      a = fma_rn(xa.w, w3, a);
-      a = fma_rn(xb.x, w4, a);
-      a = fma_rn(xb.y, w5, a);
-      a = fma_rn(xb.z, w6, a);
-      a = fma_rn(xb.w, w7, a);
-      acc[b] = a;
-    }
+    for (int j = 0; j < kBatch; ++j) w[j] = load_stream(src + (s0 + j) * 64);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) chain_step<B>(w[j], xt, bstride, s0 + j, acc);
   }
+  for (; s0 < S; ++s0) chain_step<B>(load_stream(src + s0 * 64), xt, bstride, s0, acc);
 #pragma unroll
   for (int b = 0; b < B; ++b) {
 #pragma unroll
@@ -123,6 +141,71 @@ __device__ __forceinline__ float block_rms_inverse(const uint16_t* __restrict__ 
   const float inverse = scratch[32];
   __syncthreads();
   return inverse;
+}
+
+// Stages round(round(h_b * inverse_b) * gain) for B rows of width D into the
+// staged LDS layouts for P = 16 (xs16, when non-null) and P = 32 (xs32, when
+// non-null), computing inverse_b with the reference tree
+// (normalization.cu:134-186) in the same pass: thread i < 128 keeps features
+// i + 128k of every row in registers, sums their squares in ascending k
+// (component i), combines groups of four left to right, and wave 0 reduces
+// the 32 lane totals with shuffle-down offsets 1..16.  One global round trip,
+// two barriers.  Requires D % 128 == 0, D <= 128 * kNormMaxK and B <= 2.
+constexpr int kNormMaxK = 32;
+
+template <int B>
+__device__ __forceinline__ void norm_stage(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
+                                           int D, float eps, float* xs16, float* xs32, float* scratch) {
+  static_assert(B <= 2, "one wavefront reduces at most two rows");
+  const int tid = threadIdx.x;
+  const int K = D / 128;
+  float hv[B][kNormMaxK];
+  float gv[kNormMaxK];
+  if (tid < 128) {
+#pragma unroll
+    for (int k = 0; k < kNormMaxK; ++k) {
+      if (k < K) {
+        gv[k] = dl_bf16_to_f32(gain[tid + 128 * k]);
+#pragma unroll
+        for (int b = 0; b < B; ++b) hv[b][k] = dl_bf16_to_f32(h[b * D + tid + 128 * k]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      float comp = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kNormMaxK; ++k)
+        if (k < K) comp = comp + hv[b][k] * hv[b][k];
+      const float second = __shfl_down(comp, 1, 4);
+      const float third = __shfl_down(comp, 2, 4);
+      const float fourth = __shfl_down(comp, 3, 4);
+      if ((tid & 3) == 0) scratch[b * 40 + (tid >> 2)] = ((comp + second) + third) + fourth;
+    }
+  }
+  __syncthreads();
+  if (tid < 32 * B) {
+    const int b = tid / 32;
+    float s = scratch[b * 40 + (tid & 31)];
+#pragma unroll
+    for (int off = 1; off < 32; off *= 2) s = s + __shfl_down(s, off, 32);
+    if ((tid & 31) == 0) scratch[b * 40 + 32] = inverse_sqrt(s * (1.0f / static_cast<float>(D)) + eps);
+  }
+  __syncthreads();
+  if (tid < 128) {
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const float inverse = scratch[b * 40 + 32];
+#pragma unroll
+      for (int k = 0; k < kNormMaxK; ++k) {
+        if (k < K) {
+          const float n = dl_round_bf16(dl_round_bf16(hv[b][k] * inverse) * gv[k]);
+          const int col = tid + 128 * k;
+          if (xs16) stage_put<16>(xs16, D, b, col, n);
+          if (xs32) stage_put<32>(xs32, D, b, col, n);
+        }
+      }
+    }
+  }
 }
 
 }  // namespace dl

@@ -24,6 +24,7 @@
 // (src/kernels/cuda/decode.cu:103-194, 339-353), which HIP lacks.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <vector>
@@ -231,38 +232,34 @@ __global__ __launch_bounds__(kBlock) void k_qkv(QkvArgs a) {
   extern __shared__ float lds[];
   float* xs16 = lds;
   float* xs32 = xs16 + B * staged_floats(16, a.D);
-  __shared__ float scratch[40];
+  __shared__ float scratch[80];
   if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
-  for (int b = 0; b < B; ++b) {
-    const uint16_t* hb = a.h + static_cast<uint64_t>(b) * a.D;
-    const float inverse = block_rms_inverse(hb, a.D, a.eps, scratch);
-    for (int i = threadIdx.x; i < a.D; i += blockDim.x) {
-      const float n = rbf(rbf(dl_bf16_to_f32(hb[i]) * inverse) * dl_bf16_to_f32(a.norm[i]));
-      stage_put<16>(xs16, a.D, b, i, n);
-      stage_put<32>(xs32, a.D, b, i, n);
-    }
-  }
-  __syncthreads();
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int q_tiles = a.QW / 4, k_tiles = a.KW / 2, total = q_tiles + 2 * k_tiles;
-  const uint64_t q_chunks = static_cast<uint64_t>(a.D / 128) * 64;
-  const uint64_t k_chunks = static_cast<uint64_t>(a.D / 256) * 64;
+  const int S16 = a.D / 128, S32 = a.D / 256;
+  const uint64_t q_chunks = static_cast<uint64_t>(S16) * 64;
+  const uint64_t k_chunks = static_cast<uint64_t>(S32) * 64;
+  norm_stage<B>(a.h, a.norm, a.D, a.eps, xs16, xs32, scratch);
+  __syncthreads();
+  (void)S16;
   for (int tile = blockIdx.x * kWaves + wave; tile < total; tile += gridDim.x * kWaves) {
+    const bool is_q = tile < q_tiles;
+    int kt = tile - q_tiles;
+    const bool is_v = !is_q && kt >= k_tiles;
+    if (is_v) kt -= k_tiles;
+    const u32x4* src = is_q ? a.w + tile * q_chunks
+                            : a.w + q_tiles * q_chunks + (is_v ? k_tiles : 0) * k_chunks + kt * k_chunks;
     float acc[B];
-    if (tile < q_tiles) {
-      chain_tile<16, B>(a.w + tile * q_chunks, xs16, a.D, lane, acc);
+    if (is_q) {
+      chain_tile<16, B>(src, xs16, a.D, lane, acc);
       if (lane % 16 == 0) {
         const int row = tile * 4 + lane / 16;
 #pragma unroll
         for (int b = 0; b < B; ++b) a.q_out[b * a.QW + row] = bf16_bits(acc[b]);
       }
     } else {
-      int kt = tile - q_tiles;
-      const bool is_v = kt >= k_tiles;
-      if (is_v) kt -= k_tiles;
-      chain_tile<32, B>(a.w + q_tiles * q_chunks + (is_v ? k_tiles : 0) * k_chunks + kt * k_chunks, xs32,
-                        a.D, lane, acc);
+      chain_tile<32, B>(src, xs32, a.D, lane, acc);
       if (lane % 32 == 0) {
         const int row = kt * 2 + lane / 32;
 #pragma unroll
@@ -455,6 +452,118 @@ __global__ __launch_bounds__(64) void k_attn_pv(AttnArgs a) {
   if (half == 0) a.att[static_cast<uint64_t>(b) * a.q_heads * kHeadDim + h * kHeadDim + f] = bf16_bits(acc + other);
 }
 
+// Short-context attention in one kernel (the reference's retained-score
+// kernel shape, attention.cu:231-383): grid (query head, sequence), 256
+// threads.  Wave 0 applies the head's RMSNorm + RoPE to q; wave 1 does the
+// same for the group's new key (written to the cache by the first head of
+// the group).  32 groups of 8 lanes score keys (ranges merged at 4,2,1),
+// scores stay in LDS, the max and the 32-partial denominator follow, and
+// the two PV key ranges run as 2 x 128 threads over the transposed V rows.
+constexpr int kFusedKeys = 1024;
+
+__global__ __launch_bounds__(kBlock) void k_attn_fused(AttnArgs a) {
+  __shared__ float qs[kHeadDim];
+  __shared__ float ks[kHeadDim];
+  __shared__ float sc[kFusedKeys];
+  __shared__ float red[kBlock];
+  __shared__ float denominator_shared;
+  if (!a.ctl->active) return;
+  const uint64_t pos = a.ctl->position;
+  const int count = static_cast<int>(pos) + 1;
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int wave = tid / 64, lane = tid % 64;
+  const int group = a.q_heads / a.kv_heads;
+  const int g = h / group;
+  const float* rope_pos = a.rope + pos * kHeadDim;
+  const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHeadDim, kw = static_cast<uint64_t>(a.kv_heads) * kHeadDim;
+  uint16_t* kc = a.k_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g) * a.cap * kHeadDim;
+  if (wave == 0)
+    head_norm_rope(a.q_raw + b * qw + static_cast<uint64_t>(h) * kHeadDim, a.q_norm, rope_pos, lane, a.eps, qs);
+  if (wave == 1) {
+    head_norm_rope(a.k_raw + b * kw + static_cast<uint64_t>(g) * kHeadDim, a.k_norm, rope_pos, lane, a.eps, ks);
+    if (h % group == 0) {
+      kc[pos * kHeadDim + lane] = bf16_bits(ks[lane]);
+      kc[pos * kHeadDim + lane + 64] = bf16_bits(ks[lane + 64]);
+    }
+  }
+  __syncthreads();
+  {
+    const int kg = tid / 8, l = tid % 8;
+    float q[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[i] = qs[16 * l + i];
+    for (int base = 0; base < count; base += kBlock / 8) {
+      const int j = base + kg;
+      float acc = 0.0f;
+      if (j < count) {
+        float kf[16];
+        if (static_cast<uint64_t>(j) == pos) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) kf[i] = ks[16 * l + i];
+        } else {
+          const u32x4* src = reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(j) * kHeadDim + 16 * l);
+          const u32x4 w0 = src[0], w1 = src[1];
+          kf[0] = dl_bf16_lo(w0.x); kf[1] = dl_bf16_hi(w0.x); kf[2] = dl_bf16_lo(w0.y); kf[3] = dl_bf16_hi(w0.y);
+          kf[4] = dl_bf16_lo(w0.z); kf[5] = dl_bf16_hi(w0.z); kf[6] = dl_bf16_lo(w0.w); kf[7] = dl_bf16_hi(w0.w);
+          kf[8] = dl_bf16_lo(w1.x); kf[9] = dl_bf16_hi(w1.x); kf[10] = dl_bf16_lo(w1.y); kf[11] = dl_bf16_hi(w1.y);
+          kf[12] = dl_bf16_lo(w1.z); kf[13] = dl_bf16_hi(w1.z); kf[14] = dl_bf16_lo(w1.w); kf[15] = dl_bf16_hi(w1.w);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc = fma_rn(q[i], kf[i], acc);
+      }
+#pragma unroll
+      for (int off = 4; off; off >>= 1) acc = acc + __shfl_down(acc, off, 8);
+      if (l == 0 && j < count) sc[j] = acc * a.scale;
+    }
+  }
+  __syncthreads();
+  float m = sc[0];
+  for (int j = tid; j < count; j += kBlock) m = fmaxf(m, sc[j]);
+  red[tid] = m;
+  __syncthreads();
+  for (int off = kBlock / 2; off; off >>= 1) {
+    if (tid < off) red[tid] = fmaxf(red[tid], red[tid + off]);
+    __syncthreads();
+  }
+  m = red[0];
+  __syncthreads();
+  for (int j = tid; j < count; j += kBlock) sc[j] = dl_expf(sc[j] - m);
+  __syncthreads();
+  if (tid < 32) {
+    float partial = 0.0f;
+    for (int j = tid; j < count; j += 32) partial = partial + sc[j];
+#pragma unroll
+    for (int off = 16; off; off >>= 1) partial = partial + __shfl_down(partial, off, 32);
+    if (tid == 0) denominator_shared = partial;
+  }
+  __syncthreads();
+  const float l = denominator_shared;
+  for (int j = tid; j < count; j += kBlock) sc[j] = sc[j] / l;
+  __syncthreads();
+  const int split = (count - 1) / 2 + 1;
+  const int f = tid % kHeadDim, half = tid / kHeadDim;
+  const uint16_t* v = a.v_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g * kHeadDim + f) * a.cap;
+  const int begin = half ? split : 0, end = half ? count : split;
+  float acc = 0.0f;
+  int j = begin;
+  for (; j < end && (j & 7); ++j) acc = fma_rn(sc[j], dl_bf16_to_f32(v[j]), acc);
+  for (; j + 8 <= end; j += 8) {
+    const u32x4 vv = *reinterpret_cast<const u32x4*>(v + j);
+    acc = fma_rn(sc[j], dl_bf16_lo(vv.x), acc);
+    acc = fma_rn(sc[j + 1], dl_bf16_hi(vv.x), acc);
+    acc = fma_rn(sc[j + 2], dl_bf16_lo(vv.y), acc);
+    acc = fma_rn(sc[j + 3], dl_bf16_hi(vv.y), acc);
+    acc = fma_rn(sc[j + 4], dl_bf16_lo(vv.z), acc);
+    acc = fma_rn(sc[j + 5], dl_bf16_hi(vv.z), acc);
+    acc = fma_rn(sc[j + 6], dl_bf16_lo(vv.w), acc);
+    acc = fma_rn(sc[j + 7], dl_bf16_hi(vv.w), acc);
+  }
+  for (; j < end; ++j) acc = fma_rn(sc[j], dl_bf16_to_f32(v[j]), acc);
+  red[tid] = acc;
+  __syncthreads();
+  if (tid < kHeadDim) a.att[static_cast<uint64_t>(b) * qw + h * kHeadDim + tid] = bf16_bits(red[tid] + red[tid + kHeadDim]);
+}
+
 // ------------------------------------------------- residual GEMV (O, down)
 struct ResidualArgs {
   const Control* ctl;
@@ -473,15 +582,16 @@ __global__ __launch_bounds__(kBlock) void k_residual(ResidualArgs a) {
   extern __shared__ float xs[];
   if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  constexpr int RW = 64 / P;
+  const int tiles = a.D / RW;
+  const int S = a.I / (8 * P);
+  const uint64_t chunks = static_cast<uint64_t>(S) * 64;
   for (int b = 0; b < B; ++b) {
     const uint16_t* xb = a.x + static_cast<uint64_t>(b) * a.I;
     for (int i = threadIdx.x; i < a.I; i += blockDim.x) stage_put<P>(xs, a.I, b, i, dl_bf16_to_f32(xb[i]));
   }
   __syncthreads();
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  constexpr int RW = 64 / P;
-  const int tiles = a.D / RW;
-  const uint64_t chunks = static_cast<uint64_t>(a.I / (8 * P)) * 64;
   const bool steer = a.steer != nullptr && a.layer == a.ctl->steer_layer;
   const bool capture = a.capture != nullptr && a.layer == a.ctl->capture_layer;
   const uint32_t steer_mask = a.ctl->steer_mask;
@@ -516,18 +626,15 @@ struct GateUpArgs {
 template <int B>
 __global__ __launch_bounds__(kBlock) void k_gateup(GateUpArgs a) {
   extern __shared__ float xs[];
-  __shared__ float scratch[40];
+  __shared__ float scratch[80];
   if (!a.ctl->active) return;
-  for (int b = 0; b < B; ++b) {
-    const uint16_t* hb = a.h + static_cast<uint64_t>(b) * a.D;
-    const float inverse = block_rms_inverse(hb, a.D, a.eps, scratch);
-    for (int i = threadIdx.x; i < a.D; i += blockDim.x)
-      stage_put<16>(xs, a.D, b, i, rbf(rbf(dl_bf16_to_f32(hb[i]) * inverse) * dl_bf16_to_f32(a.norm[i])));
-  }
-  __syncthreads();
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int tiles = a.F / 2;
-  const uint64_t chunks = static_cast<uint64_t>(a.D / 128) * 64;
+  const int S = a.D / 128;
+  const uint64_t chunks = static_cast<uint64_t>(S) * 64;
+  norm_stage<B>(a.h, a.norm, a.D, a.eps, xs, nullptr, scratch);
+  __syncthreads();
+  (void)S;
   for (int tile = blockIdx.x * kWaves + wave; tile < tiles; tile += gridDim.x * kWaves) {
     float acc[B];
     chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc);
@@ -587,20 +694,18 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 template <int B>
 __global__ __launch_bounds__(kBlock) void k_lm_head(HeadArgs a) {
   extern __shared__ float xs[];
-  __shared__ float scratch[40];
+  __shared__ float scratch[80];
   __shared__ uint64_t wave_keys[kWaves][B];
   __shared__ uint32_t wave_flags[kWaves][B];
   if (!a.ctl->active || !selecting(a.ctl)) return;
-  for (int b = 0; b < B; ++b) {
-    const uint16_t* hb = a.h + static_cast<uint64_t>(b) * a.D;
-    const float inverse = block_rms_inverse(hb, a.D, a.eps, scratch);
-    for (int i = threadIdx.x; i < a.D; i += blockDim.x)
-      stage_put<16>(xs, a.D, b, i, rbf(rbf(dl_bf16_to_f32(hb[i]) * inverse) * dl_bf16_to_f32(a.norm[i])));
-  }
-  __syncthreads();
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int tiles = static_cast<int>(a.V / 4);
-  const uint64_t chunks = static_cast<uint64_t>(a.D / 128) * 64;
+  const int S = a.D / 128;
+  const uint64_t chunks = static_cast<uint64_t>(S) * 64;
+  const int first = blockIdx.x * kWaves + wave;
+  (void)S;
+  norm_stage<B>(a.h, a.norm, a.D, a.eps, xs, nullptr, scratch);
+  __syncthreads();
   uint64_t best[B];
   uint32_t flags[B];
 #pragma unroll
@@ -608,7 +713,7 @@ __global__ __launch_bounds__(kBlock) void k_lm_head(HeadArgs a) {
     best[b] = 0;
     flags[b] = 0;
   }
-  for (int tile = blockIdx.x * kWaves + wave; tile < tiles; tile += gridDim.x * kWaves) {
+  for (int tile = first; tile < tiles; tile += gridDim.x * kWaves) {
     float acc[B];
     chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc);
     if (lane % 16 == 0) {
@@ -731,6 +836,16 @@ __global__ void k_fill_rowmajor(uint16_t* p, uint64_t n, uint64_t seed, uint64_t
 
 // Partial count of the reference projection rule (projection.cu:277-318).
 int partials_for(uint64_t in_w, uint64_t out_w) { return (in_w <= 4096 && out_w > 1024) ? 16 : 32; }
+
+__global__ void k_bench_control(const Control* live, Control* bench) {
+  Control c = *live;
+  c.active = 1;
+  c.select_row = 1;
+  c.capture_layer = -1;
+  c.steer_layer = -1;
+  if (c.position >= 1) c.position -= 1;
+  *bench = c;
+}
 
 __global__ void k_seek(Control* c, uint64_t position) {
   c->position = position;
@@ -998,9 +1113,10 @@ struct dl_plan {
   dl_qwen3* model = nullptr;
   dl_queue* queue = nullptr;
   uint32_t batch = 1, capacity = 0, cap = 0;  // cap: padded to 64
-  int head_blocks = 1024;
+  int head_blocks = 256;
   std::vector<void*> allocations;
   dl::Control* ctl = nullptr;
+  dl::Control* bench_ctl = nullptr;
   uint16_t *h = nullptr, *q_raw = nullptr, *k_raw = nullptr, *att = nullptr, *act = nullptr, *logits = nullptr;
   uint16_t *k_cache = nullptr, *v_cache = nullptr, *capture = nullptr, *override_row = nullptr;
   float *scores = nullptr, *probs = nullptr, *rope = nullptr, *steer = nullptr;
@@ -1010,8 +1126,18 @@ struct dl_plan {
   uint32_t* cancel_host = nullptr;
   uint32_t* cancel_device = nullptr;
   uint64_t cache_seq_stride = 0, cache_layer_stride = 0;
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
+  hipGraph_t graphs[2] = {nullptr, nullptr};  // [0] long context, [1] short context
+  hipGraphExec_t execs[2] = {nullptr, nullptr};
+  uint64_t host_position = 0;                 // position the next enqueued step consumes
+  bool eager = false;
+  // Workgroups per decode-step kernel (0: one tile per wavefront).
+  // Defaults from the workgroup sweep on MI355X (grid-stride over tiles).
+  uint32_t grid_override[8] = {256, 0, 0, 0, 256, 256, 512, 0};
+  unsigned grid_for(int which, uint64_t tiles) const {
+    const uint64_t full = dl::ceil_div(tiles, 4);
+    const uint64_t g = grid_override[which] ? grid_override[which] : full;
+    return static_cast<unsigned>(g < full ? g : full);
+  }
   // Host mirror of settings.
   uint64_t position = 0;
   int32_t capture_layer = -1;
@@ -1035,13 +1161,15 @@ struct dl_plan {
   }
 
   ~dl_plan() {
-    if (exec) (void)hipGraphExecDestroy(exec);
-    if (graph) (void)hipGraphDestroy(graph);
+    for (int i = 0; i < 2; ++i) {
+      if (execs[i]) (void)hipGraphExecDestroy(execs[i]);
+      if (graphs[i]) (void)hipGraphDestroy(graphs[i]);
+    }
     for (void* p : allocations) (void)hipFree(p);
     if (cancel_host) (void)hipHostFree(cancel_host);
   }
 
-  void record_step(hipStream_t s);
+  void record_step(hipStream_t s, bool short_context);
   void prepare_kernels();
   void capture_step();
 };
@@ -1071,57 +1199,82 @@ void prepare_kernels_b(dl_plan* p) {
   allow_lds(k_attn_softmax, size_t(p->cap) * sizeof(float));
 }
 
+// Launches one decode-step kernel `which` of layer `l` with control `ctl`.
 template <int B>
-void record_step_b(dl_plan* p, hipStream_t s) {
+void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Control* ctl) {
   using namespace dl;
   const dl_qwen3* m = p->model;
   const auto& c = m->cfg;
   const int D = c.hidden, QW = c.q_heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
   const uint32_t V = c.vocab;
-
-  BeginArgs begin{p->ctl, p->tokens, p->selected, p->h, m->lm_head, m->embedding, p->override_row,
-                  p->cancel_device, D, V, c.tied_embeddings ? 1 : 0};
-  k_step_begin<<<B, kBlock, 0, s>>>(begin);
-
   const size_t qkv_lds = size_t(B) * (staged_floats(16, D) + staged_floats(32, D)) * sizeof(float);
   const size_t o_lds = size_t(B) * staged_floats(16, QW) * sizeof(float);
   const size_t gu_lds = size_t(B) * staged_floats(16, D) * sizeof(float);
   const size_t down_lds = size_t(B) * staged_floats(32, F) * sizeof(float);
   const size_t soft_lds = size_t(p->cap) * sizeof(float);
-  const unsigned qkv_grid = ceil_div(QW / 4 + KW, kWaves);
-  const unsigned o_grid = ceil_div(D / 4, kWaves);
-  const unsigned gu_grid = ceil_div(F / 2, kWaves);
-  const unsigned down_grid = ceil_div(D / 2, kWaves);
   const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));
-
-  for (uint32_t l = 0; l < c.layers; ++l) {
-    uint16_t* kc = p->k_cache + uint64_t(l) * p->cache_layer_stride;
-    uint16_t* vc = p->v_cache + uint64_t(l) * p->cache_layer_stride;
-    QkvArgs qa{p->ctl, p->h, m->input_norm[l], reinterpret_cast<const u32x4*>(m->qkv[l]), p->q_raw, p->k_raw,
-               vc, p->cache_seq_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps};
-    k_qkv<B><<<qkv_grid, kBlock, qkv_lds, s>>>(qa);
-
-    AttnArgs aa{p->ctl, p->q_raw, p->k_raw, m->q_norm[l], m->k_norm[l], p->rope, kc, vc, p->cache_seq_stride,
-                p->scores, p->probs, p->att, static_cast<int>(c.q_heads), static_cast<int>(c.kv_heads),
-                static_cast<int>(p->cap), c.rms_eps, scale};
-    k_attn_qk<<<dim3(c.kv_heads, p->cap / 64, B), kBlock, 0, s>>>(aa);
-    k_attn_softmax<<<dim3(c.q_heads, B), kBlock, soft_lds, s>>>(aa);
-    k_attn_pv<<<dim3(c.kv_heads * 16, B), 64, 0, s>>>(aa);
-
-    ResidualArgs oa{p->ctl, p->att, reinterpret_cast<const u32x4*>(m->o[l]), p->h, nullptr, nullptr, QW, D,
-                    static_cast<int>(p->cap), static_cast<int>(l)};
-    k_residual<16, B><<<o_grid, kBlock, o_lds, s>>>(oa);
-
-    GateUpArgs ga{p->ctl, p->h, m->post_norm[l], reinterpret_cast<const u32x4*>(m->gu[l]), p->act, D, F, c.rms_eps};
-    k_gateup<B><<<gu_grid, kBlock, gu_lds, s>>>(ga);
-
-    ResidualArgs da{p->ctl, p->act, reinterpret_cast<const u32x4*>(m->down[l]), p->h, p->capture, p->steer, F, D,
-                    static_cast<int>(p->cap), static_cast<int>(l)};
-    k_residual<32, B><<<down_grid, kBlock, down_lds, s>>>(da);
+  uint16_t* kc = p->k_cache + uint64_t(l) * p->cache_layer_stride;
+  uint16_t* vc = p->v_cache + uint64_t(l) * p->cache_layer_stride;
+  AttnArgs aa{ctl, p->q_raw, p->k_raw, m->q_norm[l], m->k_norm[l], p->rope, kc, vc, p->cache_seq_stride,
+              p->scores, p->probs, p->att, static_cast<int>(c.q_heads), static_cast<int>(c.kv_heads),
+              static_cast<int>(p->cap), c.rms_eps, scale};
+  switch (which) {
+    case 0: {
+      QkvArgs qa{ctl, p->h, m->input_norm[l], reinterpret_cast<const u32x4*>(m->qkv[l]), p->q_raw, p->k_raw, vc,
+                 p->cache_seq_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps};
+      k_qkv<B><<<p->grid_for(0, QW / 4 + KW), kBlock, qkv_lds, s>>>(qa);
+      break;
+    }
+    case 1: k_attn_qk<<<dim3(c.kv_heads, p->cap / 64, B), kBlock, 0, s>>>(aa); break;
+    case 2: k_attn_softmax<<<dim3(c.q_heads, B), kBlock, soft_lds, s>>>(aa); break;
+    case 3: k_attn_pv<<<dim3(c.kv_heads * 16, B), 64, 0, s>>>(aa); break;
+    case 8: k_attn_fused<<<dim3(c.q_heads, B), kBlock, 0, s>>>(aa); break;
+    case 4: {
+      ResidualArgs oa{ctl, p->att, reinterpret_cast<const u32x4*>(m->o[l]), p->h, nullptr, nullptr, QW, D,
+                      static_cast<int>(p->cap), static_cast<int>(l)};
+      k_residual<16, B><<<p->grid_for(4, D / 4), kBlock, o_lds, s>>>(oa);
+      break;
+    }
+    case 5: {
+      GateUpArgs ga{ctl, p->h, m->post_norm[l], reinterpret_cast<const u32x4*>(m->gu[l]), p->act, D, F, c.rms_eps};
+      k_gateup<B><<<p->grid_for(5, F / 2), kBlock, gu_lds, s>>>(ga);
+      break;
+    }
+    case 6: {
+      ResidualArgs da{ctl, p->act, reinterpret_cast<const u32x4*>(m->down[l]), p->h, p->capture, p->steer, F, D,
+                      static_cast<int>(p->cap), static_cast<int>(l)};
+      k_residual<32, B><<<p->grid_for(6, D / 2), kBlock, down_lds, s>>>(da);
+      break;
+    }
+    case 7: {
+      HeadArgs ha{ctl, p->h, m->final_norm, reinterpret_cast<const u32x4*>(m->lm_head), p->logits, p->partial_keys,
+                  p->partial_flags, D, V, c.rms_eps};
+      k_lm_head<B><<<p->head_blocks, kBlock, gu_lds, s>>>(ha);
+      break;
+    }
+    default: fail(DL_INVALID_ARGUMENT, "unknown step kernel");
   }
-  HeadArgs ha{p->ctl, p->h, m->final_norm, reinterpret_cast<const u32x4*>(m->lm_head), p->logits, p->partial_keys,
-              p->partial_flags, D, V, c.rms_eps};
-  k_lm_head<B><<<p->head_blocks, kBlock, gu_lds, s>>>(ha);
+}
+
+// Records one decode step.  `short_context` selects the fused attention
+// kernel (positions below kFusedKeys) instead of the three-kernel split.
+template <int B>
+void record_step_b(dl_plan* p, hipStream_t s, bool short_context) {
+  using namespace dl;
+  const dl_qwen3* m = p->model;
+  const auto& c = m->cfg;
+  BeginArgs begin{p->ctl, p->tokens, p->selected, p->h, m->lm_head, m->embedding, p->override_row,
+                  p->cancel_device, static_cast<int>(c.hidden), c.vocab, c.tied_embeddings ? 1 : 0};
+  k_step_begin<<<B, kBlock, 0, s>>>(begin);
+  static const int kShort[] = {0, 8, 4, 5, 6};
+  static const int kLong[] = {0, 1, 2, 3, 4, 5, 6};
+  for (uint32_t l = 0; l < c.layers; ++l) {
+    if (short_context)
+      for (int which : kShort) launch_step_kernel<B>(p, s, which, l, p->ctl);
+    else
+      for (int which : kLong) launch_step_kernel<B>(p, s, which, l, p->ctl);
+  }
+  launch_step_kernel<B>(p, s, 7, 0, p->ctl);
   EndArgs ea{p->ctl, p->partial_keys, p->partial_flags, p->head_blocks, p->selected, p->out_tokens, p->cap,
              p->stop_mask, p->cancel_device, B};
   k_step_end<<<1, kBlock, 0, s>>>(ea);
@@ -1129,10 +1282,10 @@ void record_step_b(dl_plan* p, hipStream_t s) {
 
 }  // namespace
 
-void dl_plan::record_step(hipStream_t s) {
+void dl_plan::record_step(hipStream_t s, bool short_context) {
   switch (batch) {
-    case 1: record_step_b<1>(this, s); break;
-    case 2: record_step_b<2>(this, s); break;
+    case 1: record_step_b<1>(this, s, short_context); break;
+    case 2: record_step_b<2>(this, s, short_context); break;
     default: dl::fail(DL_LENGTH_ERROR, "batch sizes above 2 are not supported yet");
   }
 }
@@ -1147,30 +1300,54 @@ void dl_plan::prepare_kernels() {
 
 void dl_plan::capture_step() {
   hipStream_t s = queue->stream;
-  if (exec) (void)hipGraphExecDestroy(exec);
-  if (graph) (void)hipGraphDestroy(graph);
-  exec = nullptr;
-  graph = nullptr;
-  prepare_kernels();
-  dl::check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture");
-  try {
-    record_step(s);
-  } catch (...) {
-    hipGraph_t g = nullptr;
-    (void)hipStreamEndCapture(s, &g);
-    if (g) (void)hipGraphDestroy(g);
-    throw;
+  const char* env = std::getenv("DL_EAGER");
+  eager = env != nullptr && env[0] == '1';
+  for (int i = 0; i < 2; ++i) {
+    if (execs[i]) (void)hipGraphExecDestroy(execs[i]);
+    if (graphs[i]) (void)hipGraphDestroy(graphs[i]);
+    execs[i] = nullptr;
+    graphs[i] = nullptr;
   }
-  dl::check_hip(hipStreamEndCapture(s, &graph), "end capture");
-  dl::check_hip(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "graph instantiate");
+  prepare_kernels();
+  if (eager) return;
+  for (int i = 0; i < 2; ++i) {
+    if (i == 0 && cap <= static_cast<uint32_t>(dl::kFusedKeys)) continue;  // short graph covers every position
+    dl::check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture");
+    try {
+      record_step(s, i == 1);
+    } catch (...) {
+      hipGraph_t g = nullptr;
+      (void)hipStreamEndCapture(s, &g);
+      if (g) (void)hipGraphDestroy(g);
+      throw;
+    }
+    dl::check_hip(hipStreamEndCapture(s, &graphs[i]), "end capture");
+    dl::check_hip(hipGraphInstantiate(&execs[i], graphs[i], nullptr, nullptr, 0), "graph instantiate");
+  }
 }
 
 namespace {
+// Graph replay per step; with DL_EAGER=1 in the environment the same
+// kernels are launched directly on the stream (for profilers that cannot
+// trace graph launches).
+// The host tracks the position each enqueued step will consume (the device
+// position advances by one per step while the loop is active) and picks the
+// short-context graph below kFusedKeys.  A step launched after the loop
+// stopped exits at once in either graph.
 void launch_steps(dl_plan* p, uint32_t steps) {
-  for (uint32_t i = 0; i < steps; ++i) dl::check_hip(hipGraphLaunch(p->exec, p->queue->stream), "hipGraphLaunch");
+  for (uint32_t i = 0; i < steps; ++i) {
+    const bool short_context = p->host_position < static_cast<uint64_t>(dl::kFusedKeys);
+    if (p->eager)
+      p->record_step(p->queue->stream, short_context);
+    else
+      dl::check_hip(hipGraphLaunch(p->execs[short_context ? 1 : 0], p->queue->stream), "hipGraphLaunch");
+    ++p->host_position;
+  }
+  if (p->eager) dl::check_launch(p->queue, "decode step");
 }
 
 void init_control(dl_plan* p, uint64_t position, uint32_t prompt_length, uint32_t max_new, uint32_t mode) {
+  p->host_position = position;
   dl::InitArgs a{p->ctl, position, prompt_length, max_new, p->batch, mode, p->capture_layer, p->steer_layer,
                  p->steer_mask, p->override_active ? 1u : 0u, p->override_mask, p->override_position};
   dl::k_init_control<<<1, 1, 0, p->queue->stream>>>(a);
@@ -1196,6 +1373,7 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
     const uint64_t B = batch, D = c.hidden, QW = uint64_t(c.q_heads) * c.head_dim,
                    KW = uint64_t(c.kv_heads) * c.head_dim, F = c.ffn, V = c.vocab, L = c.layers, cap = p->cap;
     p->ctl = p->alloc<dl::Control>(1);
+    p->bench_ctl = p->alloc<dl::Control>(1);
     p->h = p->alloc<uint16_t>(B * D);
     p->q_raw = p->alloc<uint16_t>(B * QW);
     p->k_raw = p->alloc<uint16_t>(B * KW);
@@ -1212,8 +1390,8 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
     p->probs = p->alloc<float>(B * c.q_heads * cap);
     dl::check_hip(hipMemsetAsync(p->probs, 0, B * c.q_heads * cap * 4, queue->stream), "probs clear");
     p->rope = p->alloc<float>(cap * c.head_dim);
-    p->partial_keys = p->alloc<uint64_t>(B * p->head_blocks);
-    p->partial_flags = p->alloc<uint32_t>(B * p->head_blocks);
+    p->partial_keys = p->alloc<uint64_t>(B * 1024);
+    p->partial_flags = p->alloc<uint32_t>(B * 1024);
     p->tokens = p->alloc<uint32_t>(cap);
     p->selected = p->alloc<uint32_t>(B);
     p->out_tokens = p->alloc<uint32_t>(B * cap);
@@ -1239,6 +1417,49 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
   });
 }
 
+int dl_plan_bench_prepare(dl_plan* plan) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    dl::enter(plan->queue);
+    dl::k_bench_control<<<1, 1, 0, plan->queue->stream>>>(plan->ctl, plan->bench_ctl);
+    dl::check_launch(plan->queue, "bench control");
+  });
+}
+
+int dl_plan_launch_kernel(dl_plan* plan, uint32_t which, uint32_t first_layer, uint32_t count) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    dl::enter(plan->queue);
+    require(which <= 8, "unknown step kernel");
+    const uint32_t L = plan->model->cfg.layers;
+    require(first_layer < L, "layer out of range");
+    for (uint32_t i = 0; i < count; ++i) {
+      const uint32_t l = (first_layer + i) % L;
+      if (plan->batch == 1)
+        launch_step_kernel<1>(plan, plan->queue->stream, static_cast<int>(which), l, plan->bench_ctl);
+      else
+        launch_step_kernel<2>(plan, plan->queue->stream, static_cast<int>(which), l, plan->bench_ctl);
+    }
+    dl::check_launch(plan->queue, "step kernel");
+  });
+}
+
+int dl_plan_set_grid(dl_plan* plan, uint32_t which, uint32_t blocks) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    require(which <= 7, "unknown step kernel");
+    dl::enter(plan->queue);
+    if (which == 7) {
+      require(blocks >= 1 && blocks <= 1024, "LM head workgroups must be in [1, 1024]");
+      plan->head_blocks = static_cast<int>(blocks);
+    } else {
+      plan->grid_override[which] = blocks;
+    }
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "set grid wait");
+    plan->capture_step();
+  });
+}
+
 int dl_plan_destroy(dl_plan* plan) {
   return guard([&] {
     if (!plan) return;
@@ -1256,6 +1477,7 @@ int dl_plan_reset(dl_plan* plan) {
     dl::check_hip(hipMemsetAsync(plan->ctl, 0, sizeof(dl::Control), plan->queue->stream), "control clear");
     *plan->cancel_host = 0;
     plan->position = 0;
+    plan->host_position = 0;
     dl::check_hip(hipStreamSynchronize(plan->queue->stream), "reset");
   });
 }
@@ -1441,6 +1663,7 @@ int dl_plan_seek(dl_plan* plan, uint64_t position) {
     dl::enter(plan->queue);
     require(position < plan->capacity, "position outside the capacity", DL_LENGTH_ERROR);
     dl::k_seek<<<1, 1, 0, plan->queue->stream>>>(plan->ctl, position);
+    plan->host_position = position;
     dl::check_launch(plan->queue, "seek");
     dl::check_hip(hipStreamSynchronize(plan->queue->stream), "seek wait");
   });

@@ -308,6 +308,18 @@ int dl_plan_prepare_generation(dl_plan* plan, const uint32_t* prompt, uint32_t p
 /* Enqueues `steps` further decode steps of an active generation (no host
  * wait); used by the benchmark to time steady-state decoding. */
 int dl_plan_decode_steps(dl_plan* plan, uint32_t steps);
+/* Measurement hooks (not part of the reference interface).  bench_prepare
+ * snapshots the live control block into a separate always-active one;
+ * launch_kernel then enqueues `count` instances of one decode-step kernel
+ * (0 QKV, 1 attention scores, 2 softmax, 3 PV, 4 O + residual, 5 gate/up,
+ * 6 down + residual, 7 LM head, 8 short-context fused attention), cycling
+ * through layers from `first_layer`
+ * so repeated launches stream distinct weights, on the plan's queue. */
+int dl_plan_bench_prepare(dl_plan* plan);
+int dl_plan_launch_kernel(dl_plan* plan, uint32_t which, uint32_t first_layer, uint32_t count);
+/* Workgroup count of one decode-step kernel (0 restores the default of one
+ * weight tile per wavefront); re-records the step graph. */
+int dl_plan_set_grid(dl_plan* plan, uint32_t which, uint32_t blocks);
 /* Waits for the enqueued loop and copies each sequence's generated ids
  * (tokens[seq * max_new + i]) and results. */
 int dl_plan_collect(dl_plan* plan, uint32_t* tokens, uint32_t max_new,

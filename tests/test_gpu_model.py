@@ -125,6 +125,31 @@ def test_config1_single_block_decode(device, queue, oracle):
     assert np.array_equal(plan.logits(0), oracle.logits(w, run.h))
 
 
+@pytest.mark.parametrize("position", [77, 1023, 1024, 1500])
+def test_single_block_both_attention_paths(device, queue, oracle, position):
+    """Positions below 1024 run the fused short-context attention kernel,
+    positions from 1024 the three-kernel split; both equal the oracle."""
+    from dolittle_amd.qwen3 import Plan, Qwen3Model
+    model = Qwen3Model(device, queue, qwen_config(layers=1, vocab=2048))
+    model.fill_synthetic(SEED + 7, 0.02)
+    w = oracle_weights(oracle, model)
+    plan = Plan(model, batch=1, capacity=1600)
+    kw = 8 * 128
+    keys = oracle.normal_bf16(position * kw, SEED + 3, 2000, 1.0)
+    values = oracle.normal_bf16(position * kw, SEED + 3, 2001, 1.0)
+    plan.write_cache(0, 0, keys, values)
+    x = oracle.normal_bf16(4096, SEED + 3, 2002, 1.0)
+    plan.set_embedding_override(position, x, 1)
+    plan.seek(position)
+    plan.forward([0])
+    run = OracleRun(oracle, w, 1600)
+    run.k[0][: position * kw] = keys
+    run.v[0][: position * kw] = values
+    run.pos = position
+    run.step(0, logits=False, row=x)
+    assert np.array_equal(plan.hidden(0), run.h)
+
+
 def test_greedy_stream_bit_exact(small_model, oracle):
     """Prefill + greedy decode through the device-owned loop equals the
     contract mirror token for token, and the final logits bit for bit."""
