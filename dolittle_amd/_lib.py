@@ -115,12 +115,18 @@ SIGNATURES = {
     "dl_plan_launch_kernel": [vp, u32, u32, u32],
     "dl_plan_set_grid": [vp, u32, u32],
     "dl_plan_request_stop": [vp],
-    "dl_sampler_create": [vp, vp, u64, cint, vpp],
+    "dl_sampler_required_bytes": [u64, C.POINTER(u64)],
+    "dl_sampler_create": [vp, vp, u64, cint, u64, vpp],
     "dl_sampler_destroy": [vp],
-    "dl_sampler_submit": [vp, vp, C.POINTER(Sampling), u64],
-    "dl_sampler_start": [vp, C.POINTER(Sampling), u64],
-    "dl_sampler_submit_next": [vp, vp],
+    "dl_sampler_submit": [vp, vp, u64, C.POINTER(Sampling), u64],
+    "dl_sampler_start": [vp, C.POINTER(Sampling), u64, u32p, u32],
+    "dl_sampler_submit_next": [vp, vp, u64],
+    "dl_sampler_result_address": [vp, vpp],
+    "dl_sampler_terminal_address": [vp, vpp],
+    "dl_sampler_current_token_address": [vp, vpp],
     "dl_sampler_result": [vp, u32p, u32p],
+    "dl_sampler_set_exact": [vp, cint],
+    "dl_sampler_exact_replays": [vp, C.POINTER(u64)],
 }
 
 

@@ -29,6 +29,7 @@
 #include <memory>
 #include <vector>
 
+#include "dl_control.h"
 #include "dl_device.h"
 #include "dl_internal.h"
 #include "dl_synth.h"
@@ -36,27 +37,6 @@
 
 namespace dl {
 
-// Device-owned loop state (the reference's decode.cu State + Control).
-struct Control {
-  uint64_t position;        // absolute position consumed by the current step
-  uint32_t active;          // loop running
-  uint32_t prompt_length;   // positions [0, prompt_length) come from `tokens`
-  uint32_t generated;       // selections made so far (per sequence, lockstep)
-  uint32_t max_new;         // selection budget
-  uint32_t stop_pending;    // last selection made; the next step only consumes
-  uint32_t finished_mask;   // sequences that emitted a stop id
-  uint32_t all_mask;        // (1 << batch) - 1
-  uint32_t status;          // 0 ok, 1 NaN/+inf logit, 2 no finite logit, 4 bad token
-  uint32_t reason;          // 0 limit, 1 eos, 2 cancelled, 3 failure
-  uint32_t mode;            // 0 greedy, 1 categorical
-  uint32_t override_active;
-  uint32_t override_mask;
-  uint64_t override_position;
-  int32_t capture_layer;
-  int32_t steer_layer;
-  uint32_t steer_mask;
-  uint32_t select_row;      // 1 when the current step selects (set by k_step_begin)
-};
 
 namespace {
 

@@ -330,22 +330,41 @@ int dl_plan_request_stop(dl_plan* plan);
 
 /* ------------------------------------------------------- device sampler */
 /* DeviceCategorical (src/inference/sampling/device.h:58-85) over one BF16
- * or FP32 logits row in device memory. */
+ * logits row in device memory.  Selection follows the host law of
+ * src/inference/sampling/categorical.cpp:146-201 bit for bit: the device
+ * decides with guarded FP64 comparisons and replays the serial fold when a
+ * decision lies within its error band.  The result is two uint32 words
+ * {token, status} (status 0 ok, 1 NaN/+inf logit, 2 no finite logit). */
 typedef struct dl_sampler dl_sampler;
+/* DeviceCategorical::required_bytes (device.h:69). */
+int dl_sampler_required_bytes(uint64_t vocabulary, uint64_t* bytes);
+/* Constructor (device.h:60-61): budget below the required bytes is a
+ * DL_LENGTH_ERROR; dtype must be DL_BF16 (FP32 rows are rejected). */
 int dl_sampler_create(dl_device* device, dl_queue* queue, uint64_t vocabulary, int dtype,
-                      dl_sampler** out);
+                      uint64_t budget, dl_sampler** out);
 int dl_sampler_destroy(dl_sampler* sampler);
-/* One selection with explicit 64-bit draw bits (DeviceCategorical::submit).
- * Result pair {token, status} is written to *result_device (device memory,
- * 8 bytes) when non-null and returned by dl_sampler_result. */
-int dl_sampler_submit(dl_sampler* sampler, const void* logits, const dl_sampling* settings,
-                      uint64_t draw_bits);
-/* Seeds the device MT19937-64 stream (DeviceCategorical::start). */
-int dl_sampler_start(dl_sampler* sampler, const dl_sampling* settings, uint64_t seed);
-/* One selection drawing from the device stream (submit_next). */
-int dl_sampler_submit_next(dl_sampler* sampler, const void* logits);
+/* DeviceCategorical::submit (device.h:70-71): diagnostic selection with
+ * explicit draw bits (u = (bits >> 11) * 2^-53); row_bytes = vocabulary * 2. */
+int dl_sampler_submit(dl_sampler* sampler, const void* logits, uint64_t row_bytes,
+                      const dl_sampling* settings, uint64_t draw_bits);
+/* DeviceCategorical::start (device.h:75-76): validates, builds the stop mask
+ * and seeds the device MT19937-64 stream once. */
+int dl_sampler_start(dl_sampler* sampler, const dl_sampling* settings, uint64_t seed,
+                     const uint32_t* stop_ids, uint32_t stop_count);
+/* DeviceCategorical::submit_next (device.h:77): one draw from the device
+ * stream, then the terminal latch (a stop id or failure freezes the result). */
+int dl_sampler_submit_next(dl_sampler* sampler, const void* logits, uint64_t row_bytes);
+/* result_storage / terminal_state / current_token (device.h:78-80): device
+ * addresses of the 8-byte result, the uint32 terminal latch and the token. */
+int dl_sampler_result_address(dl_sampler* sampler, void** out);
+int dl_sampler_terminal_address(dl_sampler* sampler, void** out);
+int dl_sampler_current_token_address(dl_sampler* sampler, void** out);
 /* Waits for the queue and returns {token, status}. */
 int dl_sampler_result(dl_sampler* sampler, uint32_t* token, uint32_t* status);
+/* Diagnostics without a reference counterpart: always decide by the exact
+ * serial replay, and the number of selections the replay decided. */
+int dl_sampler_set_exact(dl_sampler* sampler, int exact);
+int dl_sampler_exact_replays(dl_sampler* sampler, uint64_t* count);
 
 #ifdef __cplusplus
 }

@@ -123,6 +123,18 @@ int ors_categorical_select(const float* logits, size_t n, int mode, double tempe
 int ors_categorical_select_bits(const float* logits, size_t n, int mode, double temperature,
                                 size_t top_k, double top_p, uint64_t draw_bits, uint32_t* id);
 
+/* Same law with the weight exp chosen: build_exp 0 = glibc exp (the
+ * reference host), 1 = the build's dl_exp (the device's serial replay). */
+int ors_categorical_select_bits_exp(const float* logits, size_t n, int mode, double temperature,
+                                    size_t top_k, double top_p, uint64_t draw_bits, int build_exp,
+                                    uint32_t* id);
+/* The categorical law's serial quantities for building boundary cases:
+ * kept ids in sorted order (size), fold[k-1] = F_k, the cutoff count and
+ * cumulative[i-1] = G_i for i <= count.  Arrays hold n entries. */
+int ors_categorical_trace(const float* logits, size_t n, double temperature, size_t top_k,
+                          double top_p, int build_exp, uint32_t* ids, double* fold,
+                          double* cumulative, size_t* size, size_t* count);
+
 /* ---- synthetic inputs (dolittle_amd/csrc/dl_synth.h), regenerated on the CPU ---- */
 void or_fill_normal_bf16(uint16_t* out, size_t n, uint64_t seed, uint64_t stream, float scale,
                          size_t first_index);

@@ -83,6 +83,13 @@ def lib():
         L.ors_categorical_select_bits.argtypes = [f32p, sz, C.c_int, C.c_double, sz, C.c_double,
                                                   C.c_uint64, C.POINTER(C.c_uint32)]
         L.ors_categorical_select_bits.restype = C.c_int
+        L.ors_categorical_select_bits_exp.argtypes = [f32p, sz, C.c_int, C.c_double, sz, C.c_double,
+                                                      C.c_uint64, C.c_int, C.POINTER(C.c_uint32)]
+        L.ors_categorical_select_bits_exp.restype = C.c_int
+        f64o = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+        L.ors_categorical_trace.argtypes = [f32p, sz, C.c_double, sz, C.c_double, C.c_int, u32p, f64o,
+                                            f64o, C.POINTER(sz), C.POINTER(sz)]
+        L.ors_categorical_trace.restype = C.c_int
         L.or_fill_normal_bf16.argtypes = [u16p, sz, C.c_uint64, C.c_uint64, C.c_float, sz]
         L.or_set_threads.argtypes = [C.c_int]
         L.orc_rope_angles.argtypes = [sz, sz, C.c_double, f32p, f32p]
@@ -207,6 +214,31 @@ def categorical_bits(logits_f32, mode, temperature, top_k, top_p, bits) -> tuple
                                                len(logits_f32), mode, temperature, top_k, top_p,
                                                bits, C.byref(out))
     return status, out.value
+
+
+def categorical_bits_exp(logits_f32, mode, temperature, top_k, top_p, bits, build_exp) -> tuple[int, int]:
+    """The law with the weight exp chosen: build_exp False = glibc exp (the
+    reference host), True = the build's dl_exp (the device's serial replay)."""
+    out = C.c_uint32(0)
+    status = lib().ors_categorical_select_bits_exp(np.ascontiguousarray(logits_f32, np.float32),
+                                                   len(logits_f32), mode, temperature, top_k, top_p,
+                                                   bits, int(build_exp), C.byref(out))
+    return status, out.value
+
+
+def categorical_trace(logits_f32, temperature, top_k, top_p, build_exp=False):
+    """Serial quantities of the categorical law: (ids in kept order, F_k for
+    k = 1..size, G_i for i = 1..cutoff)."""
+    x = np.ascontiguousarray(logits_f32, np.float32)
+    n = len(x)
+    ids = np.zeros(n, np.uint32)
+    fold = np.zeros(n, np.float64)
+    cumulative = np.zeros(n, np.float64)
+    size, count = C.c_size_t(0), C.c_size_t(0)
+    status = lib().ors_categorical_trace(x, n, temperature, top_k, top_p, int(build_exp), ids, fold,
+                                         cumulative, C.byref(size), C.byref(count))
+    assert status == 0, status
+    return ids[: size.value], fold[: size.value], cumulative[: count.value]
 
 
 class MT19937_64:

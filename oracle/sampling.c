@@ -17,6 +17,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "../dolittle_amd/csrc/dl_math.h"
 #include "oracle.h"
 
 void or_mt64_seed(or_mt64* s, uint64_t seed) {
@@ -68,8 +69,23 @@ static int valid_settings(int mode, double temperature, double top_p, size_t top
   return 1;
 }
 
-static int select_impl(const float* logits, size_t n, int mode, double temperature, size_t top_k,
-                       double top_p, or_mt64* rng, uint64_t bits, uint32_t* id) {
+/* Weight exp: glibc's exp (the reference host, std::exp) or, for checking
+ * the device's serial replay, the build's deterministic dl_exp. */
+static double weight_exp(double x, int build_exp) { return build_exp ? dl_exp(x) : exp(x); }
+
+/* Serial trace of the categorical law: sorted kept ids, the fold F_k of
+ * the first k weights, the cutoff count and the cumulative draw sums G_i. */
+typedef struct trace {
+  uint32_t* ids;
+  double* fold;
+  double* cumulative;
+  size_t size;
+  size_t count;
+} trace;
+
+static int select_impl_exp(const float* logits, size_t n, int mode, double temperature, size_t top_k,
+                           double top_p, or_mt64* rng, uint64_t bits, int build_exp, trace* out,
+                           uint32_t* id) {
   if (!valid_settings(mode, temperature, top_p, top_k) || top_k > n) return 3;
   for (size_t i = 0; i < n; ++i)
     if (isnan(logits[i]) || (isinf(logits[i]) && logits[i] > 0)) return 1;
@@ -99,14 +115,25 @@ static int select_impl(const float* logits, size_t n, int mode, double temperatu
   const double maximum = (double)c[0].value;
   double total = 0;
   for (size_t i = 0; i < size; ++i) {
-    c[i].weight = exp(((double)c[i].value - maximum) / temperature);
+    c[i].weight = weight_exp(((double)c[i].value - maximum) / temperature, build_exp);
     total += c[i].weight;
+    if (out) out->fold[i] = total;
   }
   double retained = 0;
   size_t count = 0;
   for (;;) {
     retained += c[count++].weight;
     if (!(count < size && retained / total < top_p)) break;
+  }
+  if (out) {
+    out->size = size;
+    out->count = count;
+    double g = 0;
+    for (size_t i = 0; i < size; ++i) out->ids[i] = c[i].id;
+    for (size_t i = 0; i < count; ++i) {
+      g += c[i].weight / retained;
+      out->cumulative[i] = g;
+    }
   }
   const uint64_t x = rng ? or_mt64_next(rng) : bits;
   const double u = (double)(x >> 11) * 0x1p-53;
@@ -126,10 +153,29 @@ static int select_impl(const float* logits, size_t n, int mode, double temperatu
 
 int ors_categorical_select(const float* logits, size_t n, int mode, double temperature,
                            size_t top_k, double top_p, or_mt64* rng, uint32_t* id) {
-  return select_impl(logits, n, mode, temperature, top_k, top_p, rng, 0, id);
+  return select_impl_exp(logits, n, mode, temperature, top_k, top_p, rng, 0, 0, NULL, id);
 }
 
 int ors_categorical_select_bits(const float* logits, size_t n, int mode, double temperature,
                                 size_t top_k, double top_p, uint64_t draw_bits, uint32_t* id) {
-  return select_impl(logits, n, mode, temperature, top_k, top_p, NULL, draw_bits, id);
+  return select_impl_exp(logits, n, mode, temperature, top_k, top_p, NULL, draw_bits, 0, NULL, id);
+}
+
+int ors_categorical_select_bits_exp(const float* logits, size_t n, int mode, double temperature,
+                                    size_t top_k, double top_p, uint64_t draw_bits, int build_exp,
+                                    uint32_t* id) {
+  return select_impl_exp(logits, n, mode, temperature, top_k, top_p, NULL, draw_bits, build_exp, NULL,
+                         id);
+}
+
+int ors_categorical_trace(const float* logits, size_t n, double temperature, size_t top_k,
+                          double top_p, int build_exp, uint32_t* ids, double* fold,
+                          double* cumulative, size_t* size, size_t* count) {
+  trace t = {ids, fold, cumulative, 0, 0};
+  uint32_t id = 0;
+  const int status =
+      select_impl_exp(logits, n, 1, temperature, top_k, top_p, NULL, 0, build_exp, &t, &id);
+  *size = t.size;
+  *count = t.count;
+  return status;
 }

@@ -174,6 +174,48 @@ def test_sampler_distribution_contract_against_reference(oracle):
                 assert st == 0 and got == expected[i]
 
 
+def test_sampler_trace_restates_the_law(oracle):
+    """The serial trace used to place boundary draws: F_n is the serial fold
+    (checked against a Python left fold), G at the cutoff is within a few
+    ulps of 1, a draw at G_i picks candidate i + 1 and one below picks i, and
+    the glibc-exp law equals the default law."""
+    gen = oracle.MT19937_64(11)
+    logits = oracle.f32_from_bf16(oracle.normal_bf16(3000, 5, 77, 1.28))
+    ids, fold, cumulative = oracle.categorical_trace(logits, 1.0, 0, 0.9)
+    order = sorted(range(len(logits)), key=lambda i: (-float(logits[i]), i))
+    assert ids.tolist() == order
+    z0 = float(logits[order[0]])
+    total = 0.0
+    for i in order:
+        total += math.exp(float(logits[i]) - z0)
+    assert fold[-1] == total
+    assert abs(cumulative[-1] - 1.0) < 1e-12
+    c = len(cumulative)
+    assert fold[c - 1] / fold[-1] >= 0.9 and fold[c - 2] / fold[-1] < 0.9
+    for i in (0, c // 2, c - 2):
+        u = cumulative[i]
+        m = int(u * 2.0**53)
+        if m * 2.0**-53 != u:
+            continue
+        assert oracle.categorical_bits(logits, 1, 1.0, 0, 0.9, m << 11)[1] == ids[i + 1]
+        assert oracle.categorical_bits(logits, 1, 1.0, 0, 0.9, (m - 1) << 11)[1] == ids[i]
+    for _ in range(20):
+        bits = gen()
+        assert oracle.categorical_bits_exp(logits, 1, 1.0, 0, 0.9, bits, False) == \
+            oracle.categorical_bits(logits, 1, 1.0, 0, 0.9, bits)
+
+
+def test_sampler_build_exp_law_agrees_off_boundary(oracle):
+    """With the build's exp the law picks the same ids as with glibc exp for
+    ordinary draws (they differ only on draws within ~1e-12 of a boundary)."""
+    gen = oracle.MT19937_64(12)
+    logits = oracle.f32_from_bf16(oracle.normal_bf16(151936, 6, 77, 1.28))
+    for _ in range(16):
+        bits = gen()
+        assert oracle.categorical_bits_exp(logits, 1, 1.0, 0, 0.95, bits, True) == \
+            oracle.categorical_bits_exp(logits, 1, 1.0, 0, 0.95, bits, False)
+
+
 def _ulp64(a, b):
     ia = a.view(np.int64).copy()
     ib = b.view(np.int64).copy()
