@@ -143,23 +143,25 @@ __device__ __forceinline__ float block_rms_inverse(const uint16_t* __restrict__ 
   return inverse;
 }
 
-// Stages round(round(h_b * inverse_b) * gain) for B rows of width D into the
-// staged LDS layouts for P = 16 (xs16, when non-null) and P = 32 (xs32, when
-// non-null), computing inverse_b with the reference tree
-// (normalization.cu:134-186) in the same pass: thread i < 128 keeps features
-// i + 128k of every row in registers, sums their squares in ascending k
-// (component i), combines groups of four left to right, and wave 0 reduces
-// the 32 lane totals with shuffle-down offsets 1..16.  One global round trip,
-// two barriers.  Requires D % 128 == 0, D <= 128 * kNormMaxK and B <= 2.
+// Stages round(round(h_b * inverse_b) * gain) for R <= 2 rows (starting at
+// row b0) of width D into the staged LDS layouts for P = 16 (xs16, when
+// non-null) and P = 32 (xs32, when non-null), computing inverse_b with the
+// reference tree (normalization.cu:134-186) in the same pass: thread i < 128
+// keeps features i + 128k of every row in registers, sums their squares in
+// ascending k (component i), combines groups of four left to right, and the
+// lanes below 32 R reduce the 32 lane totals with shuffle-down offsets 1..16.
+// One global round trip, two barriers.  Requires D % 128 == 0 and
+// D <= 128 * kNormMaxK.
 constexpr int kNormMaxK = 32;
 
-template <int B>
-__device__ __forceinline__ void norm_stage(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
-                                           int D, float eps, float* xs16, float* xs32, float* scratch) {
-  static_assert(B <= 2, "one wavefront reduces at most two rows");
+template <int R>
+__device__ __forceinline__ void norm_stage_rows(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
+                                                int D, float eps, float* xs16, float* xs32, float* scratch,
+                                                int b0) {
+  static_assert(R <= 2, "one wavefront reduces at most two rows");
   const int tid = threadIdx.x;
   const int K = D / 128;
-  float hv[B][kNormMaxK];
+  float hv[R][kNormMaxK];
   float gv[kNormMaxK];
   if (tid < 128) {
 #pragma unroll
@@ -167,11 +169,11 @@ __device__ __forceinline__ void norm_stage(const uint16_t* __restrict__ h, const
       if (k < K) {
         gv[k] = dl_bf16_to_f32(gain[tid + 128 * k]);
 #pragma unroll
-        for (int b = 0; b < B; ++b) hv[b][k] = dl_bf16_to_f32(h[b * D + tid + 128 * k]);
+        for (int b = 0; b < R; ++b) hv[b][k] = dl_bf16_to_f32(h[(b0 + b) * D + tid + 128 * k]);
       }
     }
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
+    for (int b = 0; b < R; ++b) {
       float comp = 0.0f;
 #pragma unroll
       for (int k = 0; k < kNormMaxK; ++k)
@@ -183,7 +185,7 @@ __device__ __forceinline__ void norm_stage(const uint16_t* __restrict__ h, const
     }
   }
   __syncthreads();
-  if (tid < 32 * B) {
+  if (tid < 32 * R) {
     const int b = tid / 32;
     float s = scratch[b * 40 + (tid & 31)];
 #pragma unroll
@@ -193,18 +195,33 @@ __device__ __forceinline__ void norm_stage(const uint16_t* __restrict__ h, const
   __syncthreads();
   if (tid < 128) {
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
+    for (int b = 0; b < R; ++b) {
       const float inverse = scratch[b * 40 + 32];
 #pragma unroll
       for (int k = 0; k < kNormMaxK; ++k) {
         if (k < K) {
           const float n = dl_round_bf16(dl_round_bf16(hv[b][k] * inverse) * gv[k]);
           const int col = tid + 128 * k;
-          if (xs16) stage_put<16>(xs16, D, b, col, n);
-          if (xs32) stage_put<32>(xs32, D, b, col, n);
+          if (xs16) stage_put<16>(xs16, D, b0 + b, col, n);
+          if (xs32) stage_put<32>(xs32, D, b0 + b, col, n);
         }
       }
     }
+  }
+}
+
+// norm_stage_rows over B rows, two at a time (scratch is reused between
+// pairs behind a barrier).
+template <int B>
+__device__ __forceinline__ void norm_stage(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
+                                           int D, float eps, float* xs16, float* xs32, float* scratch) {
+#pragma unroll
+  for (int b0 = 0; b0 < B; b0 += 2) {
+    if (b0) __syncthreads();
+    if (B - b0 >= 2)
+      norm_stage_rows<2>(h, gain, D, eps, xs16, xs32, scratch, b0);
+    else
+      norm_stage_rows<1>(h, gain, D, eps, xs16, xs32, scratch, b0);
   }
 }
 

@@ -34,6 +34,7 @@
 #include "dl_internal.h"
 #include "dl_synth.h"
 #include "gemv.h"
+#include "sampler.h"
 
 namespace dl {
 
@@ -553,6 +554,7 @@ struct ResidualArgs {
   uint16_t* capture;     // [B][cap][D] or null
   const float* steer;    // [B][D] or null
   int I, D, cap, layer;
+  int row0;              // first sequence of this launch's row group
 };
 
 // y = round(x W^T); h = round(h + y); optionally h = round(h + steer) and a
@@ -568,7 +570,7 @@ __global__ __launch_bounds__(kBlock) void k_residual(ResidualArgs a) {
   const int S = a.I / (8 * P);
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
   for (int b = 0; b < B; ++b) {
-    const uint16_t* xb = a.x + static_cast<uint64_t>(b) * a.I;
+    const uint16_t* xb = a.x + static_cast<uint64_t>(a.row0 + b) * a.I;
     for (int i = threadIdx.x; i < a.I; i += blockDim.x) stage_put<P>(xs, a.I, b, i, dl_bf16_to_f32(xb[i]));
   }
   __syncthreads();
@@ -582,11 +584,12 @@ __global__ __launch_bounds__(kBlock) void k_residual(ResidualArgs a) {
       const int row = tile * RW + lane / P;
 #pragma unroll
       for (int b = 0; b < B; ++b) {
-        const uint64_t at = static_cast<uint64_t>(b) * a.D + row;
+        const int seq = a.row0 + b;
+        const uint64_t at = static_cast<uint64_t>(seq) * a.D + row;
         float value = rbf(dl_bf16_to_f32(a.h[at]) + rbf(acc[b]));
-        if (steer && ((steer_mask >> b) & 1u)) value = rbf(value + a.steer[at]);
+        if (steer && ((steer_mask >> seq) & 1u)) value = rbf(value + a.steer[at]);
         a.h[at] = bf16_bits(value);
-        if (capture) a.capture[(static_cast<uint64_t>(b) * a.cap + pos) * a.D + row] = bf16_bits(value);
+        if (capture) a.capture[(static_cast<uint64_t>(seq) * a.cap + pos) * a.D + row] = bf16_bits(value);
       }
     }
   }
@@ -641,6 +644,7 @@ struct HeadArgs {
   int D;
   uint32_t V;
   float eps;
+  int row0;                // first sequence of this launch's row group
 };
 
 // Orders BF16 logits: key = (ordered value << 32) | ~id, so the maximum key
@@ -684,7 +688,7 @@ __global__ __launch_bounds__(kBlock) void k_lm_head(HeadArgs a) {
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
   const int first = blockIdx.x * kWaves + wave;
   (void)S;
-  norm_stage<B>(a.h, a.norm, a.D, a.eps, xs, nullptr, scratch);
+  norm_stage<B>(a.h + static_cast<uint64_t>(a.row0) * a.D, a.norm, a.D, a.eps, xs, nullptr, scratch);
   __syncthreads();
   uint64_t best[B];
   uint32_t flags[B];
@@ -701,7 +705,7 @@ __global__ __launch_bounds__(kBlock) void k_lm_head(HeadArgs a) {
 #pragma unroll
       for (int b = 0; b < B; ++b) {
         const uint16_t bits = bf16_bits(acc[b]);
-        a.logits[static_cast<uint64_t>(b) * a.V + row] = bits;
+        a.logits[static_cast<uint64_t>(a.row0 + b) * a.V + row] = bits;
         logit_key(bits, row, &best[b], &flags[b]);
       }
     }
@@ -726,8 +730,8 @@ __global__ __launch_bounds__(kBlock) void k_lm_head(HeadArgs a) {
       k = wave_keys[w][b] > k ? wave_keys[w][b] : k;
       f |= wave_flags[w][b];
     }
-    a.partial_keys[static_cast<uint64_t>(b) * gridDim.x + blockIdx.x] = k;
-    a.partial_flags[static_cast<uint64_t>(b) * gridDim.x + blockIdx.x] = f;
+    a.partial_keys[static_cast<uint64_t>(a.row0 + b) * gridDim.x + blockIdx.x] = k;
+    a.partial_flags[static_cast<uint64_t>(a.row0 + b) * gridDim.x + blockIdx.x] = f;
   }
 }
 
@@ -745,8 +749,10 @@ struct EndArgs {
   int batch;
 };
 
-// Greedy selection from the argmax partials, token stream, stop latches
-// and position advance (decode.cu finish_selection / finish_consumption).
+// Greedy selection from the argmax partials (categorical rows were selected
+// by the device sampler before this kernel), per-sequence token streams,
+// stop latches and position advance (decode.cu finish_selection /
+// finish_consumption).  A sequence that emitted a stop id emits nothing more.
 __global__ __launch_bounds__(kBlock) void k_step_end(EndArgs a) {
   __shared__ uint64_t keys[kBlock];
   __shared__ uint32_t flags[kBlock];
@@ -755,6 +761,7 @@ __global__ __launch_bounds__(kBlock) void k_step_end(EndArgs a) {
   const bool select = selecting(c);
   if (select && c->mode == 0) {
     for (int b = 0; b < a.batch; ++b) {
+      if (!row_selects(c, b)) continue;
       uint64_t k = 0;
       uint32_t f = 0;
       for (int i = threadIdx.x; i < a.partials; i += blockDim.x) {
@@ -780,7 +787,9 @@ __global__ __launch_bounds__(kBlock) void k_step_end(EndArgs a) {
         } else {
           const uint32_t id = 0xffffffffu - static_cast<uint32_t>(keys[0] & 0xffffffffu);
           a.selected[b] = id;
-          if (c->generated < a.out_capacity) a.out_tokens[static_cast<uint64_t>(b) * a.out_capacity + c->generated] = id;
+          const uint32_t emitted = c->row_generated[b];
+          if (emitted < a.out_capacity) a.out_tokens[static_cast<uint64_t>(b) * a.out_capacity + emitted] = id;
+          c->row_generated[b] = emitted + 1;
           if (a.stop_mask[id]) c->finished_mask |= 1u << b;
         }
       }
@@ -1110,6 +1119,8 @@ struct dl_plan {
   hipGraphExec_t execs[2] = {nullptr, nullptr};
   uint64_t host_position = 0;                 // position the next enqueued step consumes
   bool eager = false;
+  dl::sampling::Settings sampling{0, 0, 1.0, 1.0};  // law recorded into the step graphs
+  dl::sampling::Workspace sampler{};                // per-sequence device sampler state
   // Workgroups per decode-step kernel (0: one tile per wavefront).
   // Defaults from the workgroup sweep on MI355X (grid-stride over tiles).
   uint32_t grid_override[8] = {256, 0, 0, 0, 256, 256, 512, 0};
@@ -1164,34 +1175,84 @@ void allow_lds(K kernel, size_t bytes) {
                   "hipFuncSetAttribute");
 }
 
+// Largest rows per launch of each GEMV kernel: the staged FP32 inputs of
+// a row group must fit the 160 KiB LDS (QKV stages D twice, for P = 16 and
+// P = 32; down stages F = 12288 for P = 32).  Wider batches launch several
+// row groups, each streaming the weights once.
+constexpr int kQkvRows = 4;
+constexpr int kDownRows = 2;
+constexpr int kWideRows = 8;
+
+size_t qkv_lds(int rows, int D) { return size_t(rows) * (dl::staged_floats(16, D) + dl::staged_floats(32, D)) * 4; }
+size_t p16_lds(int rows, int I) { return size_t(rows) * dl::staged_floats(16, I) * 4; }
+size_t p32_lds(int rows, int I) { return size_t(rows) * dl::staged_floats(32, I) * 4; }
+
+// Calls f(row0, rows) over row groups of templated sizes 8, 4, 2, 1 not
+// above `limit`.
+template <class F>
+void for_row_groups(uint32_t batch, int limit, F&& f) {
+  uint32_t row0 = 0;
+  for (int g = 8; g >= 1; g /= 2) {
+    if (g > limit) continue;
+    while (batch - row0 >= static_cast<uint32_t>(g)) {
+      f(row0, g);
+      row0 += g;
+    }
+  }
+}
+
 // Dynamic LDS above 64 KiB needs an explicit opt-in per kernel; this runs
 // before stream capture begins.
-template <int B>
-void prepare_kernels_b(dl_plan* p) {
+void prepare_kernels_all(dl_plan* p) {
   using namespace dl;
   const auto& c = p->model->cfg;
   const int D = c.hidden, QW = c.q_heads * c.head_dim, F = c.ffn;
-  allow_lds(k_qkv<B>, size_t(B) * (staged_floats(16, D) + staged_floats(32, D)) * sizeof(float));
-  allow_lds(k_residual<16, B>, size_t(B) * staged_floats(16, QW) * sizeof(float));
-  allow_lds(k_gateup<B>, size_t(B) * staged_floats(16, D) * sizeof(float));
-  allow_lds(k_residual<32, B>, size_t(B) * staged_floats(32, F) * sizeof(float));
-  allow_lds(k_lm_head<B>, size_t(B) * staged_floats(16, D) * sizeof(float));
+  allow_lds(k_qkv<1>, qkv_lds(1, D));
+  allow_lds(k_qkv<2>, qkv_lds(2, D));
+  allow_lds(k_qkv<4>, qkv_lds(4, D));
+  allow_lds(k_residual<16, 1>, p16_lds(1, QW));
+  allow_lds(k_residual<16, 2>, p16_lds(2, QW));
+  allow_lds(k_residual<16, 4>, p16_lds(4, QW));
+  allow_lds(k_residual<16, 8>, p16_lds(8, QW));
+  allow_lds(k_gateup<1>, p16_lds(1, D));
+  allow_lds(k_gateup<2>, p16_lds(2, D));
+  allow_lds(k_gateup<4>, p16_lds(4, D));
+  allow_lds(k_gateup<8>, p16_lds(8, D));
+  allow_lds(k_residual<32, 1>, p32_lds(1, F));
+  allow_lds(k_residual<32, 2>, p32_lds(2, F));
+  allow_lds(k_lm_head<1>, p16_lds(1, D));
+  allow_lds(k_lm_head<2>, p16_lds(2, D));
+  allow_lds(k_lm_head<4>, p16_lds(4, D));
+  allow_lds(k_lm_head<8>, p16_lds(8, D));
   allow_lds(k_attn_softmax, size_t(p->cap) * sizeof(float));
 }
 
-// Launches one decode-step kernel `which` of layer `l` with control `ctl`.
-template <int B>
+template <int G>
+void launch_qkv(dl_plan* p, hipStream_t s, const dl::QkvArgs& a) {
+  dl::k_qkv<G><<<p->grid_for(0, a.QW / 4 + a.KW), dl::kBlock, qkv_lds(G, a.D), s>>>(a);
+}
+template <int P, int G>
+void launch_residual(dl_plan* p, hipStream_t s, int which, const dl::ResidualArgs& a) {
+  const size_t lds = P == 16 ? p16_lds(G, a.I) : p32_lds(G, a.I);
+  dl::k_residual<P, G><<<p->grid_for(which, a.D / (64 / P)), dl::kBlock, lds, s>>>(a);
+}
+template <int G>
+void launch_gateup(dl_plan* p, hipStream_t s, const dl::GateUpArgs& a) {
+  dl::k_gateup<G><<<p->grid_for(5, a.F / 2), dl::kBlock, p16_lds(G, a.D), s>>>(a);
+}
+template <int G>
+void launch_head(dl_plan* p, hipStream_t s, const dl::HeadArgs& a) {
+  dl::k_lm_head<G><<<p->head_blocks, dl::kBlock, p16_lds(G, a.D), s>>>(a);
+}
+
+// Launches one decode-step kernel `which` of layer `l` with control `ctl`
+// over every sequence of the plan.
 void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Control* ctl) {
   using namespace dl;
   const dl_qwen3* m = p->model;
   const auto& c = m->cfg;
   const int D = c.hidden, QW = c.q_heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
-  const uint32_t V = c.vocab;
-  const size_t qkv_lds = size_t(B) * (staged_floats(16, D) + staged_floats(32, D)) * sizeof(float);
-  const size_t o_lds = size_t(B) * staged_floats(16, QW) * sizeof(float);
-  const size_t gu_lds = size_t(B) * staged_floats(16, D) * sizeof(float);
-  const size_t down_lds = size_t(B) * staged_floats(32, F) * sizeof(float);
-  const size_t soft_lds = size_t(p->cap) * sizeof(float);
+  const uint32_t V = c.vocab, B = p->batch;
   const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));
   uint16_t* kc = p->k_cache + uint64_t(l) * p->cache_layer_stride;
   uint16_t* vc = p->v_cache + uint64_t(l) * p->cache_layer_stride;
@@ -1199,84 +1260,104 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
               p->scores, p->probs, p->att, static_cast<int>(c.q_heads), static_cast<int>(c.kv_heads),
               static_cast<int>(p->cap), c.rms_eps, scale};
   switch (which) {
-    case 0: {
-      QkvArgs qa{ctl, p->h, m->input_norm[l], reinterpret_cast<const u32x4*>(m->qkv[l]), p->q_raw, p->k_raw, vc,
-                 p->cache_seq_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps};
-      k_qkv<B><<<p->grid_for(0, QW / 4 + KW), kBlock, qkv_lds, s>>>(qa);
+    case 0:
+      for_row_groups(B, kQkvRows, [&](uint32_t r0, int g) {
+        QkvArgs qa{ctl, p->h + uint64_t(r0) * D, m->input_norm[l], reinterpret_cast<const u32x4*>(m->qkv[l]),
+                   p->q_raw + uint64_t(r0) * QW, p->k_raw + uint64_t(r0) * KW, vc + r0 * p->cache_seq_stride,
+                   p->cache_seq_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps};
+        if (g == 4) launch_qkv<4>(p, s, qa);
+        else if (g == 2) launch_qkv<2>(p, s, qa);
+        else launch_qkv<1>(p, s, qa);
+      });
       break;
-    }
     case 1: k_attn_qk<<<dim3(c.kv_heads, p->cap / 64, B), kBlock, 0, s>>>(aa); break;
-    case 2: k_attn_softmax<<<dim3(c.q_heads, B), kBlock, soft_lds, s>>>(aa); break;
+    case 2: k_attn_softmax<<<dim3(c.q_heads, B), kBlock, size_t(p->cap) * sizeof(float), s>>>(aa); break;
     case 3: k_attn_pv<<<dim3(c.kv_heads * 16, B), 64, 0, s>>>(aa); break;
     case 8: k_attn_fused<<<dim3(c.q_heads, B), kBlock, 0, s>>>(aa); break;
-    case 4: {
-      ResidualArgs oa{ctl, p->att, reinterpret_cast<const u32x4*>(m->o[l]), p->h, nullptr, nullptr, QW, D,
-                      static_cast<int>(p->cap), static_cast<int>(l)};
-      k_residual<16, B><<<p->grid_for(4, D / 4), kBlock, o_lds, s>>>(oa);
+    case 4:
+      for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
+        ResidualArgs oa{ctl, p->att, reinterpret_cast<const u32x4*>(m->o[l]), p->h, nullptr, nullptr, QW, D,
+                        static_cast<int>(p->cap), static_cast<int>(l), static_cast<int>(r0)};
+        if (g == 8) launch_residual<16, 8>(p, s, 4, oa);
+        else if (g == 4) launch_residual<16, 4>(p, s, 4, oa);
+        else if (g == 2) launch_residual<16, 2>(p, s, 4, oa);
+        else launch_residual<16, 1>(p, s, 4, oa);
+      });
       break;
-    }
-    case 5: {
-      GateUpArgs ga{ctl, p->h, m->post_norm[l], reinterpret_cast<const u32x4*>(m->gu[l]), p->act, D, F, c.rms_eps};
-      k_gateup<B><<<p->grid_for(5, F / 2), kBlock, gu_lds, s>>>(ga);
+    case 5:
+      for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
+        GateUpArgs ga{ctl, p->h + uint64_t(r0) * D, m->post_norm[l], reinterpret_cast<const u32x4*>(m->gu[l]),
+                      p->act + uint64_t(r0) * F, D, F, c.rms_eps};
+        if (g == 8) launch_gateup<8>(p, s, ga);
+        else if (g == 4) launch_gateup<4>(p, s, ga);
+        else if (g == 2) launch_gateup<2>(p, s, ga);
+        else launch_gateup<1>(p, s, ga);
+      });
       break;
-    }
-    case 6: {
-      ResidualArgs da{ctl, p->act, reinterpret_cast<const u32x4*>(m->down[l]), p->h, p->capture, p->steer, F, D,
-                      static_cast<int>(p->cap), static_cast<int>(l)};
-      k_residual<32, B><<<p->grid_for(6, D / 2), kBlock, down_lds, s>>>(da);
+    case 6:
+      for_row_groups(B, kDownRows, [&](uint32_t r0, int g) {
+        ResidualArgs da{ctl, p->act, reinterpret_cast<const u32x4*>(m->down[l]), p->h, p->capture, p->steer, F, D,
+                        static_cast<int>(p->cap), static_cast<int>(l), static_cast<int>(r0)};
+        if (g == 2) launch_residual<32, 2>(p, s, 6, da);
+        else launch_residual<32, 1>(p, s, 6, da);
+      });
       break;
-    }
-    case 7: {
-      HeadArgs ha{ctl, p->h, m->final_norm, reinterpret_cast<const u32x4*>(m->lm_head), p->logits, p->partial_keys,
-                  p->partial_flags, D, V, c.rms_eps};
-      k_lm_head<B><<<p->head_blocks, kBlock, gu_lds, s>>>(ha);
+    case 7:
+      for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
+        HeadArgs ha{ctl, p->h, m->final_norm, reinterpret_cast<const u32x4*>(m->lm_head), p->logits,
+                    p->partial_keys, p->partial_flags, D, V, c.rms_eps, static_cast<int>(r0)};
+        if (g == 8) launch_head<8>(p, s, ha);
+        else if (g == 4) launch_head<4>(p, s, ha);
+        else if (g == 2) launch_head<2>(p, s, ha);
+        else launch_head<1>(p, s, ha);
+      });
       break;
-    }
     default: fail(DL_INVALID_ARGUMENT, "unknown step kernel");
   }
 }
 
 // Records one decode step.  `short_context` selects the fused attention
-// kernel (positions below kFusedKeys) instead of the three-kernel split.
-template <int B>
-void record_step_b(dl_plan* p, hipStream_t s, bool short_context) {
+// kernel (positions below kFusedKeys) instead of the three-kernel split;
+// categorical generation adds the device sampler after the LM head.
+void record_step_all(dl_plan* p, hipStream_t s, bool short_context) {
   using namespace dl;
   const dl_qwen3* m = p->model;
   const auto& c = m->cfg;
   BeginArgs begin{p->ctl, p->tokens, p->selected, p->h, m->lm_head, m->embedding, p->override_row,
                   p->cancel_device, static_cast<int>(c.hidden), c.vocab, c.tied_embeddings ? 1 : 0};
-  k_step_begin<<<B, kBlock, 0, s>>>(begin);
+  k_step_begin<<<p->batch, kBlock, 0, s>>>(begin);
   static const int kShort[] = {0, 8, 4, 5, 6};
   static const int kLong[] = {0, 1, 2, 3, 4, 5, 6};
   for (uint32_t l = 0; l < c.layers; ++l) {
     if (short_context)
-      for (int which : kShort) launch_step_kernel<B>(p, s, which, l, p->ctl);
+      for (int which : kShort) launch_step_kernel(p, s, which, l, p->ctl);
     else
-      for (int which : kLong) launch_step_kernel<B>(p, s, which, l, p->ctl);
+      for (int which : kLong) launch_step_kernel(p, s, which, l, p->ctl);
   }
-  launch_step_kernel<B>(p, s, 7, 0, p->ctl);
+  launch_step_kernel(p, s, 7, 0, p->ctl);
+  if (p->sampling.mode == 1) {
+    sampling::RowsArgs ra{};
+    ra.logits = p->logits;
+    ra.row_stride = c.vocab;
+    ra.n = c.vocab;
+    ra.rows = static_cast<int>(p->batch);
+    ra.settings = p->sampling;
+    ra.ws = p->sampler;
+    ra.loop_rng = 1;
+    ra.loop = sampling::LoopOutput{p->ctl, p->selected, p->out_tokens, p->cap, p->stop_mask};
+    sampling::launch_count(s, ra);
+    sampling::launch_select(s, ra);
+  }
   EndArgs ea{p->ctl, p->partial_keys, p->partial_flags, p->head_blocks, p->selected, p->out_tokens, p->cap,
-             p->stop_mask, p->cancel_device, B};
+             p->stop_mask, p->cancel_device, static_cast<int>(p->batch)};
   k_step_end<<<1, kBlock, 0, s>>>(ea);
 }
 
 }  // namespace
 
-void dl_plan::record_step(hipStream_t s, bool short_context) {
-  switch (batch) {
-    case 1: record_step_b<1>(this, s, short_context); break;
-    case 2: record_step_b<2>(this, s, short_context); break;
-    default: dl::fail(DL_LENGTH_ERROR, "batch sizes above 2 are not supported yet");
-  }
-}
+void dl_plan::record_step(hipStream_t s, bool short_context) { record_step_all(this, s, short_context); }
 
-void dl_plan::prepare_kernels() {
-  switch (batch) {
-    case 1: prepare_kernels_b<1>(this); break;
-    case 2: prepare_kernels_b<2>(this); break;
-    default: dl::fail(DL_LENGTH_ERROR, "batch sizes above 2 are not supported yet");
-  }
-}
+void dl_plan::prepare_kernels() { prepare_kernels_all(this); }
 
 void dl_plan::capture_step() {
   hipStream_t s = queue->stream;
@@ -1341,7 +1422,8 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
   return guard([&] {
     require(model && out, "null argument");
     dl::enter(queue);
-    require(batch >= 1 && batch <= 2, "batch must be 1 or 2", DL_LENGTH_ERROR);
+    require(batch >= 1 && batch <= static_cast<uint32_t>(dl::kMaxBatch), "batch must be in [1, 8]",
+            DL_LENGTH_ERROR);
     require(capacity >= 1 && capacity <= 32768, "capacity must be in [1, 32768]", DL_LENGTH_ERROR);
     auto p = std::make_unique<dl_plan>();
     p->model = model;
@@ -1378,6 +1460,10 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
     p->stop_mask = p->alloc<uint8_t>(V);
     p->override_row = p->alloc<uint16_t>(D);
     p->steer = p->alloc<float>(B * D);
+    p->sampler = dl::sampling::carve_workspace(p->alloc<uint8_t>(dl::sampling::workspace_bytes(batch, 0)),
+                                               static_cast<int>(batch), 0);
+    dl::sampling::launch_clear(queue->stream, p->sampler, static_cast<int>(batch));
+    dl::check_launch(queue, "sampler clear");
     dl::check_hip(hipMemsetAsync(p->stop_mask, 0, V, queue->stream), "stop mask clear");
     dl::check_hip(hipMemsetAsync(p->selected, 0, B * 4, queue->stream), "selection clear");
     dl::check_hip(hipMemsetAsync(p->tokens, 0, cap * 4, queue->stream), "token clear");
@@ -1415,10 +1501,7 @@ int dl_plan_launch_kernel(dl_plan* plan, uint32_t which, uint32_t first_layer, u
     require(first_layer < L, "layer out of range");
     for (uint32_t i = 0; i < count; ++i) {
       const uint32_t l = (first_layer + i) % L;
-      if (plan->batch == 1)
-        launch_step_kernel<1>(plan, plan->queue->stream, static_cast<int>(which), l, plan->bench_ctl);
-      else
-        launch_step_kernel<2>(plan, plan->queue->stream, static_cast<int>(which), l, plan->bench_ctl);
+      launch_step_kernel(plan, plan->queue->stream, static_cast<int>(which), l, plan->bench_ctl);
     }
     dl::check_launch(plan->queue, "step kernel");
   });
@@ -1679,23 +1762,38 @@ int dl_plan_prepare_generation(dl_plan* plan, const uint32_t* prompt, uint32_t p
     require(prompt_length > 0, "empty prompt");
     require(uint64_t(prompt_length) + max_new <= plan->capacity, "generation exceeds the cache capacity",
             DL_LENGTH_ERROR);
-    (void)seeds;
-    uint32_t mode = 0;
+    dl::sampling::Settings law{0, 0, 1.0, 1.0};
     if (sampling) {
-      require(sampling->mode == 0 || sampling->mode == 1, "invalid sampling mode");
-      require(std::isfinite(sampling->temperature) && sampling->temperature > 0, "invalid temperature");
-      require(std::isfinite(sampling->top_p) && sampling->top_p > 0 && sampling->top_p <= 1, "invalid top_p");
+      require(sampling->mode == 0 || sampling->mode == 1, "invalid sampling settings");
+      require(std::isfinite(sampling->temperature) && sampling->temperature > 0, "invalid sampling settings");
+      require(std::isfinite(sampling->top_p) && sampling->top_p > 0 && sampling->top_p <= 1,
+              "invalid sampling settings");
       if (sampling->mode == 0)
         require(sampling->temperature == 1 && sampling->top_k == 0 && sampling->top_p == 1,
-                "greedy selection takes temperature 1, top_k 0, top_p 1");
-      mode = sampling->mode;
+                "invalid sampling settings");
+      law = dl::sampling::Settings{sampling->mode, sampling->top_k, sampling->temperature, sampling->top_p};
     }
-    require(mode == 0, "categorical sampling inside the device loop is not available yet");
+    const uint32_t mode = law.mode;
     const uint32_t V = plan->model->cfg.vocab;
+    require(law.top_k <= V, "sampling shape or top-k mismatch");
     for (uint32_t i = 0; i < prompt_length; ++i) require(prompt[i] < V, "prompt id outside the vocabulary");
     for (uint32_t i = 0; i < stop_count; ++i) require(stop_ids && stop_ids[i] < V, "stop id outside the vocabulary");
     hipStream_t s = plan->queue->stream;
     dl::check_hip(hipStreamSynchronize(s), "generate wait");
+    const dl::sampling::Settings& had = plan->sampling;
+    const bool recapture = had.mode != law.mode || (law.mode == 1 && (had.top_k != law.top_k ||
+                                                                     had.temperature != law.temperature ||
+                                                                     had.top_p != law.top_p));
+    if (recapture) {
+      plan->sampling = law;
+      plan->capture_step();
+    }
+    if (mode == 1) {
+      dl::sampling::Seeds sd{};
+      for (uint32_t b = 0; b < plan->batch; ++b) sd.seed[b] = seeds ? seeds[b] : 0;
+      dl::sampling::launch_seed(s, plan->sampler.state, static_cast<int>(plan->batch), sd);
+      dl::check_launch(plan->queue, "sampler seed");
+    }
     *plan->cancel_host = 0;
     dl::check_hip(hipMemcpyAsync(plan->tokens, prompt, prompt_length * 4ull, hipMemcpyHostToDevice, s), "prompt");
     dl::check_hip(hipMemsetAsync(plan->stop_mask, 0, V, s), "stop mask");
@@ -1730,14 +1828,14 @@ int dl_plan_collect(dl_plan* plan, uint32_t* tokens, uint32_t max_new, dl_genera
     }
     dl::Control c;
     dl::check_hip(hipMemcpy(&c, plan->ctl, sizeof c, hipMemcpyDeviceToHost), "read control");
-    const uint32_t n = std::min(c.generated, max_new);
     for (uint32_t b = 0; b < plan->batch; ++b) {
+      const uint32_t n = std::min(c.row_generated[b], max_new);
       if (tokens && n)
         dl::check_hip(hipMemcpy(tokens + uint64_t(b) * max_new, plan->out_tokens + uint64_t(b) * plan->cap, n * 4ull,
                                 hipMemcpyDeviceToHost),
                       "read tokens");
       if (results) {
-        results[b].generated = c.generated;
+        results[b].generated = c.row_generated[b];
         results[b].reason = c.active ? 0u : c.reason;
         if (!c.active && c.reason == 0 && ((c.finished_mask >> b) & 1u)) results[b].reason = 1;
         results[b].status = c.status;

@@ -220,3 +220,96 @@ def test_batch_two_equals_batch_one(small_model):
     p2.generate(prompt, 8)
     t2, _ = p2.collect()
     assert t2[0].tolist() == t1[0].tolist() and t2[1].tolist() == t1[0].tolist()
+
+
+def test_batch_eight_equals_batch_one(small_model):
+    """Batch 8 runs QKV in two row groups of 4 and down in four groups of 2;
+    every sequence reproduces the batch-1 stream."""
+    from dolittle_amd.qwen3 import Plan
+    prompt = [9, 150000, 3, 77, 4096]
+    p1 = Plan(small_model, batch=1, capacity=32)
+    p1.generate(prompt, 10)
+    t1, _ = p1.collect()
+    p8 = Plan(small_model, batch=8, capacity=32)
+    p8.generate(prompt, 10)
+    t8, res = p8.collect()
+    for b in range(8):
+        assert t8[b].tolist() == t1[0].tolist(), b
+        assert res[b]["generated"] == 10
+
+
+def _categorical_run(plan, prompt, max_new, settings, seeds, override=None, stop_ids=None):
+    """Drives the loop one step at a time; returns the per-step logits rows
+    and the emitted tokens of every sequence."""
+    plan.prepare_generation(prompt, max_new, settings, seeds, stop_ids=stop_ids)
+    plan.decode_steps(len(prompt))
+    logits = []
+    for step in range(max_new):
+        logits.append([plan.logits(b) for b in range(plan.batch)])
+        if step + 1 < max_new:
+            plan.decode_steps(1)
+    plan.decode_steps(1)
+    tokens, results = plan.collect()
+    return logits, tokens, results
+
+
+def test_categorical_loop_ids_follow_the_law(small_model, oracle):
+    """Interpretation-sampling shape at reduced length: 8 sequences share a
+    prompt with one injected embedding row (BF16 N(0,1) x 40), top-p 0.95 at
+    T 1 with per-sequence MT19937-64 seeds.  Every sampled id equals the host
+    law applied to that step's device logits with the sequence's draws."""
+    from dolittle_amd.qwen3 import Plan, SamplingSettings
+    prompt = [int(t) for t in np.random.default_rng(21).integers(0, 151936, 24)]
+    plan = Plan(small_model, batch=8, capacity=64)
+    row = oracle.normal_bf16(4096, SEED + 5, 3000, 40.0)
+    plan.set_embedding_override(7, row, 0xFF)
+    seeds = [1000 + 17 * b for b in range(8)]
+    settings = SamplingSettings("categorical", 1.0, 0, 0.95)
+    max_new = 6
+    logits, tokens, results = _categorical_run(plan, prompt, max_new, settings, seeds)
+    for b in range(8):
+        assert results[b]["generated"] == max_new, results[b]
+        rng = oracle.MT19937_64(seeds[b])
+        for i in range(max_new):
+            status, want = oracle.categorical_bits(oracle.f32_from_bf16(logits[i][b]), 1, 1.0, 0, 0.95, rng())
+            assert status == 0
+            assert tokens[b][i] == want, (b, i)
+    assert len({tuple(t) for t in tokens.tolist()}) > 1
+
+
+def test_categorical_stop_id_ends_one_sequence(small_model, oracle):
+    from dolittle_amd.qwen3 import Plan, SamplingSettings
+    prompt = [5, 6, 7, 8, 9]
+    seeds = [3, 4, 5, 6]
+    settings = SamplingSettings("categorical", 1.0, 0, 0.95)
+    plan = Plan(small_model, batch=4, capacity=32)
+    plan.generate(prompt, 6, settings, seeds)
+    base, _ = plan.collect()
+    stop = int(base[2][1])
+    plan.generate(prompt, 6, settings, seeds, stop_ids=[stop])
+    tokens, results = plan.collect()
+    for b in range(4):
+        stream = base[b].tolist()
+        if stop in stream:
+            first = stream.index(stop)
+            assert results[b]["generated"] == first + 1 and results[b]["reason"] == "eos"
+            assert tokens[b][: first + 1].tolist() == stream[: first + 1]
+        else:
+            assert results[b]["generated"] == 6
+            assert tokens[b].tolist() == stream
+
+
+def test_categorical_then_greedy_recaptures(small_model):
+    """Switching the law re-records the step graphs; greedy afterwards equals
+    a fresh greedy plan."""
+    from dolittle_amd.qwen3 import Plan, SamplingSettings
+    prompt = [11, 12, 13]
+    plan = Plan(small_model, batch=2, capacity=32)
+    plan.generate(prompt, 4, SamplingSettings("categorical", 0.8, 10, 0.9), [1, 2])
+    plan.collect()
+    plan.generate(prompt, 4)
+    t, _ = plan.collect()
+    fresh = Plan(small_model, batch=2, capacity=32)
+    fresh.generate(prompt, 4)
+    t2, _ = fresh.collect()
+    assert t.tolist() == t2.tolist()
