@@ -266,6 +266,13 @@ void orc_add(const uint16_t* a, const uint16_t* b, uint16_t* y, size_t n) {
   for (size_t i = 0; i < n; ++i) y[i] = or_bf16_from_f32(or_f32_from_bf16(a[i]) + or_f32_from_bf16(b[i]));
 }
 
+/* All-position steering of one row (the config-4 variant of
+ * src/kernels/cuda/steering.cu:69-159 with a fixed FP32 vector): after the
+ * block's second residual addition, h <- BF16(FP32(h) + v). */
+void orc_steer(uint16_t* h, const float* v, size_t n) {
+  for (size_t i = 0; i < n; ++i) h[i] = or_bf16_from_f32(or_f32_from_bf16(h[i]) + v[i]);
+}
+
 void orc_silu_multiply(const uint16_t* gate, const uint16_t* up, uint16_t* y, size_t n) {
   for (size_t i = 0; i < n; ++i) {
     const float a = or_f32_from_bf16(gate[i]);

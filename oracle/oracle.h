@@ -61,6 +61,9 @@ void orc_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint
 float orc_attention_scale(size_t width);
 /* elementwise.cu:2-18,62-87 */
 void orc_add(const uint16_t* a, const uint16_t* b, uint16_t* y, size_t n);
+/* h <- BF16(FP32(h) + v): all-position residual steering (steering.cu:69-159,
+ * the fixed-vector variant). */
+void orc_steer(uint16_t* h, const float* v, size_t n);
 void orc_silu_multiply(const uint16_t* gate, const uint16_t* up, uint16_t* y, size_t n);
 /* embedding.cu:60-80 */
 void orc_embedding(const uint32_t* tokens, const uint16_t* table, uint16_t* y, size_t rows,

@@ -66,6 +66,7 @@ def lib():
         L.orc_attention_scale.argtypes = [sz]
         L.orc_attention_scale.restype = C.c_float
         L.orc_add.argtypes = [u16p, u16p, u16p, sz]
+        L.orc_steer.argtypes = [u16p, f32p, sz]
         for name in ("orc_silu_multiply", "ors_silu_multiply"):
             getattr(L, name).argtypes = [u16p, u16p, u16p, sz]
         L.orc_embedding.argtypes = [u32p, u16p, u16p, sz, sz]
@@ -192,6 +193,11 @@ def add(a, b):
     y = np.empty(len(a), dtype=np.uint16)
     lib().orc_add(np.ascontiguousarray(a, np.uint16), np.ascontiguousarray(b, np.uint16), y, len(a))
     return y
+
+
+def steer(h: np.ndarray, vector: np.ndarray) -> None:
+    """In place: h <- BF16(FP32(h) + vector)."""
+    lib().orc_steer(h, np.ascontiguousarray(vector, np.float32), len(h))
 
 
 def silu_multiply(g, u, serial=False):

@@ -313,3 +313,49 @@ def test_categorical_then_greedy_recaptures(small_model):
     fresh.generate(prompt, 4)
     t2, _ = fresh.collect()
     assert t.tolist() == t2.tolist()
+
+
+def test_capture_and_steering_batch_two(small_model, oracle):
+    """Config-4 semantics at two blocks: both sequences capture block 0's
+    output at every consumed position; sequence 1 is steered there by a unit
+    FP32 vector times 8 (h <- BF16(FP32(h) + v)) and the capture sees the
+    steered row.  Streams, captures and final logits equal the oracle."""
+    from dolittle_amd.qwen3 import Plan
+    w = oracle_weights(oracle, small_model)
+    d = w.dims
+    layer = 0
+    rng = np.random.default_rng(44)
+    v = rng.standard_normal(d.hidden).astype(np.float32)
+    v = (v / np.float32(np.linalg.norm(v.astype(np.float64)))).astype(np.float32) * np.float32(8.0)
+    prompt = [int(t) for t in rng.integers(0, 151936, 10)]
+    max_new = 6
+    plan = Plan(small_model, batch=2, capacity=64)
+    plan.set_capture(layer)
+    plan.set_steering(1, layer, v)
+    plan.generate(prompt, max_new)
+    tokens, results = plan.collect()
+    consumed = len(prompt) + max_new
+    for seq in (0, 1):
+        assert results[seq]["generated"] == max_new
+        kw = d.kv_heads * d.head_dim
+        k = [np.zeros(64 * kw, np.uint16) for _ in w.blocks]
+        vv = [np.zeros(64 * kw, np.uint16) for _ in w.blocks]
+        stream, captures, logits = list(prompt), [], None
+        for pos in range(consumed):
+            h = w.embedding.reshape(d.vocab, d.hidden)[stream[pos]].copy()
+            for l in range(len(w.blocks)):
+                oracle.block_forward(w, l, h, 1, pos, k[l], vv[l])
+                if l == layer:
+                    if seq == 1:
+                        oracle.steer(h, v)
+                    captures.append(h.copy())
+            if pos >= len(prompt) - 1 and len(stream) < consumed:
+                logits = oracle.logits(w, h)
+                status, nxt = oracle.greedy(logits)
+                assert status == 0
+                stream.append(nxt)
+        assert tokens[seq].tolist() == stream[len(prompt):], seq
+        got = plan.read_capture(seq, 0, consumed)
+        assert np.array_equal(got, np.stack(captures)), seq
+        assert np.array_equal(plan.logits(seq), logits), seq
+    assert tokens[0].tolist() != tokens[1].tolist()

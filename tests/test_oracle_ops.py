@@ -214,3 +214,15 @@ def test_attention_scale(oracle):
     assert oracle.lib().orc_attention_scale(128) == np.float32(1.0 / np.sqrt(128.0))
 
 
+
+
+def test_steer_closed_forms(oracle):
+    """h <- BF16(FP32(h) + v): zero vector is the identity, exact sums stay
+    exact, and ties round to even once (1 + 2^-8 -> 1, 1 + 3*2^-8 -> 1 + 2^-6)."""
+    h0 = oracle.normal_bf16(4096, 3, 5, 1.0)
+    h = h0.copy()
+    oracle.steer(h, np.zeros(4096, np.float32))
+    assert np.array_equal(h, h0)
+    h = oracle.bf16_from_f32(np.array([1.0, 1.0, 1.0, -2.0], np.float32))
+    oracle.steer(h, np.array([2.0**-8, 3 * 2.0**-8, 0.5, 0.25], np.float32))
+    assert oracle.f32_from_bf16(h).tolist() == [1.0, 1.0 + 2.0**-6, 1.5, -1.75]
