@@ -224,8 +224,11 @@ int dl_qwen3_read_tensor(dl_qwen3* model, dl_queue* queue, int role, uint32_t la
 int dl_qwen3_resident_bytes(dl_qwen3* model, uint64_t* bytes);
 
 /* ---------------------------------------------------------------- the plan */
-/* A cached forward plan for `batch` independent sequences sharing the
- * model, each with a contiguous KV cache of `capacity` positions. */
+/* A cached forward plan for `batch` (1..8) independent sequences sharing
+ * the model, each with a contiguous KV cache of `capacity` (<= 32768)
+ * positions.  Every sequence's results are independent of the batch size
+ * (transformer-execution.md:180-190): each row keeps the single-row
+ * reduction trees. */
 typedef struct dl_plan dl_plan;
 
 typedef struct dl_sampling {
