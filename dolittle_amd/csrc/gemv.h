@@ -54,6 +54,39 @@ __device__ __forceinline__ void stage_put(float* xs, int I, int b, int i, float 
   xs[b * P * stride + (i % P) * stride + i / P] = v;
 }
 
+// Stages BF16 rows [b0, b0 + R) of x (width I) into the P-partial layout.
+// Each thread moves 16-byte chunks; all of a thread's loads are issued
+// before any is consumed.  Requires I % 8 == 0 and I <= 8 * 8 * blockDim.x.
+template <int P>
+__device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ x, int I, int rows, float* xs) {
+  constexpr int kMaxChunks = 8;
+  const int chunks = I / 8;
+  for (int b = 0; b < rows; ++b) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(x + static_cast<uint64_t>(b) * I);
+    u32x4 v[kMaxChunks];
+#pragma unroll
+    for (int j = 0; j < kMaxChunks; ++j) {
+      const int c = threadIdx.x + j * blockDim.x;
+      v[j] = src[c < chunks ? c : 0];
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxChunks; ++j) {
+      const int c = threadIdx.x + j * blockDim.x;
+      if (c < chunks) {
+        const int i = c * 8;
+        stage_put<P>(xs, I, b, i + 0, dl_bf16_lo(v[j].x));
+        stage_put<P>(xs, I, b, i + 1, dl_bf16_hi(v[j].x));
+        stage_put<P>(xs, I, b, i + 2, dl_bf16_lo(v[j].y));
+        stage_put<P>(xs, I, b, i + 3, dl_bf16_hi(v[j].y));
+        stage_put<P>(xs, I, b, i + 4, dl_bf16_lo(v[j].z));
+        stage_put<P>(xs, I, b, i + 5, dl_bf16_hi(v[j].z));
+        stage_put<P>(xs, I, b, i + 6, dl_bf16_lo(v[j].w));
+        stage_put<P>(xs, I, b, i + 7, dl_bf16_hi(v[j].w));
+      }
+    }
+  }
+}
+
 // One wavefront computes RW output rows for B input rows.  `tile` points at
 // the tile's first 16-byte chunk; on return lane (row, 0) of each P-lane
 // segment holds the merged FP32 sum of that row for every b.
@@ -164,13 +197,14 @@ __device__ __forceinline__ void norm_stage_rows(const uint16_t* __restrict__ h, 
   float hv[R][kNormMaxK];
   float gv[kNormMaxK];
   if (tid < 128) {
+    // Unconditional loads (indices past D clamp to a valid feature and are
+    // never used) so that all of them are in flight at once.
 #pragma unroll
     for (int k = 0; k < kNormMaxK; ++k) {
-      if (k < K) {
-        gv[k] = dl_bf16_to_f32(gain[tid + 128 * k]);
+      const int kk = k < K ? k : 0;
+      gv[k] = dl_bf16_to_f32(gain[tid + 128 * kk]);
 #pragma unroll
-        for (int b = 0; b < R; ++b) hv[b][k] = dl_bf16_to_f32(h[(b0 + b) * D + tid + 128 * k]);
-      }
+      for (int b = 0; b < R; ++b) hv[b][k] = dl_bf16_to_f32(h[(b0 + b) * D + tid + 128 * kk]);
     }
 #pragma unroll
     for (int b = 0; b < R; ++b) {

@@ -569,10 +569,7 @@ __global__ __launch_bounds__(kBlock) void k_residual(ResidualArgs a) {
   const int tiles = a.D / RW;
   const int S = a.I / (8 * P);
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
-  for (int b = 0; b < B; ++b) {
-    const uint16_t* xb = a.x + static_cast<uint64_t>(a.row0 + b) * a.I;
-    for (int i = threadIdx.x; i < a.I; i += blockDim.x) stage_put<P>(xs, a.I, b, i, dl_bf16_to_f32(xb[i]));
-  }
+  stage_rows<P>(a.x + static_cast<uint64_t>(a.row0) * a.I, a.I, B, xs);
   __syncthreads();
   const bool steer = a.steer != nullptr && a.layer == a.ctl->steer_layer;
   const bool capture = a.capture != nullptr && a.layer == a.ctl->capture_layer;
@@ -939,6 +936,10 @@ void validate_config(const dl_qwen3_config& c) {
   require(c.head_dim == 128, "this backend requires head_dim 128");
   require(c.q_heads == 4 * c.kv_heads, "this backend requires 4 query heads per KV head");
   require(c.hidden % 256 == 0 && c.ffn % 256 == 0, "hidden and ffn widths must be multiples of 256");
+  // Register-resident RMSNorm prologue (128 lanes x 32 features) and
+  // 16-byte staging (8 chunks per lane of 256) bound the widths.
+  require(c.hidden <= 4096 && c.ffn <= 16384 && uint64_t(c.q_heads) * c.head_dim <= 16384,
+          "hidden must be at most 4096 and ffn / query widths at most 16384");
   require(uint64_t(c.q_heads) * c.head_dim % 256 == 0, "query width must be a multiple of 256");
   require(c.vocab % 4 == 0, "vocabulary must be a multiple of 4");
   require(c.rms_eps > 0.0f, "rms epsilon must be positive");
