@@ -177,41 +177,37 @@ __device__ __forceinline__ float block_rms_inverse(const uint16_t* __restrict__ 
 }
 
 // Stages round(round(h_b * inverse_b) * gain) for R <= 2 rows (starting at
-// row b0) of width D into the staged LDS layouts for P = 16 (xs16, when
-// non-null) and P = 32 (xs32, when non-null), computing inverse_b with the
-// reference tree (normalization.cu:134-186) in the same pass: thread i < 128
-// keeps features i + 128k of every row in registers, sums their squares in
+// row b0) of width D = 128 * kNormK into the staged LDS layouts for P = 16
+// (when S16) and P = 32 (when S32), computing inverse_b with the reference
+// tree (normalization.cu:134-186) in the same pass: thread i < 128 keeps
+// features i + 128k of every row in registers, sums their squares in
 // ascending k (component i), combines groups of four left to right, and the
 // lanes below 32 R reduce the 32 lane totals with shuffle-down offsets 1..16.
-// One global round trip, two barriers.  Requires D % 128 == 0 and
-// D <= 128 * kNormMaxK.
-constexpr int kNormMaxK = 32;
+// The width and the layouts are compile-time so that loads, sums and LDS
+// stores are straight-line code with every load in flight at once.
+constexpr int kNormK = 32;
+constexpr int kNormWidth = 128 * kNormK;
 
-template <int R>
+template <int R, bool S16, bool S32>
 __device__ __forceinline__ void norm_stage_rows(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
-                                                int D, float eps, float* xs16, float* xs32, float* scratch,
-                                                int b0) {
+                                                float eps, float* xs16, float* xs32, float* scratch, int b0) {
   static_assert(R <= 2, "one wavefront reduces at most two rows");
+  constexpr int D = kNormWidth;
   const int tid = threadIdx.x;
-  const int K = D / 128;
-  float hv[R][kNormMaxK];
-  float gv[kNormMaxK];
+  float hv[R][kNormK];
+  float gv[kNormK];
   if (tid < 128) {
-    // Unconditional loads (indices past D clamp to a valid feature and are
-    // never used) so that all of them are in flight at once.
 #pragma unroll
-    for (int k = 0; k < kNormMaxK; ++k) {
-      const int kk = k < K ? k : 0;
-      gv[k] = dl_bf16_to_f32(gain[tid + 128 * kk]);
+    for (int k = 0; k < kNormK; ++k) {
+      gv[k] = dl_bf16_to_f32(gain[tid + 128 * k]);
 #pragma unroll
-      for (int b = 0; b < R; ++b) hv[b][k] = dl_bf16_to_f32(h[(b0 + b) * D + tid + 128 * kk]);
+      for (int b = 0; b < R; ++b) hv[b][k] = dl_bf16_to_f32(h[(b0 + b) * D + tid + 128 * k]);
     }
 #pragma unroll
     for (int b = 0; b < R; ++b) {
       float comp = 0.0f;
 #pragma unroll
-      for (int k = 0; k < kNormMaxK; ++k)
-        if (k < K) comp = comp + hv[b][k] * hv[b][k];
+      for (int k = 0; k < kNormK; ++k) comp = comp + hv[b][k] * hv[b][k];
       const float second = __shfl_down(comp, 1, 4);
       const float third = __shfl_down(comp, 2, 4);
       const float fourth = __shfl_down(comp, 3, 4);
@@ -232,30 +228,28 @@ __device__ __forceinline__ void norm_stage_rows(const uint16_t* __restrict__ h, 
     for (int b = 0; b < R; ++b) {
       const float inverse = scratch[b * 40 + 32];
 #pragma unroll
-      for (int k = 0; k < kNormMaxK; ++k) {
-        if (k < K) {
-          const float n = dl_round_bf16(dl_round_bf16(hv[b][k] * inverse) * gv[k]);
-          const int col = tid + 128 * k;
-          if (xs16) stage_put<16>(xs16, D, b0 + b, col, n);
-          if (xs32) stage_put<32>(xs32, D, b0 + b, col, n);
-        }
+      for (int k = 0; k < kNormK; ++k) {
+        const float n = dl_round_bf16(dl_round_bf16(hv[b][k] * inverse) * gv[k]);
+        const int col = tid + 128 * k;
+        if constexpr (S16) stage_put<16>(xs16, D, b0 + b, col, n);
+        if constexpr (S32) stage_put<32>(xs32, D, b0 + b, col, n);
       }
     }
   }
 }
 
 // norm_stage_rows over B rows, two at a time (scratch is reused between
-// pairs behind a barrier).
-template <int B>
+// pairs behind a barrier).  Rows have width kNormWidth.
+template <int B, bool S16, bool S32>
 __device__ __forceinline__ void norm_stage(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
-                                           int D, float eps, float* xs16, float* xs32, float* scratch) {
+                                           float eps, float* xs16, float* xs32, float* scratch) {
 #pragma unroll
   for (int b0 = 0; b0 < B; b0 += 2) {
     if (b0) __syncthreads();
     if (B - b0 >= 2)
-      norm_stage_rows<2>(h, gain, D, eps, xs16, xs32, scratch, b0);
+      norm_stage_rows<2, S16, S32>(h, gain, eps, xs16, xs32, scratch, b0);
     else
-      norm_stage_rows<1>(h, gain, D, eps, xs16, xs32, scratch, b0);
+      norm_stage_rows<1, S16, S32>(h, gain, eps, xs16, xs32, scratch, b0);
   }
 }
 

@@ -221,7 +221,7 @@ __global__ __launch_bounds__(kBlock) void k_qkv(QkvArgs a) {
   const int S16 = a.D / 128, S32 = a.D / 256;
   const uint64_t q_chunks = static_cast<uint64_t>(S16) * 64;
   const uint64_t k_chunks = static_cast<uint64_t>(S32) * 64;
-  norm_stage<B>(a.h, a.norm, a.D, a.eps, xs16, xs32, scratch);
+  norm_stage<B, true, true>(a.h, a.norm, a.eps, xs16, xs32, scratch);
   __syncthreads();
   (void)S16;
   for (int tile = blockIdx.x * kWaves + wave; tile < total; tile += gridDim.x * kWaves) {
@@ -612,7 +612,7 @@ __global__ __launch_bounds__(kBlock) void k_gateup(GateUpArgs a) {
   const int tiles = a.F / 2;
   const int S = a.D / 128;
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
-  norm_stage<B>(a.h, a.norm, a.D, a.eps, xs, nullptr, scratch);
+  norm_stage<B, true, false>(a.h, a.norm, a.eps, xs, nullptr, scratch);
   __syncthreads();
   (void)S;
   for (int tile = blockIdx.x * kWaves + wave; tile < tiles; tile += gridDim.x * kWaves) {
@@ -685,7 +685,7 @@ __global__ __launch_bounds__(kBlock) void k_lm_head(HeadArgs a) {
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
   const int first = blockIdx.x * kWaves + wave;
   (void)S;
-  norm_stage<B>(a.h + static_cast<uint64_t>(a.row0) * a.D, a.norm, a.D, a.eps, xs, nullptr, scratch);
+  norm_stage<B, true, false>(a.h + static_cast<uint64_t>(a.row0) * a.D, a.norm, a.eps, xs, nullptr, scratch);
   __syncthreads();
   uint64_t best[B];
   uint32_t flags[B];
@@ -938,8 +938,9 @@ void validate_config(const dl_qwen3_config& c) {
   require(c.hidden % 256 == 0 && c.ffn % 256 == 0, "hidden and ffn widths must be multiples of 256");
   // Register-resident RMSNorm prologue (128 lanes x 32 features) and
   // 16-byte staging (8 chunks per lane of 256) bound the widths.
-  require(c.hidden <= 4096 && c.ffn <= 16384 && uint64_t(c.q_heads) * c.head_dim <= 16384,
-          "hidden must be at most 4096 and ffn / query widths at most 16384");
+  require(c.hidden == static_cast<uint32_t>(dl::kNormWidth) && c.ffn <= 16384 &&
+              uint64_t(c.q_heads) * c.head_dim <= 16384,
+          "hidden must be 4096 and ffn / query widths at most 16384");
   require(uint64_t(c.q_heads) * c.head_dim % 256 == 0, "query width must be a multiple of 256");
   require(c.vocab % 4 == 0, "vocabulary must be a multiple of 4");
   require(c.rms_eps > 0.0f, "rms epsilon must be positive");
