@@ -170,8 +170,10 @@ def main() -> int:
     # launch streams distinct weights.
     _lib.call("dl_plan_bench_prepare", plan.handle)
     kernels = {}
-    names = {0: "k_qkv", 4: "k_residual<16> (O)", 5: "k_gateup", 6: "k_residual<32> (down)", 7: "k_lm_head"}
-    for which in (5, 7, 0, 6, 4):
+    names = {0: "k_qkv", 4: "k_residual<16> (O)", 5: "k_gateup", 6: "k_residual<32> (down)", 7: "k_lm_head",
+             8: "k_attn_fused"}
+    attn_keys = args.prompt + args.warmup + args.steps
+    for which in (5, 7, 0, 6, 4, 8):
         iters = args.kernel_iters if which != 7 else max(8, args.kernel_iters // 8)
         _lib.call("dl_plan_launch_kernel", plan.handle, which, 0, 2)  # warm
         ea, eb = Event(device), Event(device)
@@ -180,10 +182,27 @@ def main() -> int:
         _lib.call("dl_plan_launch_kernel", plan.handle, which, 0, iters)
         eb.record(queue)
         us = ea.elapsed_ms(eb) * 1e3 / iters
+        if which == 8:
+            # K and V rows of one layer at the bench position (the four query
+            # heads of a group share them through L2).
+            kv = attn_keys * 2 * cfg.kv_heads * cfg.head_dim * 2
+            kernels[names[which]] = {"us": round(us, 2), "keys": attn_keys, "kv_bytes": kv}
+            log(f"  {names[which]:<24} {us:8.2f} us  ({attn_keys} keys)")
+            continue
         gbs = kernel_bytes(cfg, which) / (us * 1e-6) / 1e9
         kernels[names[which]] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
         log(f"  {names[which]:<24} {us:8.2f} us  {gbs:7.0f} GB/s  {gbs / HBM_PEAK_GBS:.1%}")
     dominant = kernels["k_gateup"]
+
+    # Replay cost of the step graph with the loop stopped: every kernel
+    # exits at entry, leaving launch and dispatch overhead.
+    queue.drain()
+    ea, eb = Event(device), Event(device)
+    ea.record(queue)
+    plan.decode_steps(20)
+    eb.record(queue)
+    idle_us = ea.elapsed_ms(eb) * 1e3 / 20
+    log(f"  idle step graph           {idle_us:8.2f} us")
 
     if args.copy_calibration_mib:
         n = args.copy_calibration_mib << 20
@@ -233,6 +252,7 @@ def main() -> int:
             "avg_launch_us": dominant["us"],
         },
         "kernels": kernels,
+        "idle_step_graph_us": round(idle_us, 2),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

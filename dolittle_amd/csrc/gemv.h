@@ -57,8 +57,9 @@ __device__ __forceinline__ void stage_put(float* xs, int I, int b, int i, float 
 // Stages BF16 rows [b0, b0 + R) of x (width I) into the P-partial layout.
 // Each thread moves 16-byte chunks; all of a thread's loads are issued
 // before any is consumed.  Requires I % 8 == 0 and I <= 8 * 8 * blockDim.x.
-template <int P>
-__device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ x, int I, int rows, float* xs) {
+template <int P, class Issue>
+__device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ x, int I, int rows, float* xs,
+                                           Issue&& issue) {
   constexpr int kMaxChunks = 8;
   const int chunks = I / 8;
   for (int b = 0; b < rows; ++b) {
@@ -68,6 +69,13 @@ __device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ x, int I
     for (int j = 0; j < kMaxChunks; ++j) {
       const int c = threadIdx.x + j * blockDim.x;
       v[j] = src[c < chunks ? c : 0];
+    }
+    if (b == 0) {
+      // The caller's first weight batch follows this row's loads (loads
+      // retire in order) and overlaps the staging below.
+      __builtin_amdgcn_sched_barrier(0);
+      issue();
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int j = 0; j < kMaxChunks; ++j) {
@@ -120,15 +128,35 @@ __device__ __forceinline__ void chain_step(const u32x4 w, const float* __restric
   }
 }
 
+// First kBatch 16-byte chunks of a tile, issued ahead of a prologue.
+struct FirstBatch {
+  u32x4 w[kBatch];
+  bool valid;
+};
+
+__device__ __forceinline__ void issue_first(const u32x4* __restrict__ tile, int lane, FirstBatch& f) {
+  const u32x4* src = tile + lane;
+#pragma unroll
+  for (int j = 0; j < kBatch; ++j) f.w[j] = load_stream(src + j * 64);
+  f.valid = true;
+}
+
 template <int P, int B>
 __device__ __forceinline__ void chain_tile(const u32x4* __restrict__ tile, const float* __restrict__ xs,
-                                           int I, int lane, float (&acc)[B]) {
+                                           int I, int lane, float (&acc)[B], FirstBatch* first = nullptr) {
   const int L = I / P, S = L / 8, stride = L + kXsPad, bstride = P * stride;
   const float* xt = xs + (lane % P) * stride;
   const u32x4* src = tile + lane;
 #pragma unroll
   for (int b = 0; b < B; ++b) acc[b] = 0.0f;
   int s0 = 0;
+  if (first && first->valid && S >= kBatch) {
+    // The tile's first batch was issued before the kernel's prologue.
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) chain_step<B>(first->w[j], xt, bstride, j, acc);
+    first->valid = false;
+    s0 = kBatch;
+  }
   for (; s0 + kBatch <= S; s0 += kBatch) {
     u32x4 w[kBatch];
 #pragma unroll
@@ -188,9 +216,10 @@ __device__ __forceinline__ float block_rms_inverse(const uint16_t* __restrict__ 
 constexpr int kNormK = 32;
 constexpr int kNormWidth = 128 * kNormK;
 
-template <int R, bool S16, bool S32>
+template <int R, bool S16, bool S32, class Issue>
 __device__ __forceinline__ void norm_stage_rows(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
-                                                float eps, float* xs16, float* xs32, float* scratch, int b0) {
+                                                float eps, float* xs16, float* xs32, float* scratch, int b0,
+                                                Issue&& issue) {
   static_assert(R <= 2, "one wavefront reduces at most two rows");
   constexpr int D = kNormWidth;
   const int tid = threadIdx.x;
@@ -203,6 +232,13 @@ __device__ __forceinline__ void norm_stage_rows(const uint16_t* __restrict__ h, 
 #pragma unroll
       for (int b = 0; b < R; ++b) hv[b][k] = dl_bf16_to_f32(h[(b0 + b) * D + tid + 128 * k]);
     }
+  }
+  // Loads retire in order: the caller's own traffic (the first weight batch)
+  // goes after the row loads, and its latency overlaps the math below.
+  __builtin_amdgcn_sched_barrier(0);
+  issue();
+  __builtin_amdgcn_sched_barrier(0);
+  if (tid < 128) {
 #pragma unroll
     for (int b = 0; b < R; ++b) {
       float comp = 0.0f;
@@ -240,16 +276,24 @@ __device__ __forceinline__ void norm_stage_rows(const uint16_t* __restrict__ h, 
 
 // norm_stage_rows over B rows, two at a time (scratch is reused between
 // pairs behind a barrier).  Rows have width kNormWidth.
-template <int B, bool S16, bool S32>
+template <int B, bool S16, bool S32, class Issue>
 __device__ __forceinline__ void norm_stage(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
-                                           float eps, float* xs16, float* xs32, float* scratch) {
+                                           float eps, float* xs16, float* xs32, float* scratch, Issue&& issue) {
+  auto none = [] {};
 #pragma unroll
   for (int b0 = 0; b0 < B; b0 += 2) {
     if (b0) __syncthreads();
-    if (B - b0 >= 2)
-      norm_stage_rows<2, S16, S32>(h, gain, eps, xs16, xs32, scratch, b0);
-    else
-      norm_stage_rows<1, S16, S32>(h, gain, eps, xs16, xs32, scratch, b0);
+    if (B - b0 >= 2) {
+      if (b0 == 0)
+        norm_stage_rows<2, S16, S32>(h, gain, eps, xs16, xs32, scratch, b0, issue);
+      else
+        norm_stage_rows<2, S16, S32>(h, gain, eps, xs16, xs32, scratch, b0, none);
+    } else {
+      if (b0 == 0)
+        norm_stage_rows<1, S16, S32>(h, gain, eps, xs16, xs32, scratch, b0, issue);
+      else
+        norm_stage_rows<1, S16, S32>(h, gain, eps, xs16, xs32, scratch, b0, none);
+    }
   }
 }
 

@@ -221,26 +221,36 @@ __global__ __launch_bounds__(kBlock) void k_qkv(QkvArgs a) {
   const int S16 = a.D / 128, S32 = a.D / 256;
   const uint64_t q_chunks = static_cast<uint64_t>(S16) * 64;
   const uint64_t k_chunks = static_cast<uint64_t>(S32) * 64;
-  norm_stage<B, true, true>(a.h, a.norm, a.eps, xs16, xs32, scratch);
-  __syncthreads();
   (void)S16;
-  for (int tile = blockIdx.x * kWaves + wave; tile < total; tile += gridDim.x * kWaves) {
+  auto tile_src = [&](int tile) -> const u32x4* {
+    if (tile < q_tiles) return a.w + tile * q_chunks;
+    int kt = tile - q_tiles;
+    const bool is_v = kt >= k_tiles;
+    if (is_v) kt -= k_tiles;
+    return a.w + q_tiles * q_chunks + (is_v ? k_tiles : 0) * k_chunks + kt * k_chunks;
+  };
+  const int first = blockIdx.x * kWaves + wave;
+  FirstBatch fb{};
+  norm_stage<B, true, true>(a.h, a.norm, a.eps, xs16, xs32, scratch, [&] {
+    if (first < total) issue_first(tile_src(first), lane, fb);
+  });
+  __syncthreads();
+  for (int tile = first; tile < total; tile += gridDim.x * kWaves) {
     const bool is_q = tile < q_tiles;
     int kt = tile - q_tiles;
     const bool is_v = !is_q && kt >= k_tiles;
     if (is_v) kt -= k_tiles;
-    const u32x4* src = is_q ? a.w + tile * q_chunks
-                            : a.w + q_tiles * q_chunks + (is_v ? k_tiles : 0) * k_chunks + kt * k_chunks;
+    const u32x4* src = tile_src(tile);
     float acc[B];
     if (is_q) {
-      chain_tile<16, B>(src, xs16, a.D, lane, acc);
+      chain_tile<16, B>(src, xs16, a.D, lane, acc, &fb);
       if (lane % 16 == 0) {
         const int row = tile * 4 + lane / 16;
 #pragma unroll
         for (int b = 0; b < B; ++b) a.q_out[b * a.QW + row] = bf16_bits(acc[b]);
       }
     } else {
-      chain_tile<32, B>(src, xs32, a.D, lane, acc);
+      chain_tile<32, B>(src, xs32, a.D, lane, acc, &fb);
       if (lane % 32 == 0) {
         const int row = kt * 2 + lane / 32;
 #pragma unroll
@@ -275,12 +285,21 @@ struct AttnArgs {
 
 // Per-head RMSNorm (width 128: lane t, component c holds feature t+32c;
 // normalization.cu:82-132) followed by RoPE (rotary.cu:84-126) for one head,
-// computed by one wavefront; lane i owns the RoPE pair (i, i+64).
-__device__ __forceinline__ void head_norm_rope(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gain,
-                                               const float* __restrict__ rope_pos, int lane, float eps,
-                                               float* out) {
-  const float xa = dl_bf16_to_f32(x[lane]);
-  const float xb = dl_bf16_to_f32(x[lane + 64]);
+// computed by one wavefront; lane i owns the RoPE pair (i, i+64).  The
+// operands are loaded first (head_load) so callers can issue them ahead of
+// other memory traffic.
+struct HeadOperands {
+  float xa, xb, ga, gb, cosine, sine;
+};
+
+__device__ __forceinline__ HeadOperands head_load(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gain,
+                                                  const float* __restrict__ rope_pos, int lane) {
+  return HeadOperands{dl_bf16_to_f32(x[lane]), dl_bf16_to_f32(x[lane + 64]), dl_bf16_to_f32(gain[lane]),
+                      dl_bf16_to_f32(gain[lane + 64]), rope_pos[2 * lane], rope_pos[2 * lane + 1]};
+}
+
+__device__ __forceinline__ void head_norm_rope(const HeadOperands& o, int lane, float eps, float* out) {
+  const float xa = o.xa, xb = o.xb;
   const float xa_hi = __shfl(xa, (lane + 32) & 63);
   const float xb_hi = __shfl(xb, (lane + 32) & 63);
   float s = ((xa * xa + xa_hi * xa_hi) + xb * xb) + xb_hi * xb_hi;
@@ -288,11 +307,16 @@ __device__ __forceinline__ void head_norm_rope(const uint16_t* __restrict__ x, c
   for (int off = 1; off < 32; off *= 2) s = s + __shfl_down(s, off, 32);
   const float total = __shfl(s, 0);
   const float inverse = inverse_sqrt(total * (1.0f / 128.0f) + eps);
-  const float na = rbf(rbf(xa * inverse) * dl_bf16_to_f32(gain[lane]));
-  const float nb = rbf(rbf(xb * inverse) * dl_bf16_to_f32(gain[lane + 64]));
-  const float cosine = rope_pos[2 * lane], sine = rope_pos[2 * lane + 1];
-  out[lane] = rbf(rbf(na * cosine) - rbf(nb * sine));
-  out[lane + 64] = rbf(rbf(nb * cosine) + rbf(na * sine));
+  const float na = rbf(rbf(xa * inverse) * o.ga);
+  const float nb = rbf(rbf(xb * inverse) * o.gb);
+  out[lane] = rbf(rbf(na * o.cosine) - rbf(nb * o.sine));
+  out[lane + 64] = rbf(rbf(nb * o.cosine) + rbf(na * o.sine));
+}
+
+__device__ __forceinline__ void head_norm_rope(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gain,
+                                               const float* __restrict__ rope_pos, int lane, float eps,
+                                               float* out) {
+  head_norm_rope(head_load(x, gain, rope_pos, lane), lane, eps, out);
 }
 
 // Grid (kv head, 64-key tile, sequence); block 256 = 4 waves, one per query
@@ -441,12 +465,17 @@ __global__ __launch_bounds__(64) void k_attn_pv(AttnArgs a) {
 // scores stay in LDS, the max and the 32-partial denominator follow, and
 // the two PV key ranges run as 2 x 128 threads over the transposed V rows.
 constexpr int kFusedKeys = 1024;
+constexpr int kAttnThreads = 512;
+constexpr int kAttnKeysPerPass = kAttnThreads / 8;
+constexpr int kAttnKeyPasses = 8;     // key rows issued at kernel entry: 512 keys
+constexpr int kAttnValueBlocks = 16;  // 8-key V blocks per PV chain issued at entry
 
-__global__ __launch_bounds__(kBlock) void k_attn_fused(AttnArgs a) {
+__global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
   __shared__ float qs[kHeadDim];
   __shared__ float ks[kHeadDim];
-  __shared__ float sc[kFusedKeys];
-  __shared__ float red[kBlock];
+  __shared__ __align__(16) float sc[kFusedKeys];
+  __shared__ float red[kAttnThreads];
+  __shared__ float wave_max[kAttnThreads / 64];
   __shared__ float denominator_shared;
   if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
@@ -458,57 +487,101 @@ __global__ __launch_bounds__(kBlock) void k_attn_fused(AttnArgs a) {
   const float* rope_pos = a.rope + pos * kHeadDim;
   const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHeadDim, kw = static_cast<uint64_t>(a.kv_heads) * kHeadDim;
   uint16_t* kc = a.k_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g) * a.cap * kHeadDim;
-  if (wave == 0)
-    head_norm_rope(a.q_raw + b * qw + static_cast<uint64_t>(h) * kHeadDim, a.q_norm, rope_pos, lane, a.eps, qs);
+
+  // Cached K rows and V blocks do not depend on this token: issue the first
+  // kAttnKeyPasses passes of key rows and kAttnValueBlocks 8-key blocks of
+  // each PV chain before the head norms, so their latency overlaps them.
+  // This token's q/k head operands go first: loads retire in order, so
+  // anything issued before them would delay the head norms.
+  HeadOperands head{};
+  if (wave == 0) head = head_load(a.q_raw + b * qw + static_cast<uint64_t>(h) * kHeadDim, a.q_norm, rope_pos, lane);
+  if (wave == 1) head = head_load(a.k_raw + b * kw + static_cast<uint64_t>(g) * kHeadDim, a.k_norm, rope_pos, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  const int kg = tid / 8, l = tid % 8;
+  u32x4 kpre[kAttnKeyPasses][2];
+#pragma unroll
+  for (int p = 0; p < kAttnKeyPasses; ++p) {
+    const int j = min(p * kAttnKeysPerPass + kg, count - 1);
+    const u32x4* src = reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(j) * kHeadDim + 16 * l);
+    kpre[p][0] = src[0];
+    kpre[p][1] = src[1];
+  }
+  // PV chains: thread f + 128 * half (half 0: keys [0, split), half 1:
+  // [split, count)), one chain per lane; waves 0-1 and 2-3 hold the halves.
+  const int split = (count - 1) / 2 + 1;
+  const int f = tid % kHeadDim, half = (tid / kHeadDim) & 1;
+  const bool chain = tid < 2 * kHeadDim;
+  const int begin = half ? split : 0, end = half ? count : split;
+  const int first_block = begin & ~7;
+  const uint16_t* v = a.v_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g * kHeadDim + f) * a.cap;
+  u32x4 vpre[kAttnValueBlocks];
+  if (chain) {
+#pragma unroll
+    for (int i = 0; i < kAttnValueBlocks; ++i) {
+      const int jb = min(first_block + 8 * i, a.cap - 8);
+      vpre[i] = *reinterpret_cast<const u32x4*>(v + jb);
+    }
+  }
+
+  __builtin_amdgcn_sched_barrier(0);
+  if (wave == 0) head_norm_rope(head, lane, a.eps, qs);
   if (wave == 1) {
-    head_norm_rope(a.k_raw + b * kw + static_cast<uint64_t>(g) * kHeadDim, a.k_norm, rope_pos, lane, a.eps, ks);
+    head_norm_rope(head, lane, a.eps, ks);
     if (h % group == 0) {
       kc[pos * kHeadDim + lane] = bf16_bits(ks[lane]);
       kc[pos * kHeadDim + lane + 64] = bf16_bits(ks[lane + 64]);
     }
   }
   __syncthreads();
+
+  // Scores: 8 lanes per key, each an FMA chain over 16 contiguous features,
+  // merged at offsets 4, 2, 1 (attention.cu:231-300).  The row at `pos` is
+  // the freshly rotated key (its cache row may not be written yet).
   {
-    const int kg = tid / 8, l = tid % 8;
     float q[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) q[i] = qs[16 * l + i];
-    for (int base = 0; base < count; base += kBlock / 8) {
-      const int j = base + kg;
-      float acc = 0.0f;
-      if (j < count) {
-        float kf[16];
-        if (static_cast<uint64_t>(j) == pos) {
+    auto score = [&](int j, const u32x4 w0, const u32x4 w1) {
+      float kf[16];
+      if (static_cast<uint64_t>(j) == pos) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) kf[i] = ks[16 * l + i];
-        } else {
-          const u32x4* src = reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(j) * kHeadDim + 16 * l);
-          const u32x4 w0 = src[0], w1 = src[1];
-          kf[0] = dl_bf16_lo(w0.x); kf[1] = dl_bf16_hi(w0.x); kf[2] = dl_bf16_lo(w0.y); kf[3] = dl_bf16_hi(w0.y);
-          kf[4] = dl_bf16_lo(w0.z); kf[5] = dl_bf16_hi(w0.z); kf[6] = dl_bf16_lo(w0.w); kf[7] = dl_bf16_hi(w0.w);
-          kf[8] = dl_bf16_lo(w1.x); kf[9] = dl_bf16_hi(w1.x); kf[10] = dl_bf16_lo(w1.y); kf[11] = dl_bf16_hi(w1.y);
-          kf[12] = dl_bf16_lo(w1.z); kf[13] = dl_bf16_hi(w1.z); kf[14] = dl_bf16_lo(w1.w); kf[15] = dl_bf16_hi(w1.w);
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc = fma_rn(q[i], kf[i], acc);
+        for (int i = 0; i < 16; ++i) kf[i] = ks[16 * l + i];
+      } else {
+        kf[0] = dl_bf16_lo(w0.x); kf[1] = dl_bf16_hi(w0.x); kf[2] = dl_bf16_lo(w0.y); kf[3] = dl_bf16_hi(w0.y);
+        kf[4] = dl_bf16_lo(w0.z); kf[5] = dl_bf16_hi(w0.z); kf[6] = dl_bf16_lo(w0.w); kf[7] = dl_bf16_hi(w0.w);
+        kf[8] = dl_bf16_lo(w1.x); kf[9] = dl_bf16_hi(w1.x); kf[10] = dl_bf16_lo(w1.y); kf[11] = dl_bf16_hi(w1.y);
+        kf[12] = dl_bf16_lo(w1.z); kf[13] = dl_bf16_hi(w1.z); kf[14] = dl_bf16_lo(w1.w); kf[15] = dl_bf16_hi(w1.w);
       }
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc = fma_rn(q[i], kf[i], acc);
 #pragma unroll
       for (int off = 4; off; off >>= 1) acc = acc + __shfl_down(acc, off, 8);
       if (l == 0 && j < count) sc[j] = acc * a.scale;
+    };
+#pragma unroll
+    for (int p = 0; p < kAttnKeyPasses; ++p)
+      if (p * kAttnKeysPerPass < count) score(p * kAttnKeysPerPass + kg, kpre[p][0], kpre[p][1]);
+    for (int base = kAttnKeyPasses * kAttnKeysPerPass; base < count; base += kAttnKeysPerPass) {
+      const int j = min(base + kg, count - 1);
+      const u32x4* src = reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(j) * kHeadDim + 16 * l);
+      score(base + kg, src[0], src[1]);
     }
   }
   __syncthreads();
-  float m = sc[0];
-  for (int j = tid; j < count; j += kBlock) m = fmaxf(m, sc[j]);
-  red[tid] = m;
+
+  // Softmax: exact maximum, e = exp(s - m), 32 strided partial sums merged
+  // 16..1, p = e / l (attention.cu:301-360).
+  float m = -INFINITY;
+  for (int j = tid; j < count; j += kAttnThreads) m = fmaxf(m, sc[j]);
+#pragma unroll
+  for (int off = 32; off; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if (lane == 0) wave_max[wave] = m;
   __syncthreads();
-  for (int off = kBlock / 2; off; off >>= 1) {
-    if (tid < off) red[tid] = fmaxf(red[tid], red[tid + off]);
-    __syncthreads();
-  }
-  m = red[0];
-  __syncthreads();
-  for (int j = tid; j < count; j += kBlock) sc[j] = dl_expf(sc[j] - m);
+  m = wave_max[0];
+#pragma unroll
+  for (int w = 1; w < kAttnThreads / 64; ++w) m = fmaxf(m, wave_max[w]);
+  for (int j = tid; j < count; j += kAttnThreads) sc[j] = dl_expf(sc[j] - m);
   __syncthreads();
   if (tid < 32) {
     float partial = 0.0f;
@@ -518,29 +591,61 @@ __global__ __launch_bounds__(kBlock) void k_attn_fused(AttnArgs a) {
     if (tid == 0) denominator_shared = partial;
   }
   __syncthreads();
-  const float l = denominator_shared;
-  for (int j = tid; j < count; j += kBlock) sc[j] = sc[j] / l;
+  const float denominator = denominator_shared;
+  for (int j = tid; j < count; j += kAttnThreads) sc[j] = sc[j] / denominator;
   __syncthreads();
-  const int split = (count - 1) / 2 + 1;
-  const int f = tid % kHeadDim, half = tid / kHeadDim;
-  const uint16_t* v = a.v_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g * kHeadDim + f) * a.cap;
-  const int begin = half ? split : 0, end = half ? count : split;
-  float acc = 0.0f;
-  int j = begin;
-  for (; j < end && (j & 7); ++j) acc = fma_rn(sc[j], dl_bf16_to_f32(v[j]), acc);
-  for (; j + 8 <= end; j += 8) {
-    const u32x4 vv = *reinterpret_cast<const u32x4*>(v + j);
-    acc = fma_rn(sc[j], dl_bf16_lo(vv.x), acc);
-    acc = fma_rn(sc[j + 1], dl_bf16_hi(vv.x), acc);
-    acc = fma_rn(sc[j + 2], dl_bf16_lo(vv.y), acc);
-    acc = fma_rn(sc[j + 3], dl_bf16_hi(vv.y), acc);
-    acc = fma_rn(sc[j + 4], dl_bf16_lo(vv.z), acc);
-    acc = fma_rn(sc[j + 5], dl_bf16_hi(vv.z), acc);
-    acc = fma_rn(sc[j + 6], dl_bf16_lo(vv.w), acc);
-    acc = fma_rn(sc[j + 7], dl_bf16_hi(vv.w), acc);
+
+  // PV: two ascending FMA chains over [0, split) and [split, count), read
+  // as aligned 8-key blocks.  Only the chain's first and last blocks can be
+  // partial (keys outside the chain are skipped there); full blocks read
+  // their eight probabilities as two float4s.
+  if (chain) {
+    float acc = 0.0f;
+    auto partial = [&](int jb, const u32x4 vv) {
+      const float x[8] = {dl_bf16_lo(vv.x), dl_bf16_hi(vv.x), dl_bf16_lo(vv.y), dl_bf16_hi(vv.y),
+                          dl_bf16_lo(vv.z), dl_bf16_hi(vv.z), dl_bf16_lo(vv.w), dl_bf16_hi(vv.w)};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (jb + e >= begin && jb + e < end) acc = fma_rn(sc[jb + e], x[e], acc);
+    };
+    auto full = [&](int jb, const u32x4 vv) {
+      const float4 p0 = *reinterpret_cast<const float4*>(sc + jb);
+      const float4 p1 = *reinterpret_cast<const float4*>(sc + jb + 4);
+      acc = fma_rn(p0.x, dl_bf16_lo(vv.x), acc);
+      acc = fma_rn(p0.y, dl_bf16_hi(vv.x), acc);
+      acc = fma_rn(p0.z, dl_bf16_lo(vv.y), acc);
+      acc = fma_rn(p0.w, dl_bf16_hi(vv.y), acc);
+      acc = fma_rn(p1.x, dl_bf16_lo(vv.z), acc);
+      acc = fma_rn(p1.y, dl_bf16_hi(vv.z), acc);
+      acc = fma_rn(p1.z, dl_bf16_lo(vv.w), acc);
+      acc = fma_rn(p1.w, dl_bf16_hi(vv.w), acc);
+    };
+    auto consume = [&](int jb, const u32x4 vv) {
+      if (jb >= begin && jb + 8 <= end)
+        full(jb, vv);
+      else
+        partial(jb, vv);
+    };
+#pragma unroll
+    for (int i = 0; i < kAttnValueBlocks; ++i) {
+      const int jb = first_block + 8 * i;
+      if (jb < end) consume(jb, vpre[i]);
+    }
+    for (int jb0 = first_block + 8 * kAttnValueBlocks; jb0 < end; jb0 += 8 * kAttnValueBlocks) {
+      u32x4 vb[kAttnValueBlocks];
+#pragma unroll
+      for (int i = 0; i < kAttnValueBlocks; ++i) {
+        const int jb = min(jb0 + 8 * i, a.cap - 8);
+        vb[i] = *reinterpret_cast<const u32x4*>(v + jb);
+      }
+#pragma unroll
+      for (int i = 0; i < kAttnValueBlocks; ++i) {
+        const int jb = jb0 + 8 * i;
+        if (jb < end) consume(jb, vb[i]);
+      }
+    }
+    red[tid] = acc;
   }
-  for (; j < end; ++j) acc = fma_rn(sc[j], dl_bf16_to_f32(v[j]), acc);
-  red[tid] = acc;
   __syncthreads();
   if (tid < kHeadDim) a.att[static_cast<uint64_t>(b) * qw + h * kHeadDim + tid] = bf16_bits(red[tid] + red[tid + kHeadDim]);
 }
@@ -569,14 +674,18 @@ __global__ __launch_bounds__(kBlock) void k_residual(ResidualArgs a) {
   const int tiles = a.D / RW;
   const int S = a.I / (8 * P);
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
-  stage_rows<P>(a.x + static_cast<uint64_t>(a.row0) * a.I, a.I, B, xs);
+  const int first = blockIdx.x * kWaves + wave;
+  FirstBatch fb{};
+  stage_rows<P>(a.x + static_cast<uint64_t>(a.row0) * a.I, a.I, B, xs, [&] {
+    if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
+  });
   __syncthreads();
   const bool steer = a.steer != nullptr && a.layer == a.ctl->steer_layer;
   const bool capture = a.capture != nullptr && a.layer == a.ctl->capture_layer;
   const uint32_t steer_mask = a.ctl->steer_mask;
-  for (int tile = blockIdx.x * kWaves + wave; tile < tiles; tile += gridDim.x * kWaves) {
+  for (int tile = first; tile < tiles; tile += gridDim.x * kWaves) {
     float acc[B];
-    chain_tile<P, B>(a.w + tile * chunks, xs, a.I, lane, acc);
+    chain_tile<P, B>(a.w + tile * chunks, xs, a.I, lane, acc, &fb);
     if (lane % P == 0) {
       const int row = tile * RW + lane / P;
 #pragma unroll
@@ -612,12 +721,16 @@ __global__ __launch_bounds__(kBlock) void k_gateup(GateUpArgs a) {
   const int tiles = a.F / 2;
   const int S = a.D / 128;
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
-  norm_stage<B, true, false>(a.h, a.norm, a.eps, xs, nullptr, scratch);
+  const int first = blockIdx.x * kWaves + wave;
+  FirstBatch fb{};
+  norm_stage<B, true, false>(a.h, a.norm, a.eps, xs, nullptr, scratch, [&] {
+    if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
+  });
   __syncthreads();
   (void)S;
-  for (int tile = blockIdx.x * kWaves + wave; tile < tiles; tile += gridDim.x * kWaves) {
+  for (int tile = first; tile < tiles; tile += gridDim.x * kWaves) {
     float acc[B];
-    chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc);
+    chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc, &fb);
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       const float up = __shfl_down(acc[b], 32, 64);
@@ -685,7 +798,10 @@ __global__ __launch_bounds__(kBlock) void k_lm_head(HeadArgs a) {
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
   const int first = blockIdx.x * kWaves + wave;
   (void)S;
-  norm_stage<B, true, false>(a.h + static_cast<uint64_t>(a.row0) * a.D, a.norm, a.eps, xs, nullptr, scratch);
+  FirstBatch fb{};
+  norm_stage<B, true, false>(a.h + static_cast<uint64_t>(a.row0) * a.D, a.norm, a.eps, xs, nullptr, scratch, [&] {
+    if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
+  });
   __syncthreads();
   uint64_t best[B];
   uint32_t flags[B];
@@ -696,7 +812,7 @@ __global__ __launch_bounds__(kBlock) void k_lm_head(HeadArgs a) {
   }
   for (int tile = first; tile < tiles; tile += gridDim.x * kWaves) {
     float acc[B];
-    chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc);
+    chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc, &fb);
     if (lane % 16 == 0) {
       const uint32_t row = static_cast<uint32_t>(tile * 4 + lane / 16);
 #pragma unroll
@@ -1125,7 +1241,7 @@ struct dl_plan {
   dl::sampling::Workspace sampler{};                // per-sequence device sampler state
   // Workgroups per decode-step kernel (0: one tile per wavefront).
   // Defaults from the workgroup sweep on MI355X (grid-stride over tiles).
-  uint32_t grid_override[8] = {256, 0, 0, 0, 256, 256, 512, 0};
+  uint32_t grid_override[8] = {512, 0, 0, 0, 256, 768, 512, 0};
   unsigned grid_for(int which, uint64_t tiles) const {
     const uint64_t full = dl::ceil_div(tiles, 4);
     const uint64_t g = grid_override[which] ? grid_override[which] : full;
@@ -1275,7 +1391,7 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
     case 1: k_attn_qk<<<dim3(c.kv_heads, p->cap / 64, B), kBlock, 0, s>>>(aa); break;
     case 2: k_attn_softmax<<<dim3(c.q_heads, B), kBlock, size_t(p->cap) * sizeof(float), s>>>(aa); break;
     case 3: k_attn_pv<<<dim3(c.kv_heads * 16, B), 64, 0, s>>>(aa); break;
-    case 8: k_attn_fused<<<dim3(c.q_heads, B), kBlock, 0, s>>>(aa); break;
+    case 8: k_attn_fused<<<dim3(c.q_heads, B), kAttnThreads, 0, s>>>(aa); break;
     case 4:
       for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
         ResidualArgs oa{ctl, p->att, reinterpret_cast<const u32x4*>(m->o[l]), p->h, nullptr, nullptr, QW, D,
