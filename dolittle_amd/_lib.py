@@ -115,6 +115,12 @@ SIGNATURES = {
     "dl_plan_launch_kernel": [vp, u32, u32, u32],
     "dl_plan_set_grid": [vp, u32, u32],
     "dl_plan_request_stop": [vp],
+    "dl_plan_prefill": [vp, u32p, u32],
+    "dl_plan_read_prefill_hidden": [vp, u64, u64, u16p],
+    "dl_plan_read_prefill_buffer": [vp, u32, u64, u64, u16p],
+    "dl_prefill_projection": [vp, vp, vp, vp, vp, u64, u64, u64],
+    "dl_prefill_attention": [vp, vp, vp, vp, vp, u64, u64, u64, u64, u64],
+    "dl_prefill_gate_up": [vp, vp, vp, vp, vp, u64, u64, u64],
     "dl_sampler_required_bytes": [u64, C.POINTER(u64)],
     "dl_sampler_create": [vp, vp, u64, cint, u64, vpp],
     "dl_sampler_destroy": [vp],

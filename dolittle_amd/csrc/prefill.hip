@@ -1,0 +1,537 @@
+// MFMA prefill kernels for gfx950: projections as BF16 GEMMs over the packed
+// resident weights, exact row norms written in the GEMM's permuted input
+// order, per-head QK norm + RoPE, and causal flash attention with FP32
+// softmax.  The probabilities enter the PV product at full FP32 precision:
+// each p is split exactly into three BF16 parts (p = hi + mid + lo) and
+// every part runs through a BF16 MFMA accumulating in FP32, so no
+// probability is rounded to BF16 (numerical-portability.md:8-10).
+#include <algorithm>
+#include <cmath>
+
+#include "dl_device.h"
+#include "dl_internal.h"
+#include "heads.h"
+#include "prefill.h"
+
+namespace dl::prefill {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kTK = 64;              // GEMM positions per K chunk
+constexpr int kRow = kTK + 8;        // LDS row stride in BF16 (144 B staggers banks)
+constexpr int kGemmThreads = 256;    // 4 waves, each a 64 x 64 quarter of the tile
+constexpr int kHd = 128;
+constexpr int kKeyTile = 64;
+constexpr int kQRow = kHd + 8;       // Q/K tile row stride in BF16 (272 B)
+constexpr int kVRow = kKeyTile + 8;  // V^T tile row stride in BF16
+constexpr int kPRow = kKeyTile + 4;  // probability tile row stride in floats
+constexpr int kAttnThreads = 256;    // 4 waves x 16 query rows
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Element offset of packed position `kpos` of weight row n (P partials,
+// K inputs): the row's 8P positions of block kpos / 8P are contiguous.
+__device__ __forceinline__ uint64_t packed_offset(int n, int P, int K, int kpos) {
+  const int RW = 64 / P, S = K / (8 * P), block = 8 * P;
+  const int s = kpos / block, local = kpos % block;
+  return (static_cast<uint64_t>((n / RW) * S + s) * 64 + (n % RW) * P) * 8 + local;
+}
+
+// SiluMultiply on BF16-rounded operands (elementwise.cu:62-87).
+__device__ __forceinline__ float silu_times(float a, float b) {
+  const float e = dl_expf(a >= 0.0f ? -a : a);
+  const float sigmoid = a >= 0.0f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+  return dl_round_bf16(a * sigmoid) * b;
+}
+
+// ------------------------------------------------------------------ GEMM
+// C[M x N] = A[M x K] W[N x K]^T over permuted positions.  Tile 128 x 128,
+// K chunks of 64 positions double-buffered through LDS, 32x32x16 BF16 MFMA.
+template <int EPI>
+__global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
+  __shared__ __align__(16) uint16_t As[2][kTileM * kRow];
+  __shared__ __align__(16) uint16_t Bs[2][kTileN * kRow];
+  const int n0 = blockIdx.x * kTileN, m0 = blockIdx.y * kTileM;
+  const bool alt = n0 >= a.n_split;
+  const uint16_t* A = alt ? a.a_alt : a.a;
+  const uint16_t* W = alt ? a.w_alt : a.w;
+  const int P = alt ? a.P_alt : a.P;
+  const int nb = alt ? n0 - a.n_split : n0;
+  const int K = a.K, chunks = K / kTK;
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // Each thread moves four 16-byte pieces of each operand tile per chunk:
+  // piece i = tid + 256 j covers row i / 8, positions 8 (i % 8) .. + 7.
+  const u32x4* a_src[4];
+  const uint16_t* w_row[4];
+  int lds_off[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = tid + kGemmThreads * j, row = i >> 3, col = (i & 7) * 8;
+    a_src[j] = reinterpret_cast<const u32x4*>(A + static_cast<uint64_t>(m0 + row) * K + col);
+    w_row[j] = W + packed_offset(nb + row, P, K, 0) + col;
+    lds_off[j] = row * kRow + col;
+  }
+  const int RW = 64 / P, block = 8 * P;
+  (void)RW;
+  // Packed position kpos of a row: block kpos / 8P sits 8P * RW ... apart.
+  const uint64_t block_stride = static_cast<uint64_t>(64) * 8;  // elements between consecutive blocks of a row
+  auto w_at = [&](int j, int kpos) {
+    return reinterpret_cast<const u32x4*>(w_row[j] + (kpos / block) * block_stride + (kpos % block));
+  };
+  u32x4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
+#define DL_GEMM_LOAD(c)                                      \
+  do {                                                       \
+    const int kp = (c) * kTK;                                \
+    ra0 = a_src[0][kp / 8]; ra1 = a_src[1][kp / 8];          \
+    ra2 = a_src[2][kp / 8]; ra3 = a_src[3][kp / 8];          \
+    rb0 = *w_at(0, kp); rb1 = *w_at(1, kp);                  \
+    rb2 = *w_at(2, kp); rb3 = *w_at(3, kp);                  \
+  } while (0)
+#define DL_GEMM_STORE(buf)                                                       \
+  do {                                                                           \
+    *reinterpret_cast<u32x4*>(&As[buf][lds_off[0]]) = ra0;                       \
+    *reinterpret_cast<u32x4*>(&As[buf][lds_off[1]]) = ra1;                       \
+    *reinterpret_cast<u32x4*>(&As[buf][lds_off[2]]) = ra2;                       \
+    *reinterpret_cast<u32x4*>(&As[buf][lds_off[3]]) = ra3;                       \
+    *reinterpret_cast<u32x4*>(&Bs[buf][lds_off[0]]) = rb0;                       \
+    *reinterpret_cast<u32x4*>(&Bs[buf][lds_off[1]]) = rb1;                       \
+    *reinterpret_cast<u32x4*>(&Bs[buf][lds_off[2]]) = rb2;                       \
+    *reinterpret_cast<u32x4*>(&Bs[buf][lds_off[3]]) = rb3;                       \
+  } while (0)
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  DL_GEMM_LOAD(0);
+  DL_GEMM_STORE(0);
+  __syncthreads();
+  for (int c = 0; c < chunks; ++c) {
+    const int buf = c & 1;
+    if (c + 1 < chunks) DL_GEMM_LOAD(c + 1);
+#pragma unroll
+    for (int ks = 0; ks < kTK / 16; ++ks) {
+      bf16x8 af[2], bw[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(
+            &As[buf][(64 * wm + 32 * i + lane % 32) * kRow + ks * 16 + 8 * (lane / 32)]));
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bw[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(
+            &Bs[buf][(64 * wn + 32 * j + lane % 32) * kRow + ks * 16 + 8 * (lane / 32)]));
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bw[j], acc[i][j], 0, 0, 0);
+    }
+    if (c + 1 < chunks) DL_GEMM_STORE(buf ^ 1);
+    __syncthreads();
+  }
+#undef DL_GEMM_LOAD
+#undef DL_GEMM_STORE
+
+  // Lane layout of a 32x32 accumulator: column lane % 32, row
+  // 8 (r / 4) + 4 (lane / 32) + r % 4 for r < 16.
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + 64 * wn + 32 * j + lane % 32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 64 * wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+        const float v = acc[i][j][r];
+        if constexpr (EPI == kStore) {
+          a.out[static_cast<uint64_t>(m) * a.N + n] = dl_f32_to_bf16(v);
+        } else if constexpr (EPI == kResidual) {
+          uint16_t* o = a.out + static_cast<uint64_t>(m) * a.N + n;
+          *o = dl_f32_to_bf16(dl_bf16_to_f32(*o) + dl_round_bf16(v));
+        } else if constexpr (EPI == kStoreQkv) {
+          if (n < a.q_width) {
+            a.out[static_cast<uint64_t>(m) * a.q_width + n] = dl_f32_to_bf16(v);
+          } else if (n < a.q_width + a.kv_width) {
+            a.out2[static_cast<uint64_t>(m) * a.kv_width + (n - a.q_width)] = dl_f32_to_bf16(v);
+          } else if (m < a.m_valid) {
+            a.v_cache[static_cast<uint64_t>(n - a.q_width - a.kv_width) * a.cap + a.first_position + m] =
+                dl_f32_to_bf16(v);
+          }
+        } else {
+          // Columns 4j..4j+3 hold gate rows 2j, 2j+1 and up rows 2j, 2j+1;
+          // the up value of column n sits two lanes up.
+          const float up = __shfl(v, (lane + 2) & 63);
+          if ((n & 3) < 2) {
+            const uint32_t f = 2 * (n / 4) + (n & 3);
+            a.out[static_cast<uint64_t>(m) * (a.N / 2) + permuted(f, 32)] =
+                dl_f32_to_bf16(silu_times(dl_round_bf16(v), dl_round_bf16(up)));
+          }
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- row norms
+// One workgroup per row; thread i < 128 owns features i + 128k, the
+// reference tree of normalization.cu:134-186, output in P16 / P32 order.
+constexpr int kNormK = 32;
+
+__global__ __launch_bounds__(256) void k_norm(NormArgs a) {
+  __shared__ float scratch[40];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const uint16_t* h = a.h + static_cast<uint64_t>(row) * a.width;
+  const int K = a.width / 128;
+  float hv[kNormK], gv[kNormK];
+  if (tid < 128) {
+#pragma unroll
+    for (int k = 0; k < kNormK; ++k) {
+      const int kk = k < K ? k : 0;
+      hv[k] = dl_bf16_to_f32(h[tid + 128 * kk]);
+      gv[k] = dl_bf16_to_f32(a.gain[tid + 128 * kk]);
+    }
+    float comp = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormK; ++k)
+      if (k < K) comp = comp + hv[k] * hv[k];
+    const float second = __shfl_down(comp, 1, 4);
+    const float third = __shfl_down(comp, 2, 4);
+    const float fourth = __shfl_down(comp, 3, 4);
+    if ((tid & 3) == 0) scratch[tid >> 2] = ((comp + second) + third) + fourth;
+  }
+  __syncthreads();
+  if (tid < 32) {
+    float s = scratch[tid];
+#pragma unroll
+    for (int off = 1; off < 32; off *= 2) s = s + __shfl_down(s, off, 32);
+    if (tid == 0) scratch[32] = inverse_sqrt(s * (1.0f / static_cast<float>(a.width)) + a.eps);
+  }
+  __syncthreads();
+  if (tid < 128) {
+    const float inverse = scratch[32];
+    uint16_t* x16 = a.x16 + static_cast<uint64_t>(row) * a.width;
+    uint16_t* x32 = a.x32 ? a.x32 + static_cast<uint64_t>(row) * a.width : nullptr;
+#pragma unroll
+    for (int k = 0; k < kNormK; ++k) {
+      if (k < K) {
+        const uint32_t col = tid + 128 * k;
+        const uint16_t n = dl_f32_to_bf16(dl_round_bf16(hv[k] * inverse) * gv[k]);
+        x16[permuted(col, 16)] = n;
+        if (x32) x32[permuted(col, 32)] = n;
+      }
+    }
+  }
+}
+
+// --------------------------------------------------- head norms and RoPE
+// Grid (rows, q_heads + kv_heads), one wavefront per head.
+__global__ __launch_bounds__(64) void k_heads(HeadArgs a) {
+  __shared__ float out[kHd];
+  const int row = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
+  const int position = a.first_position + row;
+  const float* rope_pos = a.rope + static_cast<uint64_t>(position) * kHd;
+  if (head < a.q_heads) {
+    const uint64_t base = static_cast<uint64_t>(row) * a.q_heads * kHd + static_cast<uint64_t>(head) * kHd;
+    head_norm_rope(a.q + base, a.q_norm, rope_pos, lane, a.eps, out);
+    a.q_rot[base + lane] = dl_f32_to_bf16(out[lane]);
+    a.q_rot[base + lane + 64] = dl_f32_to_bf16(out[lane + 64]);
+  } else {
+    const int g = head - a.q_heads;
+    const uint64_t base = static_cast<uint64_t>(row) * a.kv_heads * kHd + static_cast<uint64_t>(g) * kHd;
+    head_norm_rope(a.k + base, a.k_norm, rope_pos, lane, a.eps, out);
+    uint16_t* dst = a.k_cache + (static_cast<uint64_t>(g) * a.cap + position) * kHd;
+    dst[lane] = dl_f32_to_bf16(out[lane]);
+    dst[lane + 64] = dl_f32_to_bf16(out[lane + 64]);
+  }
+}
+
+// ------------------------------------------------------------- attention
+// Grid (query tiles of 64 rows, query heads); 4 waves of 16 rows each.
+// S = Q K^T with 16x16x32 MFMA, online softmax in FP32, O += P V with P
+// split exactly into three BF16 parts.
+__global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
+  __shared__ __align__(16) uint16_t Qs[kAttnRows * kQRow];
+  __shared__ __align__(16) uint16_t Ks[kKeyTile * kQRow];
+  __shared__ __align__(16) uint16_t Vs[kHd * kVRow];
+  __shared__ __align__(16) float Ps[4][16 * kPRow];
+  const int q0 = blockIdx.x * kAttnRows;
+  const int h = blockIdx.y, g = h / (a.q_heads / a.kv_heads);
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHd;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = tid + kAttnThreads * j, row = i / 16, col = (i % 16) * 8;
+    *reinterpret_cast<u32x4*>(&Qs[row * kQRow + col]) =
+        q0 + row < a.rows
+            ? *reinterpret_cast<const u32x4*>(a.q_rot + static_cast<uint64_t>(q0 + row) * qw + h * kHd + col)
+            : zero;
+  }
+  const uint16_t* kc = a.k_cache + static_cast<uint64_t>(g) * a.cap * kHd;
+  const uint16_t* vc = a.v_cache + static_cast<uint64_t>(g) * kHd * a.cap;
+
+  float m_run[4], l_run[4];
+  floatx4 o[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    m_run[j] = -INFINITY;
+    l_run[j] = 0.0f;
+  }
+#pragma unroll
+  for (int d = 0; d < 8; ++d) o[d] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int last_row = min(q0 + kAttnRows, a.rows) - 1;
+  const int key_end = a.first_position + last_row + 1;
+  for (int kt0 = 0; kt0 < key_end; kt0 += kKeyTile) {
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = tid + kAttnThreads * j;
+      const int key = i / 16, col = (i % 16) * 8;
+      const int kk = min(kt0 + key, a.cap - 1);
+      *reinterpret_cast<u32x4*>(&Ks[key * kQRow + col]) =
+          *reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(kk) * kHd + col);
+      const int d = i / 8, vcol = (i % 8) * 8;
+      u32x4 vv = *reinterpret_cast<const u32x4*>(vc + static_cast<uint64_t>(d) * a.cap + kt0 + vcol);
+      // Keys at or past key_end are masked for every row of this tile (p = 0);
+      // zero them so stale cache contents cannot turn 0 * v into NaN.
+      const int left = key_end - (kt0 + vcol);
+      if (left < 8) {
+        uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (e >= left) w[e / 2] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+        vv = u32x4{w[0], w[1], w[2], w[3]};
+      }
+      *reinterpret_cast<u32x4*>(&Vs[d * kVRow + vcol]) = vv;
+    }
+    __syncthreads();
+
+    floatx4 s[4];
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) s[sub] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < kHd / 32; ++ks) {
+      const bf16x8 qa = as_bf16x8(
+          *reinterpret_cast<const u32x4*>(&Qs[(16 * wave + lane % 16) * kQRow + 32 * ks + 8 * (lane / 16)]));
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        const bf16x8 kb = as_bf16x8(
+            *reinterpret_cast<const u32x4*>(&Ks[(16 * sub + lane % 16) * kQRow + 32 * ks + 8 * (lane / 16)]));
+        s[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, kb, s[sub], 0, 0, 0);
+      }
+    }
+
+    // Lane holds key kt0 + 16 sub + lane % 16 of rows 4 (lane / 16) + j.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int qpos = a.first_position + q0 + 16 * wave + 4 * (lane / 16) + j;
+      float tile_max = -INFINITY;
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        const int key = kt0 + 16 * sub + lane % 16;
+        const float v = key <= qpos ? s[sub][j] * a.scale : -INFINITY;
+        s[sub][j] = v;
+        tile_max = fmaxf(tile_max, v);
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) tile_max = fmaxf(tile_max, __shfl_xor(tile_max, off));
+      const float m_new = fmaxf(m_run[j], tile_max);
+      const float alpha = m_new == -INFINITY ? 1.0f : __expf(m_run[j] - m_new);
+      float row_sum = 0.0f;
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        const float p = s[sub][j] == -INFINITY ? 0.0f : __expf(s[sub][j] - m_new);
+        s[sub][j] = p;
+        row_sum += p;
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) row_sum += __shfl_xor(row_sum, off);
+      l_run[j] = l_run[j] * alpha + row_sum;
+      m_run[j] = m_new;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) o[d][j] *= alpha;
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) Ps[wave][(4 * (lane / 16) + j) * kPRow + 16 * sub + lane % 16] = s[sub][j];
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int ks = 0; ks < kKeyTile / 32; ++ks) {
+      const float* prow = &Ps[wave][(lane % 16) * kPRow + 32 * ks + 8 * (lane / 16)];
+      const float4 pa = *reinterpret_cast<const float4*>(prow);
+      const float4 pb = *reinterpret_cast<const float4*>(prow + 4);
+      const float p[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+      uint16_t hi[8], mid[8], lo[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        hi[e] = dl_f32_to_bf16(p[e]);
+        const float r1 = p[e] - dl_bf16_to_f32(hi[e]);
+        mid[e] = dl_f32_to_bf16(r1);
+        lo[e] = dl_f32_to_bf16(r1 - dl_bf16_to_f32(mid[e]));
+      }
+      auto pack = [](const uint16_t (&x)[8]) {
+        const u32x4 u = {uint32_t(x[0]) | (uint32_t(x[1]) << 16), uint32_t(x[2]) | (uint32_t(x[3]) << 16),
+                         uint32_t(x[4]) | (uint32_t(x[5]) << 16), uint32_t(x[6]) | (uint32_t(x[7]) << 16)};
+        return as_bf16x8(u);
+      };
+      const bf16x8 ph = pack(hi), pm = pack(mid), pl = pack(lo);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const bf16x8 vb = as_bf16x8(
+            *reinterpret_cast<const u32x4*>(&Vs[(16 * d + lane % 16) * kVRow + 32 * ks + 8 * (lane / 16)]));
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, vb, o[d], 0, 0, 0);
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pm, vb, o[d], 0, 0, 0);
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, vb, o[d], 0, 0, 0);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = q0 + 16 * wave + 4 * (lane / 16) + j;
+    if (row < a.rows) {
+      uint16_t* dst = a.out + static_cast<uint64_t>(row) * qw;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const uint32_t feature = h * kHd + 16 * d + lane % 16;
+        dst[permuted(feature, 16)] = dl_f32_to_bf16(o[d][j] / l_run[j]);
+      }
+    }
+  }
+}
+
+// x_perm[m][permuted(k, P)] = x[m][k].
+__global__ void k_permute(const uint16_t* x, uint16_t* out, uint64_t rows, uint32_t width, uint32_t P) {
+  const uint64_t n = rows * width;
+  const uint64_t step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step) {
+    const uint64_t m = i / width;
+    const uint32_t k = static_cast<uint32_t>(i % width);
+    out[m * width + permuted(k, P)] = x[i];
+  }
+}
+
+}  // namespace
+
+void launch_permute(hipStream_t stream, const uint16_t* x, uint16_t* out, uint64_t rows, uint32_t width,
+                    uint32_t P) {
+  const uint64_t n = rows * width;
+  const unsigned grid = static_cast<unsigned>(std::min<uint64_t>((n + 255) / 256, 65535));
+  hipLaunchKernelGGL(k_permute, dim3(grid), dim3(256), 0, stream, x, out, rows, width, P);
+}
+
+void launch_gemm(hipStream_t stream, const GemmArgs& a) {
+  const dim3 grid(a.N / kTileN, a.M / kTileM);
+  switch (a.epilogue) {
+    case kStore: hipLaunchKernelGGL(k_gemm<kStore>, grid, dim3(kGemmThreads), 0, stream, a); break;
+    case kStoreQkv: hipLaunchKernelGGL(k_gemm<kStoreQkv>, grid, dim3(kGemmThreads), 0, stream, a); break;
+    case kResidual: hipLaunchKernelGGL(k_gemm<kResidual>, grid, dim3(kGemmThreads), 0, stream, a); break;
+    default: hipLaunchKernelGGL(k_gemm<kGateUp>, grid, dim3(kGemmThreads), 0, stream, a); break;
+  }
+}
+
+void launch_norm(hipStream_t stream, const NormArgs& a) {
+  hipLaunchKernelGGL(k_norm, dim3(a.rows), dim3(256), 0, stream, a);
+}
+
+void launch_heads(hipStream_t stream, const HeadArgs& a) {
+  hipLaunchKernelGGL(k_heads, dim3(a.rows, a.q_heads + a.kv_heads), dim3(64), 0, stream, a);
+}
+
+void launch_attention(hipStream_t stream, const AttnArgs& a) {
+  hipLaunchKernelGGL(k_attention, dim3((a.rows + kAttnRows - 1) / kAttnRows, a.q_heads), dim3(kAttnThreads), 0,
+                     stream, a);
+}
+
+}  // namespace dl::prefill
+
+// ------------------------------------------------------------------ C ABI
+extern "C" int dl_prefill_projection(dl_queue* queue, const void* input, const void* packed, void* output,
+                                     void* workspace, uint64_t rows, uint64_t input_width,
+                                     uint64_t output_width) {
+  return dl::guard([&] {
+    dl::require(queue && input && packed && output && workspace, "null argument");
+    dl::require(rows > 0 && rows % dl::prefill::kTileM == 0, "rows must be a positive multiple of 128");
+    dl::require(output_width > 0 && output_width % dl::prefill::kTileN == 0,
+                "output width must be a positive multiple of 128");
+    const int P = (input_width <= 4096 && output_width > 1024) ? 16 : 32;
+    dl::require(input_width > 0 && input_width % (8 * P) == 0 && input_width % 64 == 0,
+                "input width must be a multiple of 8P and of 64");
+    dl::enter(queue);
+    hipStream_t s = queue->stream;
+    uint16_t* perm = static_cast<uint16_t*>(workspace);
+    dl::prefill::launch_permute(s, static_cast<const uint16_t*>(input), perm, rows,
+                                static_cast<uint32_t>(input_width), static_cast<uint32_t>(P));
+    dl::prefill::GemmArgs g{};
+    g.a = g.a_alt = perm;
+    g.w = g.w_alt = static_cast<const uint16_t*>(packed);
+    g.M = static_cast<int>(rows);
+    g.N = static_cast<int>(output_width);
+    g.K = static_cast<int>(input_width);
+    g.n_split = g.N;
+    g.P = g.P_alt = P;
+    g.epilogue = dl::prefill::kStore;
+    g.m_valid = g.M;
+    g.out = static_cast<uint16_t*>(output);
+    dl::prefill::launch_gemm(s, g);
+    dl::check_launch(queue, "prefill projection");
+  });
+}
+
+extern "C" int dl_prefill_attention(dl_queue* queue, const void* q_rot, const void* k_cache, const void* v_cache,
+                                    void* output, uint64_t rows, uint64_t q_heads, uint64_t kv_heads,
+                                    uint64_t capacity, uint64_t first_position) {
+  return dl::guard([&] {
+    dl::require(queue && q_rot && k_cache && v_cache && output, "null argument");
+    dl::require(rows > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0, "invalid attention shape");
+    dl::require(capacity % 64 == 0 && first_position + rows <= capacity, "rows exceed the cache capacity",
+                DL_LENGTH_ERROR);
+    dl::enter(queue);
+    dl::prefill::AttnArgs a{static_cast<const uint16_t*>(q_rot), static_cast<const uint16_t*>(k_cache),
+                            static_cast<const uint16_t*>(v_cache), static_cast<uint16_t*>(output),
+                            static_cast<int>(rows), static_cast<int>(q_heads), static_cast<int>(kv_heads),
+                            static_cast<int>(capacity), static_cast<int>(first_position),
+                            static_cast<float>(1.0 / std::sqrt(128.0))};
+    dl::prefill::launch_attention(queue->stream, a);
+    dl::check_launch(queue, "prefill attention");
+  });
+}
+
+extern "C" int dl_prefill_gate_up(dl_queue* queue, const void* input, const void* packed, void* output,
+                                  void* workspace, uint64_t rows, uint64_t hidden, uint64_t ffn) {
+  return dl::guard([&] {
+    dl::require(queue && input && packed && output && workspace, "null argument");
+    dl::require(rows > 0 && rows % dl::prefill::kTileM == 0 && (2 * ffn) % dl::prefill::kTileN == 0 &&
+                    hidden % 128 == 0 && hidden <= 4096 && ffn % 256 == 0,
+                "invalid gate/up shape");
+    dl::enter(queue);
+    hipStream_t s = queue->stream;
+    uint16_t* perm = static_cast<uint16_t*>(workspace);
+    dl::prefill::launch_permute(s, static_cast<const uint16_t*>(input), perm, rows, static_cast<uint32_t>(hidden),
+                                16);
+    dl::prefill::GemmArgs g{};
+    g.a = g.a_alt = perm;
+    g.w = g.w_alt = static_cast<const uint16_t*>(packed);
+    g.M = static_cast<int>(rows);
+    g.N = g.n_split = static_cast<int>(2 * ffn);
+    g.K = static_cast<int>(hidden);
+    g.P = g.P_alt = 16;
+    g.epilogue = dl::prefill::kGateUp;
+    g.m_valid = g.M;
+    g.out = static_cast<uint16_t*>(output);
+    dl::prefill::launch_gemm(s, g);
+    dl::check_launch(queue, "prefill gate/up");
+  });
+}

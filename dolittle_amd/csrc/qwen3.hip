@@ -34,6 +34,8 @@
 #include "dl_internal.h"
 #include "dl_synth.h"
 #include "gemv.h"
+#include "heads.h"
+#include "prefill.h"
 #include "sampler.h"
 
 namespace dl {
@@ -283,41 +285,6 @@ struct AttnArgs {
   float eps, scale;
 };
 
-// Per-head RMSNorm (width 128: lane t, component c holds feature t+32c;
-// normalization.cu:82-132) followed by RoPE (rotary.cu:84-126) for one head,
-// computed by one wavefront; lane i owns the RoPE pair (i, i+64).  The
-// operands are loaded first (head_load) so callers can issue them ahead of
-// other memory traffic.
-struct HeadOperands {
-  float xa, xb, ga, gb, cosine, sine;
-};
-
-__device__ __forceinline__ HeadOperands head_load(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gain,
-                                                  const float* __restrict__ rope_pos, int lane) {
-  return HeadOperands{dl_bf16_to_f32(x[lane]), dl_bf16_to_f32(x[lane + 64]), dl_bf16_to_f32(gain[lane]),
-                      dl_bf16_to_f32(gain[lane + 64]), rope_pos[2 * lane], rope_pos[2 * lane + 1]};
-}
-
-__device__ __forceinline__ void head_norm_rope(const HeadOperands& o, int lane, float eps, float* out) {
-  const float xa = o.xa, xb = o.xb;
-  const float xa_hi = __shfl(xa, (lane + 32) & 63);
-  const float xb_hi = __shfl(xb, (lane + 32) & 63);
-  float s = ((xa * xa + xa_hi * xa_hi) + xb * xb) + xb_hi * xb_hi;
-#pragma unroll
-  for (int off = 1; off < 32; off *= 2) s = s + __shfl_down(s, off, 32);
-  const float total = __shfl(s, 0);
-  const float inverse = inverse_sqrt(total * (1.0f / 128.0f) + eps);
-  const float na = rbf(rbf(xa * inverse) * o.ga);
-  const float nb = rbf(rbf(xb * inverse) * o.gb);
-  out[lane] = rbf(rbf(na * o.cosine) - rbf(nb * o.sine));
-  out[lane + 64] = rbf(rbf(nb * o.cosine) + rbf(na * o.sine));
-}
-
-__device__ __forceinline__ void head_norm_rope(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gain,
-                                               const float* __restrict__ rope_pos, int lane, float eps,
-                                               float* out) {
-  head_norm_rope(head_load(x, gain, rope_pos, lane), lane, eps, out);
-}
 
 // Grid (kv head, 64-key tile, sequence); block 256 = 4 waves, one per query
 // head of the group.  Scores use 8 lanes per key, each an FMA chain over 16
@@ -975,6 +942,57 @@ __global__ void k_cache_rows(uint16_t* k_cache, uint16_t* v_cache, int cap, int 
   }
 }
 
+// ---------------------------------------------------- MFMA prefill helpers
+// Embedding rows of prefill positions [first, first + rows) into h
+// [padded][D]; rows past `rows` are zeroed.  The embedding override row
+// replaces its position when the sequence is masked in.
+struct PrefillEmbedArgs {
+  const uint32_t* tokens;      // absolute-position history
+  const uint16_t* lm_packed;   // tied: packed LM head (P = 16)
+  const uint16_t* embedding;   // untied: row-major [V][D]
+  const uint16_t* override_row;
+  uint16_t* h;
+  uint32_t rows, D;
+  uint64_t first;
+  int tied, override_row_active;
+  uint64_t override_position;
+};
+
+__global__ __launch_bounds__(kBlock) void k_prefill_embed(PrefillEmbedArgs a) {
+  const uint32_t r = blockIdx.x;
+  uint16_t* out = a.h + static_cast<uint64_t>(r) * a.D;
+  if (r >= a.rows) {
+    for (uint32_t k = threadIdx.x; k < a.D; k += blockDim.x) out[k] = 0;
+    return;
+  }
+  const uint64_t pos = a.first + r;
+  const uint32_t token = a.tokens[pos];
+  if (a.override_row_active && pos == a.override_position) {
+    for (uint32_t k = threadIdx.x; k < a.D; k += blockDim.x) out[k] = a.override_row[k];
+  } else if (a.tied) {
+    for (uint32_t k = threadIdx.x; k < a.D; k += blockDim.x) out[k] = a.lm_packed[packed_index(token, k, 16, a.D)];
+  } else {
+    const uint16_t* row = a.embedding + static_cast<uint64_t>(token) * a.D;
+    for (uint32_t k = threadIdx.x; k < a.D; k += blockDim.x) out[k] = row[k];
+  }
+}
+
+// h <- BF16(FP32(h) + v) over prefill rows (all-position steering), then an
+// optional copy of each row into the capture arena at its position.
+__global__ __launch_bounds__(kBlock) void k_prefill_steer_capture(uint16_t* h, const float* steer, uint16_t* capture,
+                                                                  uint32_t D, uint64_t first) {
+  const uint32_t r = blockIdx.x;
+  uint16_t* row = h + static_cast<uint64_t>(r) * D;
+  for (uint32_t k = threadIdx.x; k < D; k += blockDim.x) {
+    float value = dl_bf16_to_f32(row[k]);
+    if (steer) {
+      value = rbf(value + steer[k]);
+      row[k] = bf16_bits(value);
+    }
+    if (capture) capture[(first + r) * D + k] = bf16_bits(value);
+  }
+}
+
 }  // namespace
 }  // namespace dl
 
@@ -1256,6 +1274,16 @@ struct dl_plan {
   uint32_t override_mask = 0;
   uint64_t override_position = 0;
   uint32_t max_new = 0;
+  // MFMA prefill: row buffers (allocated on first use for the capacity) and
+  // the prompt whose positions [0, prefilled) the caches hold.
+  struct Prefill {
+    uint16_t *h = nullptr, *x16 = nullptr, *x32 = nullptr, *q = nullptr, *k = nullptr, *q_rot = nullptr,
+             *att = nullptr, *act = nullptr;
+    uint32_t rows = 0;  // allocated rows (multiple of 128)
+  } pf;
+  std::vector<uint32_t> prefilled_prompt;
+  uint32_t prefilled = 0;
+  uint64_t start_position = 0;  // position the prepared generation starts at
 
   template <class T>
   T* alloc(uint64_t count) {
@@ -1659,6 +1687,7 @@ int dl_plan_reset(dl_plan* plan) {
     *plan->cancel_host = 0;
     plan->position = 0;
     plan->host_position = 0;
+    plan->prefilled = 0;
     dl::check_hip(hipStreamSynchronize(plan->queue->stream), "reset");
   });
 }
@@ -1679,6 +1708,7 @@ int dl_plan_forward(dl_plan* plan, const uint32_t* tokens, uint32_t rows) {
     require(plan && tokens, "null argument");
     dl::enter(plan->queue);
     require(rows > 0, "empty forward");
+    plan->prefilled = 0;
     dl::Control c;
     hipStream_t s = plan->queue->stream;
     dl::check_hip(hipMemcpyAsync(&c, plan->ctl, sizeof c, hipMemcpyDeviceToHost, s), "read control");
@@ -1845,6 +1875,7 @@ int dl_plan_seek(dl_plan* plan, uint64_t position) {
     require(position < plan->capacity, "position outside the capacity", DL_LENGTH_ERROR);
     dl::k_seek<<<1, 1, 0, plan->queue->stream>>>(plan->ctl, position);
     plan->host_position = position;
+    plan->prefilled = 0;
     dl::check_launch(plan->queue, "seek");
     dl::check_hip(hipStreamSynchronize(plan->queue->stream), "seek wait");
   });
@@ -1868,7 +1899,7 @@ int dl_plan_generate(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_leng
   const int status =
       dl_plan_prepare_generation(plan, prompt, prompt_length, max_new, sampling, seeds, stop_ids, stop_count);
   if (status != DL_OK) return status;
-  return dl_plan_decode_steps(plan, prompt_length + max_new);
+  return dl_plan_decode_steps(plan, static_cast<uint32_t>(prompt_length - plan->start_position) + max_new);
 }
 
 int dl_plan_prepare_generation(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length, uint32_t max_new,
@@ -1922,7 +1953,12 @@ int dl_plan_prepare_generation(dl_plan* plan, const uint32_t* prompt, uint32_t p
       dl::check_hip(hipStreamSynchronize(s), "stop mask wait");
     }
     plan->max_new = max_new;
-    init_control(plan, 0, prompt_length, max_new, mode);
+    // A prompt whose leading positions were prefilled resumes after them.
+    const bool resume = plan->prefilled > 0 && plan->prefilled_prompt.size() == prompt_length &&
+                        std::equal(prompt, prompt + prompt_length, plan->prefilled_prompt.begin());
+    plan->start_position = resume ? plan->prefilled : 0;
+    if (!resume) plan->prefilled = 0;
+    init_control(plan, plan->start_position, prompt_length, max_new, mode);
   });
 }
 
@@ -1968,6 +2004,171 @@ int dl_plan_request_stop(dl_plan* plan) {
   return guard([&] {
     require(plan != nullptr, "null plan");
     __atomic_store_n(plan->cancel_host, 1u, __ATOMIC_RELEASE);
+  });
+}
+
+
+int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length) {
+  return guard([&] {
+    require(plan && prompt, "null argument");
+    dl::enter(plan->queue);
+    const dl_qwen3* m = plan->model;
+    const auto& c = m->cfg;
+    require(prompt_length > 0, "empty prompt");
+    require(prompt_length <= plan->capacity, "prompt exceeds the cache capacity", DL_LENGTH_ERROR);
+    for (uint32_t i = 0; i < prompt_length; ++i) require(prompt[i] < c.vocab, "prompt id outside the vocabulary");
+    hipStream_t s = plan->queue->stream;
+    dl::check_hip(hipStreamSynchronize(s), "prefill wait");
+    plan->prefilled = 0;
+    plan->prefilled_prompt.assign(prompt, prompt + prompt_length);
+    // The last prompt position is consumed by the exact decode step, which
+    // also selects the first token.
+    const uint32_t rows = prompt_length - 1;
+    if (rows == 0) return;
+    const uint32_t D = c.hidden, QW = c.q_heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
+    const uint32_t M = static_cast<uint32_t>(dl::ceil_div(rows, dl::prefill::kTileM) * dl::prefill::kTileM);
+    auto& pf = plan->pf;
+    if (pf.rows < M) {
+      const uint32_t R = static_cast<uint32_t>(dl::ceil_div(plan->capacity, dl::prefill::kTileM) * dl::prefill::kTileM);
+      pf.h = plan->alloc<uint16_t>(uint64_t(R) * D);
+      pf.x16 = plan->alloc<uint16_t>(uint64_t(R) * D);
+      pf.x32 = plan->alloc<uint16_t>(uint64_t(R) * D);
+      pf.q = plan->alloc<uint16_t>(uint64_t(R) * QW);
+      pf.k = plan->alloc<uint16_t>(uint64_t(R) * KW);
+      pf.q_rot = plan->alloc<uint16_t>(uint64_t(R) * QW);
+      pf.att = plan->alloc<uint16_t>(uint64_t(R) * QW);
+      pf.act = plan->alloc<uint16_t>(uint64_t(R) * F);
+      dl::check_hip(hipMemsetAsync(pf.att, 0, uint64_t(R) * QW * 2, s), "prefill clear");
+      pf.rows = R;
+    }
+    dl::check_hip(hipMemcpyAsync(plan->tokens, prompt, prompt_length * 4ull, hipMemcpyHostToDevice, s), "prompt");
+    const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));
+    // Sequences share the prompt: prefill each separately only when
+    // steering or capture differs between them, else copy sequence 0.
+    const bool per_sequence = plan->batch > 1 && (plan->steer_mask != 0 || plan->capture_layer >= 0);
+    const uint32_t runs = per_sequence ? plan->batch : 1;
+    for (uint32_t seq = 0; seq < runs; ++seq) {
+      dl::PrefillEmbedArgs ea{plan->tokens, m->lm_head, m->embedding, plan->override_row, pf.h, rows, D, 0,
+                              c.tied_embeddings ? 1 : 0,
+                              (plan->override_active && ((plan->override_mask >> seq) & 1u)) ? 1 : 0,
+                              plan->override_position};
+      dl::k_prefill_embed<<<M, dl::kBlock, 0, s>>>(ea);
+      for (uint32_t l = 0; l < c.layers; ++l) {
+        uint16_t* kc = plan->k_cache + uint64_t(seq) * plan->cache_seq_stride + uint64_t(l) * plan->cache_layer_stride;
+        uint16_t* vc = plan->v_cache + uint64_t(seq) * plan->cache_seq_stride + uint64_t(l) * plan->cache_layer_stride;
+        dl::prefill::launch_norm(s, {pf.h, m->input_norm[l], pf.x16, pf.x32, static_cast<int>(M), static_cast<int>(D),
+                                     c.rms_eps});
+        dl::prefill::GemmArgs g{};
+        g.a = pf.x16;
+        g.a_alt = pf.x32;
+        g.w = m->qkv[l];
+        g.w_alt = m->qkv[l] + uint64_t(QW) * D;
+        g.M = static_cast<int>(M);
+        g.N = static_cast<int>(QW + 2 * KW);
+        g.K = static_cast<int>(D);
+        g.n_split = static_cast<int>(QW);
+        g.P = m->p_q;
+        g.P_alt = m->p_kv;
+        g.epilogue = dl::prefill::kStoreQkv;
+        g.m_valid = static_cast<int>(rows);
+        g.out = pf.q;
+        g.out2 = pf.k;
+        g.v_cache = vc;
+        g.q_width = static_cast<int>(QW);
+        g.kv_width = static_cast<int>(KW);
+        g.cap = static_cast<int>(plan->cap);
+        g.first_position = 0;
+        dl::prefill::launch_gemm(s, g);
+        dl::prefill::launch_heads(s, {pf.q, pf.k, m->q_norm[l], m->k_norm[l], plan->rope, pf.q_rot, kc,
+                                      static_cast<int>(rows), static_cast<int>(c.q_heads),
+                                      static_cast<int>(c.kv_heads), static_cast<int>(plan->cap), 0, c.rms_eps});
+        dl::prefill::launch_attention(s, {pf.q_rot, kc, vc, pf.att, static_cast<int>(rows),
+                                          static_cast<int>(c.q_heads), static_cast<int>(c.kv_heads),
+                                          static_cast<int>(plan->cap), 0, scale});
+        dl::prefill::GemmArgs o{};
+        o.a = o.a_alt = pf.att;
+        o.w = o.w_alt = m->o[l];
+        o.M = static_cast<int>(M);
+        o.N = o.n_split = static_cast<int>(D);
+        o.K = static_cast<int>(QW);
+        o.P = o.P_alt = m->p_o;
+        o.epilogue = dl::prefill::kResidual;
+        o.m_valid = static_cast<int>(rows);
+        o.out = pf.h;
+        dl::prefill::launch_gemm(s, o);
+        dl::prefill::launch_norm(s, {pf.h, m->post_norm[l], pf.x16, nullptr, static_cast<int>(M),
+                                     static_cast<int>(D), c.rms_eps});
+        dl::prefill::GemmArgs gu{};
+        gu.a = gu.a_alt = pf.x16;
+        gu.w = gu.w_alt = m->gu[l];
+        gu.M = static_cast<int>(M);
+        gu.N = gu.n_split = static_cast<int>(2 * F);
+        gu.K = static_cast<int>(D);
+        gu.P = gu.P_alt = m->p_gu;
+        gu.epilogue = dl::prefill::kGateUp;
+        gu.m_valid = static_cast<int>(rows);
+        gu.out = pf.act;
+        dl::prefill::launch_gemm(s, gu);
+        dl::prefill::GemmArgs dn{};
+        dn.a = dn.a_alt = pf.act;
+        dn.w = dn.w_alt = m->down[l];
+        dn.M = static_cast<int>(M);
+        dn.N = dn.n_split = static_cast<int>(D);
+        dn.K = static_cast<int>(F);
+        dn.P = dn.P_alt = m->p_down;
+        dn.epilogue = dl::prefill::kResidual;
+        dn.m_valid = static_cast<int>(rows);
+        dn.out = pf.h;
+        dl::prefill::launch_gemm(s, dn);
+        const bool steer = plan->steer_layer == static_cast<int32_t>(l) && ((plan->steer_mask >> seq) & 1u);
+        const bool capture = plan->capture && plan->capture_layer == static_cast<int32_t>(l);
+        if (steer || capture)
+          dl::k_prefill_steer_capture<<<rows, dl::kBlock, 0, s>>>(
+              pf.h, steer ? plan->steer + uint64_t(seq) * D : nullptr,
+              capture ? plan->capture + uint64_t(seq) * plan->cap * D : nullptr, D, 0);
+      }
+      dl::check_launch(plan->queue, "prefill");
+    }
+    if (!per_sequence) {
+      // Copy sequence 0's prefilled rows into the other sequences' caches.
+      for (uint32_t b = 1; b < plan->batch; ++b) {
+        const uint64_t off = uint64_t(b) * plan->cache_seq_stride;
+        dl::check_hip(hipMemcpy2DAsync(plan->k_cache + off, uint64_t(plan->cap) * c.head_dim * 2, plan->k_cache,
+                                       uint64_t(plan->cap) * c.head_dim * 2, uint64_t(rows) * c.head_dim * 2,
+                                       uint64_t(c.layers) * c.kv_heads, hipMemcpyDeviceToDevice, s),
+                      "prefill K copy");
+        dl::check_hip(hipMemcpy2DAsync(plan->v_cache + off, uint64_t(plan->cap) * 2, plan->v_cache,
+                                       uint64_t(plan->cap) * 2, uint64_t(rows) * 2, uint64_t(c.layers) * KW,
+                                       hipMemcpyDeviceToDevice, s),
+                      "prefill V copy");
+      }
+    }
+    dl::check_hip(hipStreamSynchronize(s), "prefill");
+    plan->prefilled = rows;
+  });
+}
+
+
+int dl_plan_read_prefill_hidden(dl_plan* plan, uint64_t first_row, uint64_t count, uint16_t* host) {
+  return dl_plan_read_prefill_buffer(plan, 0, first_row * plan->model->cfg.hidden,
+                                     count * plan->model->cfg.hidden, host);
+}
+
+int dl_plan_read_prefill_buffer(dl_plan* plan, uint32_t which, uint64_t first, uint64_t count, uint16_t* host) {
+  return guard([&] {
+    require(plan && host, "null argument");
+    dl::enter(plan->queue);
+    const auto& c = plan->model->cfg;
+    const uint64_t R = plan->pf.rows, D = c.hidden, QW = uint64_t(c.q_heads) * c.head_dim,
+                   KW = uint64_t(c.kv_heads) * c.head_dim, F = c.ffn;
+    const uint16_t* bufs[8] = {plan->pf.h, plan->pf.x16, plan->pf.x32, plan->pf.q,
+                               plan->pf.k, plan->pf.q_rot, plan->pf.att, plan->pf.act};
+    const uint64_t sizes[8] = {R * D, R * D, R * D, R * QW, R * KW, R * QW, R * QW, R * F};
+    require(which < 8, "unknown prefill buffer");
+    require(bufs[which] != nullptr && first + count <= sizes[which], "no prefill rows", DL_LENGTH_ERROR);
+    dl::check_hip(hipMemcpyAsync(host, bufs[which] + first, count * 2, hipMemcpyDeviceToHost, plan->queue->stream),
+                  "read prefill buffer");
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "read prefill buffer wait");
   });
 }
 

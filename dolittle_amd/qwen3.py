@@ -202,6 +202,12 @@ class Plan:
                   C.byref(s), seeds_a.ctypes.data_as(_lib.u64p), stops.ctypes.data_as(_lib.u32p), n)
         self.max_new = max_new
 
+    def prefill(self, prompt) -> None:
+        """MFMA prefill of positions [0, len(prompt) - 1); a following
+        generate() with the same prompt resumes at the last prompt position."""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        _lib.call("dl_plan_prefill", self.handle, p.ctypes.data_as(_lib.u32p), p.size)
+
     def decode_steps(self, steps: int) -> None:
         _lib.call("dl_plan_decode_steps", self.handle, steps)
 

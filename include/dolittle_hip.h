@@ -170,6 +170,26 @@ int dl_projection_packed(dl_queue* queue, const void* input, const void* packed,
                          uint64_t rows, uint64_t input_width, uint64_t output_width,
                          const uint64_t* output_position);
 
+/* MFMA projection for many rows (the prefill GEMM): Y[R,O] = X[R,I] W^T
+ * with W in the packed layout above, BF16 in and out, FP32 accumulation in
+ * MFMA order (tolerance, not bit-exact).  `workspace` holds R*I BF16 for the
+ * permuted input.  R and O must be multiples of 128, I a multiple of 8P. */
+int dl_prefill_projection(dl_queue* queue, const void* input, const void* packed, void* output,
+                          void* workspace, uint64_t rows, uint64_t input_width, uint64_t output_width);
+
+/* Diagnostics of the prefill kernels (tolerance checks, no reference
+ * counterpart).  dl_prefill_attention: causal attention of `rows` queries
+ * at positions first_position.. over the plan-layout caches (K
+ * [kv_heads][capacity][128], V^T [kv_heads*128][capacity]); q_rot is
+ * [rows][q_heads*128] after QK norm and RoPE; output rows are in P16
+ * order.  dl_prefill_gate_up: SiLU(x Wg^T) * (x Wu^T) for interleaved packed
+ * gate/up rows (the resident layout), output rows of `ffn` in P32 order. */
+int dl_prefill_attention(dl_queue* queue, const void* q_rot, const void* k_cache, const void* v_cache,
+                         void* output, uint64_t rows, uint64_t q_heads, uint64_t kv_heads,
+                         uint64_t capacity, uint64_t first_position);
+int dl_prefill_gate_up(dl_queue* queue, const void* input, const void* packed, void* output,
+                       void* workspace, uint64_t rows, uint64_t hidden, uint64_t ffn);
+
 /* -------------------------------------------------------------- Qwen3 model */
 typedef struct dl_qwen3 dl_qwen3;
 
@@ -292,6 +312,25 @@ int dl_plan_set_steering(dl_plan* plan, uint32_t seq, int32_t layer, const float
  * bits) for the sequences in `seq_mask` (bit i = sequence i). */
 int dl_plan_set_embedding_override(dl_plan* plan, uint64_t position, const uint16_t* row,
                                    uint32_t seq_mask);
+
+/* MFMA prefill of a long prompt: positions
+ * [0, prompt_length - 1) of every sequence run as BF16 MFMA GEMMs and causal
+ * flash attention (FP32 softmax and probabilities), filling the KV caches.
+ * A following dl_plan_generate with the same prompt resumes at the last
+ * prompt position, which the exact decode step consumes (selecting the first
+ * token).  Results follow the reference operator sequence within tolerance
+ * (MFMA accumulation order), not bit for bit.  No reference counterpart:
+ * the reference prefills with its exact row kernels (executor.cpp:285-716). */
+int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length);
+/* Diagnostic: residual-stream rows of the last prefill after its final
+ * block (rows [first_row, first_row + count), BF16 [count][hidden]). */
+int dl_plan_read_prefill_hidden(dl_plan* plan, uint64_t first_row, uint64_t count, uint16_t* host);
+/* Diagnostic: elements [first, first + count) of one prefill row buffer of
+ * the last block (0 residual, 1 x in P16 order, 2 x in P32 order, 3 q,
+ * 4 k, 5 rotated q, 6 attention output in P16 order, 7 SiLU*up in P32
+ * order). */
+int dl_plan_read_prefill_buffer(dl_plan* plan, uint32_t which, uint64_t first, uint64_t count,
+                                uint16_t* host);
 
 /* Device-owned token loop.  Consumes the prompt (shared by all sequences),
  * then generates up to max_new tokens per sequence with the sampling law of

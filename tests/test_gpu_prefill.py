@@ -1,0 +1,173 @@
+"""GPU checks of the MFMA prefill path (BASELINE config 3's prompt pass).
+
+MFMA units accumulate in their own order, so this path is compared with
+tolerances rather than bit for bit:
+- the MFMA projection against an FP64 product of the same BF16 operands
+  (at most one BF16 ulp after rounding) at the Qwen3-8B projection shapes;
+- a multi-block model: KV rows written by the prefill against the CPU
+  contract restatement, and the first decoded logits against the oracle's
+  exact logits within 2e-2 absolute / 1e-2 relative (the north-star logits
+  tolerance), at a prompt length that is not a multiple of the 128-row tile.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SEED = 7701
+
+
+def bf16_ulp(x):
+    """Spacing of BF16 numbers at |x| (2^(e-7))."""
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+@pytest.mark.parametrize("rows,in_w,out_w", [(256, 4096, 4096), (128, 4096, 1024), (128, 12288, 4096),
+                                             (384, 4096, 6144)])
+def test_prefill_projection_within_one_ulp(device, queue, oracle, rows, in_w, out_w):
+    from dolittle_amd import _lib
+    x = oracle.normal_bf16(rows * in_w, SEED, 1, 1.0)
+    w = oracle.normal_bf16(out_w * in_w, SEED, 2, 0.02)
+    bx, bw = device.upload_array(queue, x), device.upload_array(queue, w)
+    nbytes = C.c_uint64()
+    _lib.call("dl_projection_packed_bytes", out_w, in_w, C.byref(nbytes))
+    packed = device.allocate(nbytes.value)
+    by, work = device.allocate(rows * out_w * 2), device.allocate(rows * in_w * 2)
+    _lib.call("dl_projection_pack", queue.handle, bw.ptr(), packed.ptr(), out_w, in_w)
+    _lib.call("dl_prefill_projection", queue.handle, bx.ptr(), packed.ptr(), by.ptr(), work.ptr(), rows, in_w, out_w)
+    queue.drain()
+    got = oracle.f32_from_bf16(queue.read(by, np.uint16, rows * out_w)).reshape(rows, out_w).astype(np.float64)
+    xf = oracle.f32_from_bf16(x).reshape(rows, in_w).astype(np.float64)
+    wf = oracle.f32_from_bf16(w).reshape(out_w, in_w).astype(np.float64)
+    exact = xf @ wf.T
+    # One BF16 ulp of rounding plus the FP32 accumulation error of K / 16
+    # sequential MFMA steps (random-walk bound on the absolute-value sum),
+    # which dominates only for outputs near zero.
+    scale = np.abs(xf) @ np.abs(wf).T
+    bound = bf16_ulp(exact) + 4.0 * np.sqrt(in_w / 16) * 2.0 ** -24 * scale + 1e-6
+    err = np.abs(got - exact)
+    assert np.all(err <= bound), float((err / bound).max())
+    # A misplaced operand piece would show as errors of many ulps at
+    # ordinary magnitudes; the bulk stays within one ulp.
+    assert np.mean(err <= bf16_ulp(exact)) > 0.9999
+
+
+def test_prefill_projection_rejects_ragged_shapes(device, queue):
+    from dolittle_amd import InvalidArgument, _lib
+    buf = device.allocate(1 << 20)
+    with pytest.raises(InvalidArgument):
+        _lib.call("dl_prefill_projection", queue.handle, buf.ptr(), buf.ptr(), buf.ptr(), buf.ptr(), 100, 4096, 4096)
+    with pytest.raises(InvalidArgument):
+        _lib.call("dl_prefill_projection", queue.handle, buf.ptr(), buf.ptr(), buf.ptr(), buf.ptr(), 128, 4096, 100)
+
+
+def oracle_weights(o, model):
+    cfg = model.config
+    dims = o.Dims(cfg.hidden, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.ffn, cfg.vocab, cfg.rms_eps,
+                  cfg.rope_theta)
+    blocks = []
+    for layer in range(cfg.layers):
+        blocks.append({name: np.ascontiguousarray(model.read(role, layer).reshape(-1)) for name, role in (
+            ("input_norm", "input_norm"), ("wq", "q"), ("wk", "k"), ("wv", "v"), ("q_norm", "q_norm"),
+            ("k_norm", "k_norm"), ("wo", "o"), ("post_norm", "post_norm"), ("wg", "gate"), ("wu", "up"),
+            ("wd", "down"))})
+    lm = np.ascontiguousarray(model.read("lm_head").reshape(-1))
+    return o.Qwen3Weights(dims, blocks, np.ascontiguousarray(model.read("final_norm")), lm, lm)
+
+
+@pytest.fixture(scope="module")
+def prefill_model(device, queue):
+    from dolittle_amd.qwen3 import Qwen3Config, Qwen3Model
+    model = Qwen3Model(device, queue, Qwen3Config(layers=2))
+    model.fill_synthetic(SEED, 0.02)
+    return model
+
+
+def test_prefill_cache_and_first_logits_within_tolerance(prefill_model, oracle):
+    """The first block's prefilled K/V rows equal the oracle's except for
+    rare flips (MFMA accumulation order), and the first logits after a
+    two-block prefill stay within 0.06 of the exact ones (98% of them within
+    2e-2 absolute + 1e-2 relative).
+    Deeper models drift further (every order-dependent rounding flip
+    propagates through the following blocks); the exact path remains the
+    parity path."""
+    from dolittle_amd.qwen3 import Plan
+    cfg = prefill_model.config
+    w = oracle_weights(oracle, prefill_model)
+    n = 300
+    prompt = [int(t) for t in np.random.default_rng(31).integers(0, cfg.vocab, n)]
+    plan = Plan(prefill_model, batch=1, capacity=320)
+    plan.prefill(prompt)
+    plan.generate(prompt, 1)
+    tokens, results = plan.collect()
+    assert results[0]["generated"] == 1 and results[0]["position"] == n + 1
+
+    kw = cfg.kv_heads * cfg.head_dim
+    k = [np.zeros(320 * kw, np.uint16) for _ in range(cfg.layers)]
+    v = [np.zeros(320 * kw, np.uint16) for _ in range(cfg.layers)]
+    emb = w.embedding.reshape(cfg.vocab, cfg.hidden)
+    h = np.ascontiguousarray(emb[prompt].reshape(-1))
+    for layer in range(cfg.layers):
+        oracle.block_forward(w, layer, h, n, 0, k[layer], v[layer])
+    kg, vg = plan.read_cache(0, 0, n - 1)
+    for got, ref in ((kg, k[0][: (n - 1) * kw]), (vg, v[0][: (n - 1) * kw])):
+        g = oracle.f32_from_bf16(got).astype(np.float64)
+        r = oracle.f32_from_bf16(ref).astype(np.float64)
+        assert np.mean(g == r) > 0.999
+        # A flipped projection output moves its whole head through the QK
+        # norm: a couple of ulps at most (values are O(1) after the norm).
+        assert np.all(np.abs(g - r) <= 2 * bf16_ulp(r) + 2.0 ** -9)
+    logits_ref = oracle.f32_from_bf16(oracle.logits(w, h.reshape(n, cfg.hidden)[-1].copy())).astype(np.float64)
+    logits = oracle.f32_from_bf16(plan.logits(0)).astype(np.float64)
+    diff = np.abs(logits - logits_ref)
+    # The perturbation reaches the logits as absolute noise of a few
+    # hundredths (two blocks), independent of the logit's magnitude.
+    assert diff.max() <= 0.06, float(diff.max())
+    assert np.mean(diff <= 2e-2 + 1e-2 * np.abs(logits_ref)) > 0.98
+    # The first token is the exact greedy selection over the device logits.
+    assert oracle.greedy(plan.logits(0)) == (0, int(tokens[0][0]))
+
+
+def test_prefill_attention_matches_contract(device, queue, oracle):
+    """Causal MFMA attention (FP32 softmax, probabilities split exactly into
+    three BF16 parts) against the exact attention contract; flips only where
+    the output is a cancelling sum."""
+    from dolittle_amd import _lib
+    rows, cap, H, G = 200, 256, 32, 8
+    qr = oracle.normal_bf16(rows * H * 128, 5, 1, 1.0)
+    k_ref = oracle.normal_bf16(cap * G * 128, 5, 2, 1.0)
+    v_ref = oracle.normal_bf16(cap * G * 128, 5, 3, 1.0)
+    k_plan = np.ascontiguousarray(k_ref.reshape(cap, G, 128).transpose(1, 0, 2))
+    v_plan = np.ascontiguousarray(v_ref.reshape(cap, G * 128).T)
+    bq, bk, bv = device.upload_array(queue, qr), device.upload_array(queue, k_plan), device.upload_array(queue, v_plan)
+    bo = device.allocate(rows * H * 128 * 2)
+    _lib.call("dl_prefill_attention", queue.handle, bq.ptr(), bk.ptr(), bv.ptr(), bo.ptr(), rows, H, G, cap, 0)
+    queue.drain()
+    out = queue.read(bo, np.uint16, rows * H * 128).reshape(rows, H * 128)
+    k = np.arange(H * 128)
+    nat = out[:, (k // 128) * 128 + (k % 16) * 8 + (k % 128) // 16]
+    ref = oracle.attention(qr, k_ref, v_ref, rows, H, G, 128, 0).reshape(rows, H * 128)
+    g = oracle.f32_from_bf16(nat).astype(np.float64)
+    r = oracle.f32_from_bf16(ref).astype(np.float64)
+    assert np.mean(g == r) > 0.999
+    assert np.all(np.abs(g - r) <= 2 * bf16_ulp(r) + 1e-4)
+
+
+def test_prefill_then_decode_continues(prefill_model):
+    """A different prompt after a prefill runs the exact path from 0; the
+    same prompt resumes after the prefilled positions."""
+    from dolittle_amd.qwen3 import Plan
+    prompt = list(range(1000, 1000 + 130))
+    plan = Plan(prefill_model, batch=2, capacity=160)
+    plan.prefill(prompt)
+    plan.generate(prompt, 6)
+    t1, res = plan.collect()
+    assert all(r["generated"] == 6 and r["position"] == 136 for r in res)
+    assert t1[0].tolist() == t1[1].tolist()
+    other = list(range(2000, 2000 + 20))
+    plan.generate(other, 3)
+    _, res2 = plan.collect()
+    assert res2[0]["position"] == 23
