@@ -26,6 +26,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense BF16 MFMA, MI355X
 METRIC = "Qwen3-8B batch-1 decode tokens/s on 1 MI355X; % HBM roofline; prefill tok/s"
 
 
@@ -118,6 +119,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--kernel-iters", type=int, default=72)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mfma-prompt", type=int, default=4096,
+                    help="prompt length of the MFMA prefill measurement (0 skips it)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (PMC scaling reference)")
     args = ap.parse_args()
@@ -210,6 +213,36 @@ def main() -> int:
         queue.copy(b, a, n)
         queue.drain()
 
+    # BASELINE config 3's prompt pass on the MFMA prefill path (tolerance
+    # path, not bit-exact): 4096 prompt ids, positions 0..4094 as GEMMs.
+    mfma = None
+    if args.mfma_prompt:
+        n = args.mfma_prompt
+        pplan = Plan(model, batch=1, capacity=n + 512)
+        long_prompt = np.random.default_rng(args.seed + 3).integers(0, cfg.vocab, n).astype(np.uint32)
+        pplan.prefill(long_prompt)  # warm (allocates the row buffers)
+        queue.drain()
+        runs = 3
+        ea, eb = Event(device), Event(device)
+        ea.record(queue)
+        for _ in range(runs):
+            pplan.prefill(long_prompt)
+        eb.record(queue)
+        queue.drain()
+        ms = ea.elapsed_ms(eb) / runs
+        rows = n - 1
+        proj = 2 * rows * cfg.layers * (cfg.hidden * (cfg.q_heads + 2 * cfg.kv_heads) * cfg.head_dim
+                                        + cfg.q_heads * cfg.head_dim * cfg.hidden + 3 * cfg.hidden * cfg.ffn)
+        pairs = rows * (rows + 1) // 2
+        attn = 4 * pairs * cfg.head_dim * cfg.q_heads * cfg.layers
+        tflops = (proj + attn) / (ms * 1e-3) / 1e12
+        mfma = {"prompt": n, "positions": rows, "ms": round(ms, 2), "tokens_per_s": round(rows / (ms * 1e-3), 1),
+                "flop": proj + attn, "achieved_tflops": round(tflops, 1), "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+                "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                "parity": "tolerance (MFMA accumulation order); the exact path is prefill_tokens_per_s"}
+        log(f"MFMA prefill {rows} positions in {ms:.1f} ms = {rows / (ms * 1e-3):.0f} tok/s, "
+            f"{tflops:.0f} TFLOP/s ({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of BF16 peak)")
+
     cpu = None
     if not args.no_cpu_baseline:
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
@@ -238,6 +271,7 @@ def main() -> int:
             "parallelism": "single-gpu",
         },
         "prefill_tokens_per_s": round(args.prompt / (prefill_ms * 1e-3), 1),
+        "prefill_mfma": mfma,
         "hbm_roofline_step": {"bytes_per_step": int(bytes_step), "achieved_GBs": round(step_gbs, 1),
                               "peak_GBs": HBM_PEAK_GBS, "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "roofline": {
