@@ -119,6 +119,9 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--kernel-iters", type=int, default=72)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-driver", action="store_true",
+                    help="only launch k_gateup 20 times and copy 256 MiB three times "
+                         "(the program run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--mfma-prompt", type=int, default=4096,
                     help="prompt length of the MFMA prefill measurement (0 skips it)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -134,6 +137,23 @@ def main() -> int:
 
     device = Device(0)
     queue = device.create_queue()
+    if args.traffic_driver:
+        # The gate/up kernel is identical in every block; two blocks and a
+        # short vocabulary keep the counter runs short.
+        small = Qwen3Model(device, queue, Qwen3Config(layers=2, vocab=2048))
+        small.fill_synthetic(args.seed, 0.02)
+        tplan = Plan(small, batch=1, capacity=256)
+        tplan.generate(list(range(10, 40)), 2)
+        tplan.collect()
+        _lib.call("dl_plan_bench_prepare", tplan.handle)
+        _lib.call("dl_plan_launch_kernel", tplan.handle, 5, 0, 20)
+        n = 256 << 20
+        a, b = device.allocate(n), device.allocate(n)
+        for _ in range(3):
+            queue.copy(b, a, n)
+        queue.drain()
+        log("traffic driver done")
+        return 0
     cfg = Qwen3Config()
     t0 = time.perf_counter()
     model = Qwen3Model(device, queue, cfg)
