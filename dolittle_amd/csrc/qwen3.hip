@@ -435,7 +435,7 @@ constexpr int kFusedKeys = 1024;
 constexpr int kAttnThreads = 512;
 constexpr int kAttnKeysPerPass = kAttnThreads / 8;
 constexpr int kAttnKeyPasses = 8;     // key rows issued at kernel entry: 512 keys
-constexpr int kAttnValueBlocks = 16;  // 8-key V blocks per PV chain issued at entry
+constexpr int kAttnValueBlocks = 8;  // 8-key V blocks per PV chain issued at entry
 
 __global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
   __shared__ float qs[kHeadDim];
