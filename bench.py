@@ -46,12 +46,98 @@ def kernel_bytes(cfg, which):
     }[which]
 
 
-def step_bytes(cfg, context):
-    """SURVEY 8(d) algorithmic bytes of one batch-1 decode step with `context`
-    visible keys: projection weights incl. LM head, norm gains, embedding
-    row, KV read and append, BF16 logits."""
-    return (cfg.projection_bytes_per_token() + (cfg.layers * (2 * cfg.hidden + 2 * cfg.head_dim) + cfg.hidden) * 2
-            + cfg.hidden * 2 + cfg.layers * 2 * cfg.kv_heads * cfg.head_dim * 2 * (context + 1) + cfg.vocab * 2)
+def step_bytes(cfg, context, batch=1):
+    """Algorithmic bytes of one decode step of `batch` sequences with
+    `context` visible keys each: projection weights incl. LM head and norm
+    gains (read once per step), and per sequence the embedding row, KV read
+    and append, and the BF16 logits row."""
+    weights = cfg.projection_bytes_per_token() + (cfg.layers * (2 * cfg.hidden + 2 * cfg.head_dim) + cfg.hidden) * 2
+    per_seq = cfg.hidden * 2 + cfg.layers * 2 * cfg.kv_heads * cfg.head_dim * 2 * (context + 1) + cfg.vocab * 2
+    return weights + batch * per_seq
+
+
+def bf16_bits(x):
+    """Round-to-nearest-even BF16 bits of float32 values."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def timed_loop(device, queue, plan, prompt, max_new, consume_steps, sampling=None, seeds=None):
+    """Runs one device-owned generation: `consume_steps` steps take the
+    prompt (and select token 1), then tokens 2..max_new are timed with HIP
+    events on the plan's stream; returns (ms per step, tokens, results)."""
+    from dolittle_amd import Event
+    plan.prepare_generation(prompt, max_new, sampling, seeds)
+    plan.decode_steps(consume_steps)
+    queue.drain()
+    ea, eb = Event(device), Event(device)
+    ea.record(queue)
+    plan.decode_steps(max_new - 1)
+    eb.record(queue)
+    queue.drain()
+    plan.decode_steps(1)
+    tokens, results = plan.collect()
+    assert all(r["generated"] == max_new for r in results), results
+    return ea.elapsed_ms(eb) / (max_new - 1), tokens, results
+
+
+def other_configs(device, queue, model, cfg, seed, pplan, long_prompt):
+    """Decode-side measurements of BASELINE configs 3, 4 and 5 (the token
+    loop as the bench's main line runs it, at their batch and context)."""
+    from dolittle_amd.qwen3 import Plan, SamplingSettings
+    out = {}
+    if pplan is not None:
+        # Config 3: greedy decode of 512 tokens after the MFMA prefill of a
+        # 4096-id prompt; visible keys grow from 4097 to 4607.
+        n, max_new = len(long_prompt), 512
+        pplan.prefill(long_prompt)
+        ms, _, _ = timed_loop(device, queue, pplan, long_prompt, max_new, 1)
+        mean_ctx = n + 1 + (max_new - 2) / 2.0
+        gbs = step_bytes(cfg, mean_ctx) / (ms * 1e-3) / 1e9
+        out["config3_decode"] = {"prompt": n, "new_tokens": max_new, "timed_positions": [n + 1, n + max_new - 1],
+                                 "ms_per_step": round(ms, 4), "tokens_per_s": round(1000.0 / ms, 2),
+                                 "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"config 3: decode at {n + 1}..{n + max_new - 1} keys {ms * 1e3:.1f} us/token = {1000.0 / ms:.1f} tok/s "
+            f"({gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+
+    # Config 4: batch 2, 256-id prompt, 256 tokens; plain, then capture of
+    # block 24 at every position for both sequences plus an FP32 steering
+    # vector (unit N(0,1) direction x 8.0) added at block 24 of sequence 1.
+    rng = np.random.default_rng(seed + 4)
+    prompt4 = rng.integers(0, cfg.vocab, 256).astype(np.uint32)
+    plan4 = Plan(model, batch=2, capacity=256 + 256 + 2)
+    plain_ms, _, _ = timed_loop(device, queue, plan4, prompt4, 256, 256)
+    u = rng.standard_normal(cfg.hidden)
+    steer = (8.0 * u / np.linalg.norm(u)).astype(np.float32)
+    plan4.set_capture(24)
+    plan4.set_steering(1, 24, steer)
+    hook_ms, _, _ = timed_loop(device, queue, plan4, prompt4, 256, 256)
+    del plan4
+    ctx4 = 256 + 1 + 254 / 2.0
+    out["config4_capture_steering"] = {
+        "batch": 2, "prompt": 256, "new_tokens": 256, "plain_ms_per_step": round(plain_ms, 4),
+        "hooked_ms_per_step": round(hook_ms, 4), "overhead_frac": round(hook_ms / plain_ms - 1.0, 4),
+        "tokens_per_s": round(2000.0 / hook_ms, 2),
+        "hbm_frac": round(step_bytes(cfg, ctx4, 2) / (hook_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    log(f"config 4: batch 2 plain {plain_ms * 1e3:.1f} us/step, capture+steering {hook_ms * 1e3:.1f} us/step "
+        f"({hook_ms / plain_ms - 1.0:+.2%})")
+
+    # Config 5: batch 8 over one 192-id prefix with a BF16 N(0,1) x 40 row
+    # replacing the embedding at position 96 of every sequence; 128 tokens
+    # each, temperature 1.0, top-p 0.95, per-sequence MT19937-64 seeds.
+    prompt5 = rng.integers(0, cfg.vocab, 192).astype(np.uint32)
+    plan5 = Plan(model, batch=8, capacity=192 + 128 + 2)
+    plan5.set_embedding_override(96, bf16_bits(40.0 * rng.standard_normal(cfg.hidden)), 0xFF)
+    sampling = SamplingSettings("categorical", 1.0, 0, 0.95)
+    ms5, _, _ = timed_loop(device, queue, plan5, prompt5, 128, 192, sampling, list(range(8)))
+    del plan5
+    ctx5 = 192 + 1 + 126 / 2.0
+    out["config5_topp_batch8"] = {
+        "batch": 8, "prompt": 192, "new_tokens": 128, "temperature": 1.0, "top_p": 0.95,
+        "ms_per_step": round(ms5, 4), "tokens_per_s": round(8000.0 / ms5, 2),
+        "hbm_frac": round(step_bytes(cfg, ctx5, 8) / (ms5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    log(f"config 5: batch 8 top-p {ms5 * 1e3:.1f} us/step = {8000.0 / ms5:.1f} tok/s")
+    return out
 
 
 def cpu_baseline(model, plan, context, threads):
@@ -124,6 +210,8 @@ def main() -> int:
                          "(the program run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--mfma-prompt", type=int, default=4096,
                     help="prompt length of the MFMA prefill measurement (0 skips it)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the decode measurements of configs 3 (4.6K context), 4 and 5")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (PMC scaling reference)")
     args = ap.parse_args()
@@ -235,10 +323,10 @@ def main() -> int:
 
     # BASELINE config 3's prompt pass on the MFMA prefill path (tolerance
     # path, not bit-exact): 4096 prompt ids, positions 0..4094 as GEMMs.
-    mfma = None
+    mfma, pplan, long_prompt = None, None, None
     if args.mfma_prompt:
         n = args.mfma_prompt
-        pplan = Plan(model, batch=1, capacity=n + 512)
+        pplan = Plan(model, batch=1, capacity=n + 512 + 1)
         long_prompt = np.random.default_rng(args.seed + 3).integers(0, cfg.vocab, n).astype(np.uint32)
         pplan.prefill(long_prompt)  # warm (allocates the row buffers)
         queue.drain()
@@ -262,6 +350,11 @@ def main() -> int:
                 "parity": "tolerance (MFMA accumulation order); the exact path is prefill_tokens_per_s"}
         log(f"MFMA prefill {rows} positions in {ms:.1f} ms = {rows / (ms * 1e-3):.0f} tok/s, "
             f"{tflops:.0f} TFLOP/s ({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of BF16 peak)")
+
+    others = {}
+    if not args.no_other_configs:
+        others = other_configs(device, queue, model, cfg, args.seed, pplan, long_prompt)
+        del pplan
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -306,6 +399,7 @@ def main() -> int:
             "avg_launch_us": dominant["us"],
         },
         "kernels": kernels,
+        "other_configs": others,
         "idle_step_graph_us": round(idle_us, 2),
         "cpu_baseline": cpu,
     }

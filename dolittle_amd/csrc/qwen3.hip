@@ -353,10 +353,14 @@ __global__ __launch_bounds__(kBlock) void k_attn_qk(AttnArgs a) {
 
 // Grid (query head, sequence).  m = max, e = exp(s - m), denominator from 32
 // partials owning j mod 32 merged at offsets 16..1, p = e / l
-// (attention.cu:301-330).
+// (attention.cu:301-330).  Each thread issues its score loads 16 at a time
+// before using any (indices clamped to the last key, which leaves the max
+// unchanged), and each partial reads its keys from LDS 16 at a time.
+constexpr int kSoftmaxChunk = 16;
+
 __global__ __launch_bounds__(kBlock) void k_attn_softmax(AttnArgs a) {
   extern __shared__ float es[];
-  __shared__ float red[kBlock];
+  __shared__ float wave_max[kBlock / 64];
   __shared__ float denominator_shared;
   if (!a.ctl->active) return;
   const int count = static_cast<int>(a.ctl->position) + 1;
@@ -364,19 +368,36 @@ __global__ __launch_bounds__(kBlock) void k_attn_softmax(AttnArgs a) {
   const uint64_t row = (static_cast<uint64_t>(b) * a.q_heads + h) * a.cap;
   const float* sc = a.scores + row;
   float m = sc[0];
-  for (int j = tid; j < count; j += kBlock) m = fmaxf(m, sc[j]);
-  red[tid] = m;
-  __syncthreads();
-  for (int off = kBlock / 2; off; off >>= 1) {
-    if (tid < off) red[tid] = fmaxf(red[tid], red[tid + off]);
-    __syncthreads();
+  for (int base = 0; base < count; base += kBlock * kSoftmaxChunk) {
+    float s[kSoftmaxChunk];
+#pragma unroll
+    for (int i = 0; i < kSoftmaxChunk; ++i) s[i] = sc[min(base + tid + i * kBlock, count - 1)];
+#pragma unroll
+    for (int i = 0; i < kSoftmaxChunk; ++i) {
+      m = fmaxf(m, s[i]);
+      const int j = base + tid + i * kBlock;
+      if (j < count) es[j] = s[i];
+    }
   }
-  m = red[0];
-  for (int j = tid; j < count; j += kBlock) es[j] = dl_expf(sc[j] - m);
+#pragma unroll
+  for (int off = 32; off; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if (tid % 64 == 0) wave_max[tid / 64] = m;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kBlock / 64; ++w) m = fmaxf(m, wave_max[w]);
+  for (int j = tid; j < count; j += kBlock) es[j] = dl_expf(es[j] - m);
   __syncthreads();
   if (tid < 32) {
     float p = 0.0f;
-    for (int j = tid; j < count; j += 32) p = p + es[j];
+    int j = tid;
+    for (; j + 32 * (kSoftmaxChunk - 1) < count; j += 32 * kSoftmaxChunk) {
+      float e[kSoftmaxChunk];
+#pragma unroll
+      for (int i = 0; i < kSoftmaxChunk; ++i) e[i] = es[j + 32 * i];
+#pragma unroll
+      for (int i = 0; i < kSoftmaxChunk; ++i) p = p + e[i];
+    }
+    for (; j < count; j += 32) p = p + es[j];
 #pragma unroll
     for (int off = 16; off; off >>= 1) p = p + __shfl_down(p, off, 32);
     if (tid == 0) denominator_shared = p;
@@ -386,42 +407,123 @@ __global__ __launch_bounds__(kBlock) void k_attn_softmax(AttnArgs a) {
   for (int j = tid; j < count; j += kBlock) a.probs[row + j] = es[j] / l;
 }
 
-// Grid (kv head * 16 feature blocks, sequence); one wavefront: lane =
-// (head in group, key half, feature).  Each output feature is
-// round(A + B), A and B ascending FMA chains over the first ceil(n/2) keys
-// and the rest (attention.cu:331-375).  V is stored transposed so a lane
-// reads 8 consecutive keys of its feature per 16-byte load.
-__global__ __launch_bounds__(64) void k_attn_pv(AttnArgs a) {
+// Grid (kv head * 8 feature blocks, sequence), 192 threads.  Waves 0 and 1
+// run the two PV key ranges (the first ceil(n/2) keys and the rest) for the
+// group's 4 query heads x 16 features, lane = (head, feature); each output
+// feature is round(A + B), A and B ascending FMA chains (attention.cu:331-375).
+// V is stored transposed, so a lane reads 8 consecutive keys of its feature
+// per 16-byte load, 64 keys ahead of the FMAs.  Wave 2 first touches every V
+// row and probability row the chains read, so their loads hit L2 instead of
+// waiting on HBM one block at a time.
+constexpr int kPvFeatures = 16;
+constexpr int kPvThreads = 192;
+
+__global__ __launch_bounds__(kPvThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_attn_pv(AttnArgs a) {
+  __shared__ float second[64];
   if (!a.ctl->active) return;
   const int count = static_cast<int>(a.ctl->position) + 1;
   const int split = (count - 1) / 2 + 1;
-  const int g = blockIdx.x / 16, fb = blockIdx.x % 16, b = blockIdx.y;
-  const int lane = threadIdx.x;
-  const int hl = lane / 16, half = (lane / 8) % 2, fl = lane % 8;
+  constexpr int kBlocksPerHead = kHeadDim / kPvFeatures;
+  const int g = blockIdx.x / kBlocksPerHead, fb = blockIdx.x % kBlocksPerHead, b = blockIdx.y;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int group = a.q_heads / a.kv_heads;
-  const int h = g * group + hl, f = fb * 8 + fl;
-  const float* p = a.probs + (static_cast<uint64_t>(b) * a.q_heads + h) * a.cap;
-  const uint16_t* v = a.v_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g * kHeadDim + f) * a.cap;
-  const int begin = half ? split : 0, end = half ? count : split;
+  const uint16_t* vbase =
+      a.v_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g * kHeadDim + fb * kPvFeatures) * a.cap;
+  const float* pbase = a.probs + (static_cast<uint64_t>(b) * a.q_heads + g * group) * a.cap;
   float acc = 0.0f;
-  int j = begin;
-  for (; j < end && (j & 7); ++j) acc = fma_rn(p[j], dl_bf16_to_f32(v[j]), acc);
-  for (; j + 8 <= end; j += 8) {
-    const u32x4 vv = *reinterpret_cast<const u32x4*>(v + j);
-    const float4 pa = *reinterpret_cast<const float4*>(p + j);
-    const float4 pb = *reinterpret_cast<const float4*>(p + j + 4);
-    acc = fma_rn(pa.x, dl_bf16_lo(vv.x), acc);
-    acc = fma_rn(pa.y, dl_bf16_hi(vv.x), acc);
-    acc = fma_rn(pa.z, dl_bf16_lo(vv.y), acc);
-    acc = fma_rn(pa.w, dl_bf16_hi(vv.y), acc);
-    acc = fma_rn(pb.x, dl_bf16_lo(vv.z), acc);
-    acc = fma_rn(pb.y, dl_bf16_hi(vv.z), acc);
-    acc = fma_rn(pb.z, dl_bf16_lo(vv.w), acc);
-    acc = fma_rn(pb.w, dl_bf16_hi(vv.w), acc);
+  if (wave == 2) {
+    // One dword per 128-byte line of the 16 V rows and 4 probability rows.
+    const int v_lines = (count * 2 + 127) / 128, p_lines = (count * 4 + 127) / 128;
+    const int v_total = kPvFeatures * v_lines, total = v_total + group * p_lines;
+    uint32_t x = 0;
+    for (int i = lane; i < total; i += 64 * 8) {
+      uint32_t t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = min(i + u * 64, total - 1);
+        const uint32_t* src =
+            k < v_total ? reinterpret_cast<const uint32_t*>(vbase + static_cast<uint64_t>(k / v_lines) * a.cap) +
+                              (k % v_lines) * 32
+                        : reinterpret_cast<const uint32_t*>(pbase + static_cast<uint64_t>((k - v_total) / p_lines) *
+                                                                        a.cap) +
+                              ((k - v_total) % p_lines) * 32;
+        t[u] = *src;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x ^= t[u];
+    }
+    asm volatile("" ::"v"(x));
+  } else {
+    const int hl = lane / kPvFeatures, f = lane % kPvFeatures;
+    const uint16_t* v = vbase + static_cast<uint64_t>(f) * a.cap;
+    const float* p = pbase + static_cast<uint64_t>(hl) * a.cap;
+    const int begin = wave ? split : 0, end = wave ? count : split;
+    int j = begin;
+    for (; j < end && (j & 7); ++j) acc = fma_rn(p[j], dl_bf16_to_f32(v[j]), acc);
+    if (j + 64 <= end) {
+      // Two register buffers of 64 keys: the loads of one are issued before
+      // the FMAs over the other (the scheduling barriers keep them there).
+      u32x4 va[8], vb[8];
+      float4 pa[16], pb[16];
+      auto load = [&](u32x4* vd, float4* pd, int j0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vd[i] = *reinterpret_cast<const u32x4*>(v + j0 + 8 * i);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) pd[i] = *reinterpret_cast<const float4*>(p + j0 + 4 * i);
+      };
+      auto consume = [&](const u32x4* vc, const float4* pc) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float4 lo = pc[2 * i], hi = pc[2 * i + 1];
+          acc = fma_rn(lo.x, dl_bf16_lo(vc[i].x), acc);
+          acc = fma_rn(lo.y, dl_bf16_hi(vc[i].x), acc);
+          acc = fma_rn(lo.z, dl_bf16_lo(vc[i].y), acc);
+          acc = fma_rn(lo.w, dl_bf16_hi(vc[i].y), acc);
+          acc = fma_rn(hi.x, dl_bf16_lo(vc[i].z), acc);
+          acc = fma_rn(hi.y, dl_bf16_hi(vc[i].z), acc);
+          acc = fma_rn(hi.z, dl_bf16_lo(vc[i].w), acc);
+          acc = fma_rn(hi.w, dl_bf16_hi(vc[i].w), acc);
+        }
+      };
+      load(va, pa, j);
+      for (;;) {
+        // Blocks past the range reload the current one (never consumed).
+        load(vb, pb, j + 128 <= end ? j + 64 : j);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(va, pa);
+        __builtin_amdgcn_sched_barrier(0);
+        j += 64;
+        if (j + 64 > end) break;
+        load(va, pa, j + 128 <= end ? j + 64 : j);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(vb, pb);
+        __builtin_amdgcn_sched_barrier(0);
+        j += 64;
+        if (j + 64 > end) break;
+      }
+    }
+    for (; j + 8 <= end; j += 8) {
+      const u32x4 vv = *reinterpret_cast<const u32x4*>(v + j);
+      const float4 pa = *reinterpret_cast<const float4*>(p + j);
+      const float4 pb = *reinterpret_cast<const float4*>(p + j + 4);
+      acc = fma_rn(pa.x, dl_bf16_lo(vv.x), acc);
+      acc = fma_rn(pa.y, dl_bf16_hi(vv.x), acc);
+      acc = fma_rn(pa.z, dl_bf16_lo(vv.y), acc);
+      acc = fma_rn(pa.w, dl_bf16_hi(vv.y), acc);
+      acc = fma_rn(pb.x, dl_bf16_lo(vv.z), acc);
+      acc = fma_rn(pb.y, dl_bf16_hi(vv.z), acc);
+      acc = fma_rn(pb.z, dl_bf16_lo(vv.w), acc);
+      acc = fma_rn(pb.w, dl_bf16_hi(vv.w), acc);
+    }
+    for (; j < end; ++j) acc = fma_rn(p[j], dl_bf16_to_f32(v[j]), acc);
+    if (wave == 1) second[lane] = acc;
   }
-  for (; j < end; ++j) acc = fma_rn(p[j], dl_bf16_to_f32(v[j]), acc);
-  const float other = __shfl_down(acc, 8, 16);
-  if (half == 0) a.att[static_cast<uint64_t>(b) * a.q_heads * kHeadDim + h * kHeadDim + f] = bf16_bits(acc + other);
+  __syncthreads();
+  if (wave == 0) {
+    const int hl = lane / kPvFeatures, f = lane % kPvFeatures;
+    a.att[static_cast<uint64_t>(b) * a.q_heads * kHeadDim + (g * group + hl) * kHeadDim + fb * kPvFeatures + f] =
+        bf16_bits(acc + second[lane]);
+  }
 }
 
 // Short-context attention in one kernel (the reference's retained-score
@@ -1418,7 +1520,7 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       break;
     case 1: k_attn_qk<<<dim3(c.kv_heads, p->cap / 64, B), kBlock, 0, s>>>(aa); break;
     case 2: k_attn_softmax<<<dim3(c.q_heads, B), kBlock, size_t(p->cap) * sizeof(float), s>>>(aa); break;
-    case 3: k_attn_pv<<<dim3(c.kv_heads * 16, B), 64, 0, s>>>(aa); break;
+    case 3: k_attn_pv<<<dim3(c.kv_heads * (kHeadDim / kPvFeatures), B), kPvThreads, 0, s>>>(aa); break;
     case 8: k_attn_fused<<<dim3(c.q_heads, B), kAttnThreads, 0, s>>>(aa); break;
     case 4:
       for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {

@@ -125,15 +125,17 @@ def test_config1_single_block_decode(device, queue, oracle):
     assert np.array_equal(plan.logits(0), oracle.logits(w, run.h))
 
 
-@pytest.mark.parametrize("position", [77, 1023, 1024, 1500])
+@pytest.mark.parametrize("position", [77, 1023, 1024, 1500, 1543, 4607])
 def test_single_block_both_attention_paths(device, queue, oracle, position):
     """Positions below 1024 run the fused short-context attention kernel,
-    positions from 1024 the three-kernel split; both equal the oracle."""
+    positions from 1024 the three-kernel split; both equal the oracle, up to
+    BASELINE config 3's last decode position (4607)."""
     from dolittle_amd.qwen3 import Plan, Qwen3Model
     model = Qwen3Model(device, queue, qwen_config(layers=1, vocab=2048))
     model.fill_synthetic(SEED + 7, 0.02)
     w = oracle_weights(oracle, model)
-    plan = Plan(model, batch=1, capacity=1600)
+    capacity = max(1600, position + 1)
+    plan = Plan(model, batch=1, capacity=capacity)
     kw = 8 * 128
     keys = oracle.normal_bf16(position * kw, SEED + 3, 2000, 1.0)
     values = oracle.normal_bf16(position * kw, SEED + 3, 2001, 1.0)
@@ -142,7 +144,7 @@ def test_single_block_both_attention_paths(device, queue, oracle, position):
     plan.set_embedding_override(position, x, 1)
     plan.seek(position)
     plan.forward([0])
-    run = OracleRun(oracle, w, 1600)
+    run = OracleRun(oracle, w, capacity)
     run.k[0][: position * kw] = keys
     run.v[0][: position * kw] = values
     run.pos = position
