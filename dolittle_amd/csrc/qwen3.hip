@@ -27,6 +27,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <utility>
 #include <vector>
 
 #include "dl_control.h"
@@ -407,25 +408,72 @@ __global__ __launch_bounds__(kBlock) void k_attn_softmax(AttnArgs a) {
   for (int j = tid; j < count; j += kBlock) a.probs[row + j] = es[j] / l;
 }
 
+// One PV key of a 64-key block: acc = fma(p, v, acc) with v the BF16 value
+// of key K of this lane's feature and p the probability of key K of this
+// lane's head.  The 16 lanes of a head (one DPP row) hold the block's 64
+// probabilities, 4 per lane; row_newbcast reads lane K / 4 of the row as the
+// multiplicand, so the product needs no separate broadcast instruction.
+// v_fmac_f32 rounds once (fused), as fma_rn does.
+template <int C>
+__device__ inline float pick(const float4& x) {
+  if constexpr (C == 0) return x.x;
+  else if constexpr (C == 1) return x.y;
+  else if constexpr (C == 2) return x.z;
+  else return x.w;
+}
+template <int C>
+__device__ inline uint32_t pick(const u32x4& x) {
+  if constexpr (C == 0) return x.x;
+  else if constexpr (C == 1) return x.y;
+  else if constexpr (C == 2) return x.z;
+  else return x.w;
+}
+template <int K>
+__device__ inline float pv_key(float acc, const float4& pc, const u32x4* vc) {
+  const uint32_t word = pick<(K % 8) / 2>(vc[K / 8]);
+  const float v = (K % 2) ? dl_bf16_hi(word) : dl_bf16_lo(word);
+  asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+               : "+v"(acc)
+               : "v"(pick<K % 4>(pc)), "v"(v), "n"(K / 4));
+  return acc;
+}
+// The keys lo <= K < hi of a block (all 64 unless kMasked: the first and
+// last block of a range).
+template <bool kMasked, int... K>
+__device__ inline float pv_block(float acc, const float4& pc, const u32x4* vc, int lo, int hi,
+                                 std::integer_sequence<int, K...>) {
+  // Two wait states between any VALU write of the probability registers and
+  // their first DPP read.
+  asm volatile("s_nop 1");
+  ((acc = (!kMasked || (K >= lo && K < hi)) ? pv_key<K>(acc, pc, vc) : acc), ...);
+  return acc;
+}
+
 // Grid (kv head * 8 feature blocks, sequence), 192 threads.  Waves 0 and 1
 // run the two PV key ranges (the first ceil(n/2) keys and the rest) for the
 // group's 4 query heads x 16 features, lane = (head, feature); each output
 // feature is round(A + B), A and B ascending FMA chains (attention.cu:331-375).
 // V is stored transposed, so a lane reads 8 consecutive keys of its feature
-// per 16-byte load, 64 keys ahead of the FMAs.  Wave 2 first touches every V
-// row and probability row the chains read, so their loads hit L2 instead of
-// waiting on HBM one block at a time.
+// per 16-byte load; loads run 3 blocks of 64 keys ahead of the FMAs (the
+// range's unaligned ends are masked blocks of the same pipeline), and one
+// float4 per lane carries its head's 64 probabilities of a block.  Wave 2
+// first touches every V row and probability row the chains read, so the
+// chains' loads hit L2 instead of waiting on HBM.
 constexpr int kPvFeatures = 16;
 constexpr int kPvThreads = 192;
+constexpr int kPvTouchBatch = 32;
+constexpr int kPvBuffers = 4;
 
 __global__ __launch_bounds__(kPvThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_attn_pv(AttnArgs a) {
   __shared__ float second[64];
   if (!a.ctl->active) return;
   const int count = static_cast<int>(a.ctl->position) + 1;
   const int split = (count - 1) / 2 + 1;
-  constexpr int kBlocksPerHead = kHeadDim / kPvFeatures;
-  const int g = blockIdx.x / kBlocksPerHead, fb = blockIdx.x % kBlocksPerHead, b = blockIdx.y;
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  constexpr int kBlocksPerGroup = kHeadDim / kPvFeatures;
+  const int g = blockIdx.x / kBlocksPerGroup, fb = blockIdx.x % kBlocksPerGroup, b = blockIdx.y;
+  // Wave-uniform wave index: the key ranges and loop bounds below stay in
+  // scalar registers, so the loops branch on scalars.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
   const int group = a.q_heads / a.kv_heads;
   const uint16_t* vbase =
       a.v_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g * kHeadDim + fb * kPvFeatures) * a.cap;
@@ -436,10 +484,10 @@ __global__ __launch_bounds__(kPvThreads) __attribute__((amdgpu_waves_per_eu(1, 2
     const int v_lines = (count * 2 + 127) / 128, p_lines = (count * 4 + 127) / 128;
     const int v_total = kPvFeatures * v_lines, total = v_total + group * p_lines;
     uint32_t x = 0;
-    for (int i = lane; i < total; i += 64 * 8) {
-      uint32_t t[8];
+    for (int i = lane; i < total; i += 64 * kPvTouchBatch) {
+      uint32_t t[kPvTouchBatch];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < kPvTouchBatch; ++u) {
         const int k = min(i + u * 64, total - 1);
         const uint32_t* src =
             k < v_total ? reinterpret_cast<const uint32_t*>(vbase + static_cast<uint64_t>(k / v_lines) * a.cap) +
@@ -450,7 +498,7 @@ __global__ __launch_bounds__(kPvThreads) __attribute__((amdgpu_waves_per_eu(1, 2
         t[u] = *src;
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) x ^= t[u];
+      for (int u = 0; u < kPvTouchBatch; ++u) x ^= t[u];
     }
     asm volatile("" ::"v"(x));
   } else {
@@ -458,64 +506,51 @@ __global__ __launch_bounds__(kPvThreads) __attribute__((amdgpu_waves_per_eu(1, 2
     const uint16_t* v = vbase + static_cast<uint64_t>(f) * a.cap;
     const float* p = pbase + static_cast<uint64_t>(hl) * a.cap;
     const int begin = wave ? split : 0, end = wave ? count : split;
-    int j = begin;
-    for (; j < end && (j & 7); ++j) acc = fma_rn(p[j], dl_bf16_to_f32(v[j]), acc);
-    if (j + 64 <= end) {
-      // Two register buffers of 64 keys: the loads of one are issued before
-      // the FMAs over the other (the scheduling barriers keep them there).
-      u32x4 va[8], vb[8];
-      float4 pa[16], pb[16];
-      auto load = [&](u32x4* vd, float4* pd, int j0) {
+    // Blocks of 64 keys from the 8-aligned key below `begin`; the first and
+    // last block mask the keys outside [begin, end).  Loads past the range
+    // are clamped to its last 8-key group (last 4 keys for probabilities),
+    // which stays inside the row because the capacity is a multiple of 64;
+    // their values are never used.
+    const int jb0 = begin & ~7;
+    const int blocks = end > begin ? (end - jb0 + 63) / 64 : 0;
+    if (blocks > 0) {
+      const int last8 = (end - 1) & ~7, last4 = (end - 1) & ~3;
+      u32x4 vbuf[kPvBuffers][8];
+      float4 pbuf[kPvBuffers];
+      auto load = [&](int buf, int x) {
+        const int jb = jb0 + 64 * min(x, blocks - 1);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vd[i] = *reinterpret_cast<const u32x4*>(v + j0 + 8 * i);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) pd[i] = *reinterpret_cast<const float4*>(p + j0 + 4 * i);
+        for (int i = 0; i < 8; ++i) vbuf[buf][i] = *reinterpret_cast<const u32x4*>(v + min(jb + 8 * i, last8));
+        pbuf[buf] = *reinterpret_cast<const float4*>(p + min(jb + 4 * f, last4));
       };
-      auto consume = [&](const u32x4* vc, const float4* pc) {
+      const auto keys = std::make_integer_sequence<int, 64>{};
+      auto run = [&](int buf, int x) {
+        const int jb = jb0 + 64 * x;
+        const int lo = max(begin - jb, 0), hi = min(end - jb, 64);
+        if (lo == 0 && hi == 64)
+          acc = pv_block<false>(acc, pbuf[buf], vbuf[buf], lo, hi, keys);
+        else
+          acc = pv_block<true>(acc, pbuf[buf], vbuf[buf], lo, hi, keys);
+      };
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float4 lo = pc[2 * i], hi = pc[2 * i + 1];
-          acc = fma_rn(lo.x, dl_bf16_lo(vc[i].x), acc);
-          acc = fma_rn(lo.y, dl_bf16_hi(vc[i].x), acc);
-          acc = fma_rn(lo.z, dl_bf16_lo(vc[i].y), acc);
-          acc = fma_rn(lo.w, dl_bf16_hi(vc[i].y), acc);
-          acc = fma_rn(hi.x, dl_bf16_lo(vc[i].z), acc);
-          acc = fma_rn(hi.y, dl_bf16_hi(vc[i].z), acc);
-          acc = fma_rn(hi.z, dl_bf16_lo(vc[i].w), acc);
-          acc = fma_rn(hi.w, dl_bf16_hi(vc[i].w), acc);
+      for (int u = 0; u < kPvBuffers - 1; ++u) load(u, u);
+      // Uniform trip count and one exit: the loop head always has the same
+      // kPvBuffers - 1 blocks outstanding.
+      int k = 0;
+      for (; k + kPvBuffers <= blocks; k += kPvBuffers) {
+#pragma unroll
+        for (int u = 0; u < kPvBuffers; ++u) {
+          load((u + kPvBuffers - 1) % kPvBuffers, k + u + kPvBuffers - 1);
+          __builtin_amdgcn_sched_barrier(0);
+          run(u, k + u);
+          __builtin_amdgcn_sched_barrier(0);
         }
-      };
-      load(va, pa, j);
-      for (;;) {
-        // Blocks past the range reload the current one (never consumed).
-        load(vb, pb, j + 128 <= end ? j + 64 : j);
-        __builtin_amdgcn_sched_barrier(0);
-        consume(va, pa);
-        __builtin_amdgcn_sched_barrier(0);
-        j += 64;
-        if (j + 64 > end) break;
-        load(va, pa, j + 128 <= end ? j + 64 : j);
-        __builtin_amdgcn_sched_barrier(0);
-        consume(vb, pb);
-        __builtin_amdgcn_sched_barrier(0);
-        j += 64;
-        if (j + 64 > end) break;
       }
+      // Fewer than kPvBuffers blocks remain, already in buffers 0, 1, ...
+#pragma unroll
+      for (int u = 0; u < kPvBuffers - 1; ++u)
+        if (k + u < blocks) run(u, k + u);
     }
-    for (; j + 8 <= end; j += 8) {
-      const u32x4 vv = *reinterpret_cast<const u32x4*>(v + j);
-      const float4 pa = *reinterpret_cast<const float4*>(p + j);
-      const float4 pb = *reinterpret_cast<const float4*>(p + j + 4);
-      acc = fma_rn(pa.x, dl_bf16_lo(vv.x), acc);
-      acc = fma_rn(pa.y, dl_bf16_hi(vv.x), acc);
-      acc = fma_rn(pa.z, dl_bf16_lo(vv.y), acc);
-      acc = fma_rn(pa.w, dl_bf16_hi(vv.y), acc);
-      acc = fma_rn(pb.x, dl_bf16_lo(vv.z), acc);
-      acc = fma_rn(pb.y, dl_bf16_hi(vv.z), acc);
-      acc = fma_rn(pb.z, dl_bf16_lo(vv.w), acc);
-      acc = fma_rn(pb.w, dl_bf16_hi(vv.w), acc);
-    }
-    for (; j < end; ++j) acc = fma_rn(p[j], dl_bf16_to_f32(v[j]), acc);
     if (wave == 1) second[lane] = acc;
   }
   __syncthreads();
