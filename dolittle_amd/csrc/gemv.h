@@ -57,13 +57,16 @@ __device__ __forceinline__ void stage_put(float* xs, int I, int b, int i, float 
 // Stages BF16 rows [b0, b0 + R) of x (width I) into the P-partial layout.
 // Each thread moves 16-byte chunks; all of a thread's loads are issued
 // before any is consumed.  Requires I % 8 == 0 and I <= 8 * 8 * blockDim.x.
+// `row_stride` (default I) is the distance between source rows, so a block
+// of columns of wider rows can be staged.
 template <int P, class Issue>
 __device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ x, int I, int rows, float* xs,
-                                           Issue&& issue) {
+                                           Issue&& issue, int row_stride = 0) {
   constexpr int kMaxChunks = 8;
   const int chunks = I / 8;
+  const uint64_t stride = row_stride ? row_stride : I;
   for (int b = 0; b < rows; ++b) {
-    const u32x4* src = reinterpret_cast<const u32x4*>(x + static_cast<uint64_t>(b) * I);
+    const u32x4* src = reinterpret_cast<const u32x4*>(x + static_cast<uint64_t>(b) * stride);
     u32x4 v[kMaxChunks];
 #pragma unroll
     for (int j = 0; j < kMaxChunks; ++j) {
@@ -95,6 +98,43 @@ __device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ x, int I
   }
 }
 
+// Stages the columns [0, I) of B BF16 rows (source rows `row_stride` apart)
+// into the P-partial layout with a compile-time shape: each of the T
+// threads moves I / (8 T) 16-byte chunks per row, all B rows' loads issued
+// before any is converted.  `issue` runs after the loads (loads retire in
+// order).  Requires I % (8 T) == 0.
+template <int P, int B, int I, int T, class Issue>
+__device__ __forceinline__ void stage_block(const uint16_t* __restrict__ x, uint64_t row_stride, float* xs,
+                                            Issue&& issue) {
+  constexpr int J = I / (8 * T);
+  static_assert(J >= 1 && I % (8 * T) == 0, "block width must be a multiple of 8 per thread");
+  u32x4 v[B][J];
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      v[b][j] = reinterpret_cast<const u32x4*>(x + b * row_stride)[threadIdx.x + j * T];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  issue();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int i = (threadIdx.x + j * T) * 8;
+      stage_put<P>(xs, I, b, i + 0, dl_bf16_lo(v[b][j].x));
+      stage_put<P>(xs, I, b, i + 1, dl_bf16_hi(v[b][j].x));
+      stage_put<P>(xs, I, b, i + 2, dl_bf16_lo(v[b][j].y));
+      stage_put<P>(xs, I, b, i + 3, dl_bf16_hi(v[b][j].y));
+      stage_put<P>(xs, I, b, i + 4, dl_bf16_lo(v[b][j].z));
+      stage_put<P>(xs, I, b, i + 5, dl_bf16_hi(v[b][j].z));
+      stage_put<P>(xs, I, b, i + 6, dl_bf16_lo(v[b][j].w));
+      stage_put<P>(xs, I, b, i + 7, dl_bf16_hi(v[b][j].w));
+    }
+  }
+}
+
 // One wavefront computes RW output rows for B input rows.  `tile` points at
 // the tile's first 16-byte chunk; on return lane (row, 0) of each P-lane
 // segment holds the merged FP32 sum of that row for every b.
@@ -103,6 +143,9 @@ __device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ x, int I
 // distinct registers before any of them is consumed, so each wavefront keeps
 // kBatch KiB in flight instead of serialising on one load-use chain.
 constexpr int kBatch = 8;
+
+// LDS per compute unit on gfx950.
+constexpr uint64_t kLdsPerCu = 160 * 1024;
 
 // One step of every lane's chain: 8 consecutive chain elements of weights w
 // against the staged inputs at step s, for each of the B rows.
@@ -141,14 +184,64 @@ __device__ __forceinline__ void issue_first(const u32x4* __restrict__ tile, int 
   f.valid = true;
 }
 
+// Several rows (B >= 2) make every chunk worth B x 8 FMAs, so a wavefront
+// spends long enough on a batch to hide the next one's latency: the batches
+// of a tile are double-buffered (batch k + 1 is issued before batch k is
+// consumed), and the last one overlaps the first batch of the wavefront's
+// next tile, handed back through `first`.  Needs an even batch count.
 template <int P, int B>
-__device__ __forceinline__ void chain_tile(const u32x4* __restrict__ tile, const float* __restrict__ xs,
-                                           int I, int lane, float (&acc)[B], FirstBatch* first = nullptr) {
+__device__ __forceinline__ void chain_tile_pipelined(const u32x4* __restrict__ src, const float* __restrict__ xt,
+                                                     int bstride, int batches, float (&acc)[B], FirstBatch* first,
+                                                     const u32x4* __restrict__ next_src) {
+  u32x4 wa[kBatch], wb[kBatch];
+  auto load = [&](u32x4* w, const u32x4* from) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) w[j] = load_stream(from + j * 64);
+  };
+  if (first && first->valid) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) wa[j] = first->w[j];
+  } else {
+    load(wa, src);
+  }
+  for (int k = 0; k < batches; k += 2) {
+    load(wb, src + (k + 1) * kBatch * 64);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) chain_step<B>(wa[j], xt, bstride, k * kBatch + j, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    load(wa, k + 2 < batches ? src + (k + 2) * kBatch * 64 : next_src);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) chain_step<B>(wb[j], xt, bstride, (k + 1) * kBatch + j, acc);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (first) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) first->w[j] = wa[j];
+  }
+}
+
+// The chain steps of one tile over I staged inputs, accumulating into acc
+// (not reset).  `next` (optional) is where the wavefront's chain continues
+// (its next tile, or this tile's next block of inputs): with B >= 2 its
+// first batch is loaded during this call's last batch and left in `first`.
+template <int P, int B>
+__device__ __forceinline__ void chain_body(const u32x4* __restrict__ tile, const float* __restrict__ xs, int I,
+                                           int lane, float (&acc)[B], FirstBatch* first = nullptr,
+                                           const u32x4* __restrict__ next = nullptr) {
   const int L = I / P, S = L / 8, stride = L + kXsPad, bstride = P * stride;
   const float* xt = xs + (lane % P) * stride;
   const u32x4* src = tile + lane;
-#pragma unroll
-  for (int b = 0; b < B; ++b) acc[b] = 0.0f;
+  if constexpr (B >= 2) {
+    const int batches = S / kBatch;
+    if (S % kBatch == 0 && batches % 2 == 0) {
+      // A missing next tile reloads this tile's first batch (never used).
+      chain_tile_pipelined<P, B>(src, xt, bstride, batches, acc, first, next ? next + lane : src);
+      if (first) first->valid = next != nullptr;
+      return;
+    }
+  }
   int s0 = 0;
   if (first && first->valid && S >= kBatch) {
     // The tile's first batch was issued before the kernel's prologue.
@@ -165,11 +258,26 @@ __device__ __forceinline__ void chain_tile(const u32x4* __restrict__ tile, const
     for (int j = 0; j < kBatch; ++j) chain_step<B>(w[j], xt, bstride, s0 + j, acc);
   }
   for (; s0 < S; ++s0) chain_step<B>(load_stream(src + s0 * 64), xt, bstride, s0, acc);
+}
+
+// Merges the P partials of each row (offsets P/2 .. 1) into lane (row, 0).
+template <int P, int B>
+__device__ __forceinline__ void chain_merge(float (&acc)[B]) {
 #pragma unroll
   for (int b = 0; b < B; ++b) {
 #pragma unroll
     for (int off = P / 2; off; off >>= 1) acc[b] = acc[b] + __shfl_down(acc[b], off, P);
   }
+}
+
+template <int P, int B>
+__device__ __forceinline__ void chain_tile(const u32x4* __restrict__ tile, const float* __restrict__ xs,
+                                           int I, int lane, float (&acc)[B], FirstBatch* first = nullptr,
+                                           const u32x4* __restrict__ next = nullptr) {
+#pragma unroll
+  for (int b = 0; b < B; ++b) acc[b] = 0.0f;
+  chain_body<P, B>(tile, xs, I, lane, acc, first, next);
+  chain_merge<P, B>(acc);
 }
 
 // Inverse RMS of one BF16 row of width D > 128 with the reference tree

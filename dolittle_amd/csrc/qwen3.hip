@@ -46,6 +46,11 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kBlock = kWaves * 64;
+// Wavefronts per workgroup of the GEMV kernels for `rows` staged rows.  From
+// four rows the staged inputs fill most of the LDS, so one workgroup is
+// resident per CU; eight wavefronts (two per SIMD) keep twice the weight
+// loads in flight.
+constexpr int gemv_waves(int rows) { return rows >= 4 ? 8 : kWaves; }
 constexpr int kHeadDim = 128;
 
 __device__ __forceinline__ uint16_t bf16_bits(float v) { return dl_f32_to_bf16(v); }
@@ -211,11 +216,18 @@ struct QkvArgs {
   float eps;
 };
 
-template <int B>
-__global__ __launch_bounds__(kBlock) void k_qkv(QkvArgs a) {
+// Part: kQkvAll projects Q, K and V; at eight rows both staged layouts do
+// not fit in LDS together, so kQkvQ (Q rows, P = 16 layout) and kQkvKV (K
+// and V rows, P = 32 layout) run as two launches.
+enum QkvPart : int { kQkvAll = 0, kQkvQ = 1, kQkvKV = 2 };
+constexpr int qkv_waves(int rows, int part) { return part == kQkvAll ? kWaves : gemv_waves(rows); }
+
+template <int B, int Part = kQkvAll>
+__global__ __launch_bounds__(qkv_waves(B, Part) * 64) void k_qkv(QkvArgs a) {
+  constexpr int W = qkv_waves(B, Part);
   extern __shared__ float lds[];
   float* xs16 = lds;
-  float* xs32 = xs16 + B * staged_floats(16, a.D);
+  float* xs32 = Part == kQkvKV ? lds : xs16 + B * staged_floats(16, a.D);
   __shared__ float scratch[80];
   if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
@@ -232,28 +244,31 @@ __global__ __launch_bounds__(kBlock) void k_qkv(QkvArgs a) {
     if (is_v) kt -= k_tiles;
     return a.w + q_tiles * q_chunks + (is_v ? k_tiles : 0) * k_chunks + kt * k_chunks;
   };
-  const int first = blockIdx.x * kWaves + wave;
+  const int tile_begin = Part == kQkvKV ? q_tiles : 0, tile_end = Part == kQkvQ ? q_tiles : total;
+  const int first = tile_begin + blockIdx.x * W + wave;
   FirstBatch fb{};
-  norm_stage<B, true, true>(a.h, a.norm, a.eps, xs16, xs32, scratch, [&] {
-    if (first < total) issue_first(tile_src(first), lane, fb);
+  norm_stage<B, Part != kQkvKV, Part != kQkvQ>(a.h, a.norm, a.eps, xs16, xs32, scratch, [&] {
+    if (first < tile_end) issue_first(tile_src(first), lane, fb);
   });
   __syncthreads();
-  for (int tile = first; tile < total; tile += gridDim.x * kWaves) {
+  for (int tile = first; tile < tile_end; tile += gridDim.x * W) {
     const bool is_q = tile < q_tiles;
     int kt = tile - q_tiles;
     const bool is_v = !is_q && kt >= k_tiles;
     if (is_v) kt -= k_tiles;
     const u32x4* src = tile_src(tile);
+    const int next = tile + gridDim.x * W;
+    const u32x4* next_src = next < tile_end ? tile_src(next) : nullptr;
     float acc[B];
-    if (is_q) {
-      chain_tile<16, B>(src, xs16, a.D, lane, acc, &fb);
+    if (Part == kQkvQ || (Part == kQkvAll && is_q)) {
+      chain_tile<16, B>(src, xs16, a.D, lane, acc, &fb, next_src);
       if (lane % 16 == 0) {
         const int row = tile * 4 + lane / 16;
 #pragma unroll
         for (int b = 0; b < B; ++b) a.q_out[b * a.QW + row] = bf16_bits(acc[b]);
       }
     } else {
-      chain_tile<32, B>(src, xs32, a.D, lane, acc, &fb);
+      chain_tile<32, B>(src, xs32, a.D, lane, acc, &fb, next_src);
       if (lane % 32 == 0) {
         const int row = kt * 2 + lane / 32;
 #pragma unroll
@@ -769,7 +784,8 @@ struct ResidualArgs {
 // y = round(x W^T); h = round(h + y); optionally h = round(h + steer) and a
 // copy of h into the capture arena at the current position.
 template <int P, int B>
-__global__ __launch_bounds__(kBlock) void k_residual(ResidualArgs a) {
+__global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual(ResidualArgs a) {
+  constexpr int W = gemv_waves(B);
   extern __shared__ float xs[];
   if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
@@ -778,7 +794,7 @@ __global__ __launch_bounds__(kBlock) void k_residual(ResidualArgs a) {
   const int tiles = a.D / RW;
   const int S = a.I / (8 * P);
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
-  const int first = blockIdx.x * kWaves + wave;
+  const int first = blockIdx.x * W + wave;
   FirstBatch fb{};
   stage_rows<P>(a.x + static_cast<uint64_t>(a.row0) * a.I, a.I, B, xs, [&] {
     if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
@@ -787,10 +803,74 @@ __global__ __launch_bounds__(kBlock) void k_residual(ResidualArgs a) {
   const bool steer = a.steer != nullptr && a.layer == a.ctl->steer_layer;
   const bool capture = a.capture != nullptr && a.layer == a.ctl->capture_layer;
   const uint32_t steer_mask = a.ctl->steer_mask;
-  for (int tile = first; tile < tiles; tile += gridDim.x * kWaves) {
+  for (int tile = first; tile < tiles; tile += gridDim.x * W) {
     float acc[B];
-    chain_tile<P, B>(a.w + tile * chunks, xs, a.I, lane, acc, &fb);
+    const int next = tile + gridDim.x * W;
+    chain_tile<P, B>(a.w + tile * chunks, xs, a.I, lane, acc, &fb, next < tiles ? a.w + next * chunks : nullptr);
     if (lane % P == 0) {
+      const int row = tile * RW + lane / P;
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const int seq = a.row0 + b;
+        const uint64_t at = static_cast<uint64_t>(seq) * a.D + row;
+        float value = rbf(dl_bf16_to_f32(a.h[at]) + rbf(acc[b]));
+        if (steer && ((steer_mask >> seq) & 1u)) value = rbf(value + a.steer[at]);
+        a.h[at] = bf16_bits(value);
+        if (capture) a.capture[(static_cast<uint64_t>(seq) * a.cap + pos) * a.D + row] = bf16_bits(value);
+      }
+    }
+  }
+}
+
+// k_residual for rows whose staged inputs do not fit in LDS at once (the
+// down projection, I = 12288, at four or more rows): the inputs are staged
+// kChunkInputs at a time and every wavefront carries its chains across the
+// blocks in ascending input order, so each partial is the same FMA chain as
+// in k_residual.  Each wavefront owns one tile per pass; all wavefronts of a
+// workgroup take part in every staging barrier (uniform trip counts).
+constexpr int kChunkInputs = 4096;
+
+template <int P, int B>
+__global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual_chunked(ResidualArgs a) {
+  constexpr int W = gemv_waves(B);
+  constexpr int kChunkSteps = kChunkInputs / (8 * P);
+  extern __shared__ float xs[];
+  if (!a.ctl->active) return;
+  const uint64_t pos = a.ctl->position;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  constexpr int RW = 64 / P;
+  const int tiles = a.D / RW;
+  const int S = a.I / (8 * P);
+  const uint64_t chunks = static_cast<uint64_t>(S) * 64;
+  const int blocks = a.I / kChunkInputs;
+  const bool steer = a.steer != nullptr && a.layer == a.ctl->steer_layer;
+  const bool capture = a.capture != nullptr && a.layer == a.ctl->capture_layer;
+  const uint32_t steer_mask = a.ctl->steer_mask;
+  for (int base = blockIdx.x * W; base < tiles; base += gridDim.x * W) {
+    const int tile = base + wave;
+    const bool active = tile < tiles;
+    const u32x4* src = a.w + static_cast<uint64_t>(active ? tile : base) * chunks;
+    float acc[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) acc[b] = 0.0f;
+    FirstBatch fb{};
+    for (int c = 0; c < blocks; ++c) {
+      __syncthreads();  // every wavefront is done with the previous block
+      stage_block<P, B, kChunkInputs, W * 64>(a.x + static_cast<uint64_t>(a.row0) * a.I + c * kChunkInputs, a.I, xs,
+                                             [&] {
+                                               if (c == 0 && active) issue_first(src, lane, fb);
+                                             });
+      __syncthreads();
+      if (active) {
+        // The block width is passed as a run-time value (a.I / blocks): a
+        // compile-time width lets the compiler unroll the whole block and
+        // hoist its LDS reads past the register file.
+        const u32x4* at = src + static_cast<uint64_t>(c) * kChunkSteps * 64;
+        chain_body<P, B>(at, xs, a.I / blocks, lane, acc, &fb, c + 1 < blocks ? at + kChunkSteps * 64 : nullptr);
+      }
+    }
+    chain_merge<P, B>(acc);
+    if (active && lane % P == 0) {
       const int row = tile * RW + lane / P;
 #pragma unroll
       for (int b = 0; b < B; ++b) {
@@ -817,7 +897,8 @@ struct GateUpArgs {
 };
 
 template <int B>
-__global__ __launch_bounds__(kBlock) void k_gateup(GateUpArgs a) {
+__global__ __launch_bounds__(gemv_waves(B) * 64) void k_gateup(GateUpArgs a) {
+  constexpr int W = gemv_waves(B);
   extern __shared__ float xs[];
   __shared__ float scratch[80];
   if (!a.ctl->active) return;
@@ -825,16 +906,17 @@ __global__ __launch_bounds__(kBlock) void k_gateup(GateUpArgs a) {
   const int tiles = a.F / 2;
   const int S = a.D / 128;
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
-  const int first = blockIdx.x * kWaves + wave;
+  const int first = blockIdx.x * W + wave;
   FirstBatch fb{};
   norm_stage<B, true, false>(a.h, a.norm, a.eps, xs, nullptr, scratch, [&] {
     if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
   });
   __syncthreads();
   (void)S;
-  for (int tile = first; tile < tiles; tile += gridDim.x * kWaves) {
+  for (int tile = first; tile < tiles; tile += gridDim.x * W) {
     float acc[B];
-    chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc, &fb);
+    const int next = tile + gridDim.x * W;
+    chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc, &fb, next < tiles ? a.w + next * chunks : nullptr);
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       const float up = __shfl_down(acc[b], 32, 64);
@@ -890,17 +972,18 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 }
 
 template <int B>
-__global__ __launch_bounds__(kBlock) void k_lm_head(HeadArgs a) {
+__global__ __launch_bounds__(gemv_waves(B) * 64) void k_lm_head(HeadArgs a) {
+  constexpr int W = gemv_waves(B);
   extern __shared__ float xs[];
   __shared__ float scratch[80];
-  __shared__ uint64_t wave_keys[kWaves][B];
-  __shared__ uint32_t wave_flags[kWaves][B];
+  __shared__ uint64_t wave_keys[W][B];
+  __shared__ uint32_t wave_flags[W][B];
   if (!a.ctl->active || !selecting(a.ctl)) return;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int tiles = static_cast<int>(a.V / 4);
   const int S = a.D / 128;
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
-  const int first = blockIdx.x * kWaves + wave;
+  const int first = blockIdx.x * W + wave;
   (void)S;
   FirstBatch fb{};
   norm_stage<B, true, false>(a.h + static_cast<uint64_t>(a.row0) * a.D, a.norm, a.eps, xs, nullptr, scratch, [&] {
@@ -914,9 +997,10 @@ __global__ __launch_bounds__(kBlock) void k_lm_head(HeadArgs a) {
     best[b] = 0;
     flags[b] = 0;
   }
-  for (int tile = first; tile < tiles; tile += gridDim.x * kWaves) {
+  for (int tile = first; tile < tiles; tile += gridDim.x * W) {
     float acc[B];
-    chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc, &fb);
+    const int next = tile + gridDim.x * W;
+    chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc, &fb, next < tiles ? a.w + next * chunks : nullptr);
     if (lane % 16 == 0) {
       const uint32_t row = static_cast<uint32_t>(tile * 4 + lane / 16);
 #pragma unroll
@@ -943,7 +1027,7 @@ __global__ __launch_bounds__(kBlock) void k_lm_head(HeadArgs a) {
     const int b = threadIdx.x;
     uint64_t k = 0;
     uint32_t f = 0;
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < W; ++w) {
       k = wave_keys[w][b] > k ? wave_keys[w][b] : k;
       f |= wave_flags[w][b];
     }
@@ -1376,6 +1460,7 @@ struct dl_plan {
   dl_queue* queue = nullptr;
   uint32_t batch = 1, capacity = 0, cap = 0;  // cap: padded to 64
   int head_blocks = 256;
+  uint64_t compute_units = 256;  // queried at creation
   std::vector<void*> allocations;
   dl::Control* ctl = nullptr;
   dl::Control* bench_ctl = nullptr;
@@ -1397,9 +1482,17 @@ struct dl_plan {
   // Workgroups per decode-step kernel (0: one tile per wavefront).
   // Defaults from the workgroup sweep on MI355X (grid-stride over tiles).
   uint32_t grid_override[8] = {512, 0, 0, 0, 256, 768, 512, 0};
-  unsigned grid_for(int which, uint64_t tiles) const {
-    const uint64_t full = dl::ceil_div(tiles, 4);
-    const uint64_t g = grid_override[which] ? grid_override[which] : full;
+  // Workgroups of `waves` wavefronts for `tiles` tiles: the tuned override
+  // (or one tile per wavefront), capped at what stays resident at once when the
+  // staged rows' LDS limits residency, so no workgroup repeats the staging
+  // prologue in a second round.
+  unsigned grid_for(int which, uint64_t tiles, size_t lds = 0, int waves = dl::kWaves) const {
+    const uint64_t full = dl::ceil_div(tiles, static_cast<uint64_t>(waves));
+    uint64_t g = grid_override[which] ? grid_override[which] : full;
+    if (lds > 0) {
+      const uint64_t resident = std::max<uint64_t>(1, dl::kLdsPerCu / (lds + 1024));
+      g = std::min<uint64_t>(g, resident * compute_units);
+    }
     return static_cast<unsigned>(g < full ? g : full);
   }
   // Host mirror of settings.
@@ -1462,11 +1555,15 @@ void allow_lds(K kernel, size_t bytes) {
 // a row group must fit the 160 KiB LDS (QKV stages D twice, for P = 16 and
 // P = 32; down stages F = 12288 for P = 32).  Wider batches launch several
 // row groups, each streaming the weights once.
-constexpr int kQkvRows = 4;
-constexpr int kDownRows = 2;
+constexpr int kQkvRows = 8;   // eight rows run as a Q launch and a K/V launch
+constexpr int kDownRows = 8;  // from four rows the inputs are staged in blocks
 constexpr int kWideRows = 8;
 
-size_t qkv_lds(int rows, int D) { return size_t(rows) * (dl::staged_floats(16, D) + dl::staged_floats(32, D)) * 4; }
+size_t qkv_lds(int rows, int D, int part = dl::kQkvAll) {
+  const size_t q = part == dl::kQkvKV ? 0 : dl::staged_floats(16, D);
+  const size_t kv = part == dl::kQkvQ ? 0 : dl::staged_floats(32, D);
+  return size_t(rows) * (q + kv) * 4;
+}
 size_t p16_lds(int rows, int I) { return size_t(rows) * dl::staged_floats(16, I) * 4; }
 size_t p32_lds(int rows, int I) { return size_t(rows) * dl::staged_floats(32, I) * 4; }
 
@@ -1493,6 +1590,10 @@ void prepare_kernels_all(dl_plan* p) {
   allow_lds(k_qkv<1>, qkv_lds(1, D));
   allow_lds(k_qkv<2>, qkv_lds(2, D));
   allow_lds(k_qkv<4>, qkv_lds(4, D));
+  allow_lds(k_qkv<8, kQkvQ>, qkv_lds(8, D, kQkvQ));
+  allow_lds(k_qkv<8, kQkvKV>, qkv_lds(8, D, kQkvKV));
+  allow_lds(k_residual_chunked<32, 4>, p32_lds(4, kChunkInputs));
+  allow_lds(k_residual_chunked<32, 8>, p32_lds(8, kChunkInputs));
   allow_lds(k_residual<16, 1>, p16_lds(1, QW));
   allow_lds(k_residual<16, 2>, p16_lds(2, QW));
   allow_lds(k_residual<16, 4>, p16_lds(4, QW));
@@ -1510,22 +1611,33 @@ void prepare_kernels_all(dl_plan* p) {
   allow_lds(k_attn_softmax, size_t(p->cap) * sizeof(float));
 }
 
-template <int G>
+template <int G, int Part = dl::kQkvAll>
 void launch_qkv(dl_plan* p, hipStream_t s, const dl::QkvArgs& a) {
-  dl::k_qkv<G><<<p->grid_for(0, a.QW / 4 + a.KW), dl::kBlock, qkv_lds(G, a.D), s>>>(a);
+  const uint64_t tiles = Part == dl::kQkvQ ? a.QW / 4 : Part == dl::kQkvKV ? a.KW : a.QW / 4 + a.KW;
+  const size_t lds = qkv_lds(G, a.D, Part);
+  constexpr int waves = dl::qkv_waves(G, Part);
+  dl::k_qkv<G, Part><<<p->grid_for(0, tiles, lds, waves), waves * 64, lds, s>>>(a);
+}
+template <int G>
+void launch_down_chunked(dl_plan* p, hipStream_t s, const dl::ResidualArgs& a) {
+  const size_t lds = p32_lds(G, dl::kChunkInputs);
+  constexpr int waves = dl::gemv_waves(G);
+  dl::k_residual_chunked<32, G><<<p->grid_for(6, a.D / 2, lds, waves), waves * 64, lds, s>>>(a);
 }
 template <int P, int G>
 void launch_residual(dl_plan* p, hipStream_t s, int which, const dl::ResidualArgs& a) {
   const size_t lds = P == 16 ? p16_lds(G, a.I) : p32_lds(G, a.I);
-  dl::k_residual<P, G><<<p->grid_for(which, a.D / (64 / P)), dl::kBlock, lds, s>>>(a);
+  dl::k_residual<P, G><<<p->grid_for(which, a.D / (64 / P), lds, dl::gemv_waves(G)), dl::gemv_waves(G) * 64, lds,
+                         s>>>(a);
 }
 template <int G>
 void launch_gateup(dl_plan* p, hipStream_t s, const dl::GateUpArgs& a) {
-  dl::k_gateup<G><<<p->grid_for(5, a.F / 2), dl::kBlock, p16_lds(G, a.D), s>>>(a);
+  dl::k_gateup<G><<<p->grid_for(5, a.F / 2, p16_lds(G, a.D), dl::gemv_waves(G)), dl::gemv_waves(G) * 64,
+                     p16_lds(G, a.D), s>>>(a);
 }
 template <int G>
 void launch_head(dl_plan* p, hipStream_t s, const dl::HeadArgs& a) {
-  dl::k_lm_head<G><<<p->head_blocks, dl::kBlock, p16_lds(G, a.D), s>>>(a);
+  dl::k_lm_head<G><<<p->head_blocks, dl::gemv_waves(G) * 64, p16_lds(G, a.D), s>>>(a);
 }
 
 // Launches one decode-step kernel `which` of layer `l` with control `ctl`
@@ -1548,9 +1660,16 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
         QkvArgs qa{ctl, p->h + uint64_t(r0) * D, m->input_norm[l], reinterpret_cast<const u32x4*>(m->qkv[l]),
                    p->q_raw + uint64_t(r0) * QW, p->k_raw + uint64_t(r0) * KW, vc + r0 * p->cache_seq_stride,
                    p->cache_seq_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps};
-        if (g == 4) launch_qkv<4>(p, s, qa);
-        else if (g == 2) launch_qkv<2>(p, s, qa);
-        else launch_qkv<1>(p, s, qa);
+        if (g == 8) {
+          launch_qkv<8, kQkvQ>(p, s, qa);
+          launch_qkv<8, kQkvKV>(p, s, qa);
+        } else if (g == 4) {
+          launch_qkv<4>(p, s, qa);
+        } else if (g == 2) {
+          launch_qkv<2>(p, s, qa);
+        } else {
+          launch_qkv<1>(p, s, qa);
+        }
       });
       break;
     case 1: k_attn_qk<<<dim3(c.kv_heads, p->cap / 64, B), kBlock, 0, s>>>(aa); break;
@@ -1578,10 +1697,14 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       });
       break;
     case 6:
-      for_row_groups(B, kDownRows, [&](uint32_t r0, int g) {
+      // Staging in blocks needs whole blocks of inputs; other widths keep
+      // two-row launches.
+      for_row_groups(B, F % kChunkInputs == 0 ? kDownRows : 2, [&](uint32_t r0, int g) {
         ResidualArgs da{ctl, p->act, reinterpret_cast<const u32x4*>(m->down[l]), p->h, p->capture, p->steer, F, D,
                         static_cast<int>(p->cap), static_cast<int>(l), static_cast<int>(r0)};
-        if (g == 2) launch_residual<32, 2>(p, s, 6, da);
+        if (g == 8) launch_down_chunked<8>(p, s, da);
+        else if (g == 4) launch_down_chunked<4>(p, s, da);
+        else if (g == 2) launch_residual<32, 2>(p, s, 6, da);
         else launch_residual<32, 1>(p, s, 6, da);
       });
       break;
@@ -1714,6 +1837,12 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
     p->batch = batch;
     p->capacity = capacity;
     p->cap = static_cast<uint32_t>(dl::ceil_div(capacity, 64) * 64);
+    {
+      int device = 0, cus = 0;
+      dl::check_hip(hipGetDevice(&device), "current device");
+      dl::check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device), "compute units");
+      p->compute_units = static_cast<uint64_t>(std::max(cus, 1));
+    }
     const auto& c = model->cfg;
     const uint64_t B = batch, D = c.hidden, QW = uint64_t(c.q_heads) * c.head_dim,
                    KW = uint64_t(c.kv_heads) * c.head_dim, F = c.ffn, V = c.vocab, L = c.layers, cap = p->cap;
