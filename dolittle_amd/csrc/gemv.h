@@ -312,33 +312,38 @@ __device__ __forceinline__ float block_rms_inverse(const uint16_t* __restrict__ 
   return inverse;
 }
 
-// Stages round(round(h_b * inverse_b) * gain) for R <= 2 rows (starting at
-// row b0) of width D = 128 * kNormK into the staged LDS layouts for P = 16
-// (when S16) and P = 32 (when S32), computing inverse_b with the reference
-// tree (normalization.cu:134-186) in the same pass: thread i < 128 keeps
-// features i + 128k of every row in registers, sums their squares in
-// ascending k (component i), combines groups of four left to right, and the
-// lanes below 32 R reduce the 32 lane totals with shuffle-down offsets 1..16.
-// The width and the layouts are compile-time so that loads, sums and LDS
-// stores are straight-line code with every load in flight at once.
+// Stages round(round(h_b * inverse_b) * gain) for the rows [b0, b0 + R G)
+// that exist (below B) of width D = 128 * kNormK into the staged LDS layouts
+// for P = 16 (when S16) and P = 32 (when S32), computing inverse_b with the
+// reference tree (normalization.cu:134-186) in the same pass.  Thread group
+// g (threads 128 g .. 128 g + 127) owns rows b0 + R g .. b0 + R g + R - 1:
+// thread t of the group keeps features t + 128k of its rows in registers, sums
+// their squares in ascending k (component t), combines groups of four left
+// to right, and the group's first wavefront reduces the 32 lane totals of
+// each row with shuffle-down offsets 1..16.  The width and the layouts are
+// compile-time so that loads, sums and LDS stores are straight-line code
+// with every load in flight at once.  `scratch` holds 80 G floats of LDS.
 constexpr int kNormK = 32;
 constexpr int kNormWidth = 128 * kNormK;
 
-template <int R, bool S16, bool S32, class Issue>
-__device__ __forceinline__ void norm_stage_rows(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
-                                                float eps, float* xs16, float* xs32, float* scratch, int b0,
+template <int R, bool S16, bool S32, int G, class Issue>
+__device__ __forceinline__ void norm_stage_pass(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
+                                                float eps, float* xs16, float* xs32, float* scratch, int b0, int B,
                                                 Issue&& issue) {
-  static_assert(R <= 2, "one wavefront reduces at most two rows");
   constexpr int D = kNormWidth;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, t = tid % 128, g = tid / 128;
+  static_assert(R == 1 || R == 2, "a thread group owns one or two rows");
+  const int r0 = b0 + R * g;
+  const bool has0 = g < G && r0 < B, has1 = R == 2 && g < G && r0 + 1 < B;
+  const int r1 = has1 ? r0 + 1 : r0;  // a missing second row repeats the first (never staged)
   float hv[R][kNormK];
   float gv[kNormK];
-  if (tid < 128) {
+  if (has0) {
 #pragma unroll
     for (int k = 0; k < kNormK; ++k) {
-      gv[k] = dl_bf16_to_f32(gain[tid + 128 * k]);
-#pragma unroll
-      for (int b = 0; b < R; ++b) hv[b][k] = dl_bf16_to_f32(h[(b0 + b) * D + tid + 128 * k]);
+      gv[k] = dl_bf16_to_f32(gain[t + 128 * k]);
+      hv[0][k] = dl_bf16_to_f32(h[r0 * D + t + 128 * k]);
+      if constexpr (R == 2) hv[R - 1][k] = dl_bf16_to_f32(h[r1 * D + t + 128 * k]);
     }
   }
   // Loads retire in order: the caller's own traffic (the first weight batch)
@@ -346,7 +351,7 @@ __device__ __forceinline__ void norm_stage_rows(const uint16_t* __restrict__ h, 
   __builtin_amdgcn_sched_barrier(0);
   issue();
   __builtin_amdgcn_sched_barrier(0);
-  if (tid < 128) {
+  if (has0) {
 #pragma unroll
     for (int b = 0; b < R; ++b) {
       float comp = 0.0f;
@@ -355,52 +360,50 @@ __device__ __forceinline__ void norm_stage_rows(const uint16_t* __restrict__ h, 
       const float second = __shfl_down(comp, 1, 4);
       const float third = __shfl_down(comp, 2, 4);
       const float fourth = __shfl_down(comp, 3, 4);
-      if ((tid & 3) == 0) scratch[b * 40 + (tid >> 2)] = ((comp + second) + third) + fourth;
+      if ((t & 3) == 0) scratch[(R * g + b) * 40 + (t >> 2)] = ((comp + second) + third) + fourth;
     }
   }
   __syncthreads();
-  if (tid < 32 * R) {
-    const int b = tid / 32;
-    float s = scratch[b * 40 + (tid & 31)];
+  if (has0 && t < 32 * R) {
+    const int slot = R * g + t / 32;
+    float s = scratch[slot * 40 + (t & 31)];
 #pragma unroll
     for (int off = 1; off < 32; off *= 2) s = s + __shfl_down(s, off, 32);
-    if ((tid & 31) == 0) scratch[b * 40 + 32] = inverse_sqrt(s * (1.0f / static_cast<float>(D)) + eps);
+    if ((t & 31) == 0) scratch[slot * 40 + 32] = inverse_sqrt(s * (1.0f / static_cast<float>(D)) + eps);
   }
   __syncthreads();
-  if (tid < 128) {
+  if (has0) {
 #pragma unroll
     for (int b = 0; b < R; ++b) {
-      const float inverse = scratch[b * 40 + 32];
+      if (b == 1 && !has1) break;
+      const float inverse = scratch[(R * g + b) * 40 + 32];
 #pragma unroll
       for (int k = 0; k < kNormK; ++k) {
         const float n = dl_round_bf16(dl_round_bf16(hv[b][k] * inverse) * gv[k]);
-        const int col = tid + 128 * k;
-        if constexpr (S16) stage_put<16>(xs16, D, b0 + b, col, n);
-        if constexpr (S32) stage_put<32>(xs32, D, b0 + b, col, n);
+        const int col = t + 128 * k;
+        if constexpr (S16) stage_put<16>(xs16, D, r0 + b, col, n);
+        if constexpr (S32) stage_put<32>(xs32, D, r0 + b, col, n);
       }
     }
   }
 }
 
-// norm_stage_rows over B rows, two at a time (scratch is reused between
-// pairs behind a barrier).  Rows have width kNormWidth.
-template <int B, bool S16, bool S32, class Issue>
+// norm_stage_pass over B rows, R G at a time (R = 2 rows per group, 1 for
+// a single row) (scratch is reused between
+// passes behind a barrier); G = threads / 128 of the calling workgroup.
+// Rows have width kNormWidth.
+template <int B, bool S16, bool S32, int G, class Issue>
 __device__ __forceinline__ void norm_stage(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
                                            float eps, float* xs16, float* xs32, float* scratch, Issue&& issue) {
+  constexpr int R = B == 1 ? 1 : 2;
   auto none = [] {};
 #pragma unroll
-  for (int b0 = 0; b0 < B; b0 += 2) {
-    if (b0) __syncthreads();
-    if (B - b0 >= 2) {
-      if (b0 == 0)
-        norm_stage_rows<2, S16, S32>(h, gain, eps, xs16, xs32, scratch, b0, issue);
-      else
-        norm_stage_rows<2, S16, S32>(h, gain, eps, xs16, xs32, scratch, b0, none);
+  for (int b0 = 0; b0 < B; b0 += R * G) {
+    if (b0) {
+      __syncthreads();
+      norm_stage_pass<R, S16, S32, G>(h, gain, eps, xs16, xs32, scratch, b0, B, none);
     } else {
-      if (b0 == 0)
-        norm_stage_rows<1, S16, S32>(h, gain, eps, xs16, xs32, scratch, b0, issue);
-      else
-        norm_stage_rows<1, S16, S32>(h, gain, eps, xs16, xs32, scratch, b0, none);
+      norm_stage_pass<R, S16, S32, G>(h, gain, eps, xs16, xs32, scratch, b0, B, issue);
     }
   }
 }

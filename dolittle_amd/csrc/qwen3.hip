@@ -228,7 +228,7 @@ __global__ __launch_bounds__(qkv_waves(B, Part) * 64) void k_qkv(QkvArgs a) {
   extern __shared__ float lds[];
   float* xs16 = lds;
   float* xs32 = Part == kQkvKV ? lds : xs16 + B * staged_floats(16, a.D);
-  __shared__ float scratch[80];
+  __shared__ float scratch[W * 40];
   if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(qkv_waves(B, Part) * 64) void k_qkv(QkvArgs a) {
   const int tile_begin = Part == kQkvKV ? q_tiles : 0, tile_end = Part == kQkvQ ? q_tiles : total;
   const int first = tile_begin + blockIdx.x * W + wave;
   FirstBatch fb{};
-  norm_stage<B, Part != kQkvKV, Part != kQkvQ>(a.h, a.norm, a.eps, xs16, xs32, scratch, [&] {
+  norm_stage<B, Part != kQkvKV, Part != kQkvQ, W / 2>(a.h, a.norm, a.eps, xs16, xs32, scratch, [&] {
     if (first < tile_end) issue_first(tile_src(first), lane, fb);
   });
   __syncthreads();
@@ -900,7 +900,7 @@ template <int B>
 __global__ __launch_bounds__(gemv_waves(B) * 64) void k_gateup(GateUpArgs a) {
   constexpr int W = gemv_waves(B);
   extern __shared__ float xs[];
-  __shared__ float scratch[80];
+  __shared__ float scratch[W * 40];
   if (!a.ctl->active) return;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int tiles = a.F / 2;
@@ -908,7 +908,7 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_gateup(GateUpArgs a) {
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
   const int first = blockIdx.x * W + wave;
   FirstBatch fb{};
-  norm_stage<B, true, false>(a.h, a.norm, a.eps, xs, nullptr, scratch, [&] {
+  norm_stage<B, true, false, W / 2>(a.h, a.norm, a.eps, xs, nullptr, scratch, [&] {
     if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
   });
   __syncthreads();
@@ -975,7 +975,7 @@ template <int B>
 __global__ __launch_bounds__(gemv_waves(B) * 64) void k_lm_head(HeadArgs a) {
   constexpr int W = gemv_waves(B);
   extern __shared__ float xs[];
-  __shared__ float scratch[80];
+  __shared__ float scratch[W * 40];
   __shared__ uint64_t wave_keys[W][B];
   __shared__ uint32_t wave_flags[W][B];
   if (!a.ctl->active || !selecting(a.ctl)) return;
@@ -986,7 +986,8 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_lm_head(HeadArgs a) {
   const int first = blockIdx.x * W + wave;
   (void)S;
   FirstBatch fb{};
-  norm_stage<B, true, false>(a.h + static_cast<uint64_t>(a.row0) * a.D, a.norm, a.eps, xs, nullptr, scratch, [&] {
+  norm_stage<B, true, false, W / 2>(a.h + static_cast<uint64_t>(a.row0) * a.D, a.norm, a.eps, xs, nullptr, scratch,
+                                    [&] {
     if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
   });
   __syncthreads();
