@@ -225,19 +225,49 @@ def test_batch_two_equals_batch_one(small_model):
 
 
 def test_batch_eight_equals_batch_one(small_model):
-    """Batch 8 runs QKV in two row groups of 4 and down in four groups of 2;
-    every sequence reproduces the batch-1 stream."""
+    """Batch 8 runs Q and K/V as two launches, the down projection with its
+    inputs staged in 4096-wide blocks, and the 8-row gate/up, O and LM-head
+    kernels; every sequence reproduces the batch-1 stream and its last
+    logits bit for bit."""
     from dolittle_amd.qwen3 import Plan
     prompt = [9, 150000, 3, 77, 4096]
     p1 = Plan(small_model, batch=1, capacity=32)
     p1.generate(prompt, 10)
     t1, _ = p1.collect()
+    l1 = p1.logits(0)
     p8 = Plan(small_model, batch=8, capacity=32)
     p8.generate(prompt, 10)
     t8, res = p8.collect()
     for b in range(8):
         assert t8[b].tolist() == t1[0].tolist(), b
         assert res[b]["generated"] == 10
+        assert np.array_equal(p8.logits(b), l1), b
+
+
+@pytest.mark.parametrize("batch", [3, 4, 5, 8])
+def test_batched_rows_follow_their_own_sequences(small_model, batch):
+    """Each sequence of a batched plan samples with its own MT19937-64 seed,
+    so the rows diverge; every row's token stream and last logits equal a
+    batch-1 run with that seed.  Covers the row groups of odd batches (3 = 2
+    + 1, 5 = 4 + 1) and the 4- and 8-row kernels, where a row read from or
+    written to the wrong sequence would show."""
+    from dolittle_amd.qwen3 import Plan, SamplingSettings
+    prompt = [11, 4242, 90000, 7]
+    settings = SamplingSettings("categorical", 1.0, 0, 0.95)
+    seeds = [1000 + 17 * b for b in range(batch)]
+    pb = Plan(small_model, batch=batch, capacity=24)
+    pb.generate(prompt, 12, settings, seeds)
+    tb, res = pb.collect()
+    streams = set()
+    for b in range(batch):
+        p1 = Plan(small_model, batch=1, capacity=24)
+        p1.generate(prompt, 12, settings, [seeds[b]])
+        t1, _ = p1.collect()
+        assert tb[b].tolist() == t1[0].tolist(), b
+        assert res[b]["generated"] == 12
+        assert np.array_equal(pb.logits(b), p1.logits(0)), b
+        streams.add(tuple(t1[0].tolist()))
+    assert len(streams) > 1  # the rows really differ
 
 
 def _categorical_run(plan, prompt, max_new, settings, seeds, override=None, stop_ids=None):
