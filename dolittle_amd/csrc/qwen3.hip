@@ -587,7 +587,7 @@ constexpr int kFusedKeys = 1024;
 constexpr int kAttnThreads = 512;
 constexpr int kAttnKeysPerPass = kAttnThreads / 8;
 constexpr int kAttnKeyPasses = 8;     // key rows issued at kernel entry: 512 keys
-constexpr int kAttnValueBlocks = 8;  // 8-key V blocks per PV chain issued at entry
+constexpr int kAttnValueBlocks = 8;  // 8-key V blocks per PV chain issued at entry (one 64-key block)
 
 __global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
   __shared__ float qs[kHeadDim];
@@ -628,8 +628,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
   // PV chains: thread f + 128 * half (half 0: keys [0, split), half 1:
   // [split, count)), one chain per lane; waves 0-1 and 2-3 hold the halves.
   const int split = (count - 1) / 2 + 1;
-  const int f = tid % kHeadDim, half = (tid / kHeadDim) & 1;
-  const bool chain = tid < 2 * kHeadDim;
+  // Wave-uniform chain half (waves 0-1: keys [0, split), waves 2-3: the
+  // rest), so the PV loop bounds stay in scalar registers.
+  const int half = __builtin_amdgcn_readfirstlane(wave) / 2;
+  const int f = tid % kHeadDim;
+  const bool chain = wave < 4;
   const int begin = half ? split : 0, end = half ? count : split;
   const int first_block = begin & ~7;
   const uint16_t* v = a.v_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g * kHeadDim + f) * a.cap;
@@ -714,54 +717,62 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
   for (int j = tid; j < count; j += kAttnThreads) sc[j] = sc[j] / denominator;
   __syncthreads();
 
-  // PV: two ascending FMA chains over [0, split) and [split, count), read
-  // as aligned 8-key blocks.  Only the chain's first and last blocks can be
-  // partial (keys outside the chain are skipped there); full blocks read
-  // their eight probabilities as two float4s.
+  // PV: two ascending FMA chains over [0, split) and [split, count), in
+  // 64-key blocks from the 8-aligned key below `begin`; the first and last
+  // block mask the keys outside the chain.  A block's 64 probabilities are
+  // read from LDS as 16 float4s before its FMAs, and the next block's V
+  // rows are in flight meanwhile (two register buffers, uniform trip count).
+  // Loads past the chain are clamped to its last 8 keys (4 for the
+  // probabilities) and never used.
   if (chain) {
     float acc = 0.0f;
-    auto partial = [&](int jb, const u32x4 vv) {
-      const float x[8] = {dl_bf16_lo(vv.x), dl_bf16_hi(vv.x), dl_bf16_lo(vv.y), dl_bf16_hi(vv.y),
-                          dl_bf16_lo(vv.z), dl_bf16_hi(vv.z), dl_bf16_lo(vv.w), dl_bf16_hi(vv.w)};
+    const int blocks = end > begin ? (end - first_block + 63) / 64 : 0;
+    const int last8 = (end - 1) & ~7, last4 = (end - 1) & ~3;
+    auto load = [&](u32x4* vb, int x) {
+      const int jb = first_block + 64 * min(x, blocks - 1);
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (jb + e >= begin && jb + e < end) acc = fma_rn(sc[jb + e], x[e], acc);
+      for (int i = 0; i < 8; ++i) vb[i] = *reinterpret_cast<const u32x4*>(v + min(jb + 8 * i, last8));
     };
-    auto full = [&](int jb, const u32x4 vv) {
-      const float4 p0 = *reinterpret_cast<const float4*>(sc + jb);
-      const float4 p1 = *reinterpret_cast<const float4*>(sc + jb + 4);
-      acc = fma_rn(p0.x, dl_bf16_lo(vv.x), acc);
-      acc = fma_rn(p0.y, dl_bf16_hi(vv.x), acc);
-      acc = fma_rn(p0.z, dl_bf16_lo(vv.y), acc);
-      acc = fma_rn(p0.w, dl_bf16_hi(vv.y), acc);
-      acc = fma_rn(p1.x, dl_bf16_lo(vv.z), acc);
-      acc = fma_rn(p1.y, dl_bf16_hi(vv.z), acc);
-      acc = fma_rn(p1.z, dl_bf16_lo(vv.w), acc);
-      acc = fma_rn(p1.w, dl_bf16_hi(vv.w), acc);
-    };
-    auto consume = [&](int jb, const u32x4 vv) {
-      if (jb >= begin && jb + 8 <= end)
-        full(jb, vv);
-      else
-        partial(jb, vv);
-    };
+    auto run = [&](const u32x4* vb, int x) {
+      const int jb = first_block + 64 * x;
+      float4 pc[16];
 #pragma unroll
-    for (int i = 0; i < kAttnValueBlocks; ++i) {
-      const int jb = first_block + 8 * i;
-      if (jb < end) consume(jb, vpre[i]);
-    }
-    for (int jb0 = first_block + 8 * kAttnValueBlocks; jb0 < end; jb0 += 8 * kAttnValueBlocks) {
-      u32x4 vb[kAttnValueBlocks];
+      for (int i = 0; i < 16; ++i) pc[i] = *reinterpret_cast<const float4*>(sc + min(jb + 4 * i, last4));
+      const int lo = max(begin - jb, 0), hi = min(end - jb, 64);
 #pragma unroll
-      for (int i = 0; i < kAttnValueBlocks; ++i) {
-        const int jb = min(jb0 + 8 * i, a.cap - 8);
-        vb[i] = *reinterpret_cast<const u32x4*>(v + jb);
+      for (int i = 0; i < 8; ++i) {
+        const float vf[8] = {dl_bf16_lo(vb[i].x), dl_bf16_hi(vb[i].x), dl_bf16_lo(vb[i].y), dl_bf16_hi(vb[i].y),
+                             dl_bf16_lo(vb[i].z), dl_bf16_hi(vb[i].z), dl_bf16_lo(vb[i].w), dl_bf16_hi(vb[i].w)};
+        const float pf[8] = {pc[2 * i].x, pc[2 * i].y, pc[2 * i].z, pc[2 * i].w,
+                             pc[2 * i + 1].x, pc[2 * i + 1].y, pc[2 * i + 1].z, pc[2 * i + 1].w};
+        if (lo == 0 && hi == 64) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc = fma_rn(pf[e], vf[e], acc);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float t = fma_rn(pf[e], vf[e], acc);
+            acc = (8 * i + e >= lo && 8 * i + e < hi) ? t : acc;
+          }
+        }
       }
+    };
+    if (blocks > 0) {
+      u32x4 va[8], vb[8];
 #pragma unroll
-      for (int i = 0; i < kAttnValueBlocks; ++i) {
-        const int jb = jb0 + 8 * i;
-        if (jb < end) consume(jb, vb[i]);
+      for (int i = 0; i < 8; ++i) va[i] = vpre[i];
+      int x = 0;
+      for (; x + 2 <= blocks; x += 2) {
+        load(vb, x + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        run(va, x);
+        __builtin_amdgcn_sched_barrier(0);
+        load(va, x + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        run(vb, x + 1);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      if (x < blocks) run(va, x);
     }
     red[tid] = acc;
   }
