@@ -49,6 +49,37 @@ __device__ __forceinline__ float silu_times(float a, float b) {
 }
 
 // ------------------------------------------------------------------ GEMM
+// Output element (m, n) of a GEMM tile through the epilogue EPI.  Every lane
+// of the wavefront calls it for the same r (the gate/up epilogue reads the
+// up value of its column from two lanes up).
+template <int EPI>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int m, int n, float v, int lane) {
+  if constexpr (EPI == kStore) {
+    a.out[static_cast<uint64_t>(m) * a.N + n] = dl_f32_to_bf16(v);
+  } else if constexpr (EPI == kResidual) {
+    uint16_t* o = a.out + static_cast<uint64_t>(m) * a.N + n;
+    *o = dl_f32_to_bf16(dl_bf16_to_f32(*o) + dl_round_bf16(v));
+  } else if constexpr (EPI == kStoreQkv) {
+    if (n < a.q_width) {
+      a.out[static_cast<uint64_t>(m) * a.q_width + n] = dl_f32_to_bf16(v);
+    } else if (n < a.q_width + a.kv_width) {
+      a.out2[static_cast<uint64_t>(m) * a.kv_width + (n - a.q_width)] = dl_f32_to_bf16(v);
+    } else if (m < a.m_valid) {
+      a.v_cache[static_cast<uint64_t>(n - a.q_width - a.kv_width) * a.cap + a.first_position + m] =
+          dl_f32_to_bf16(v);
+    }
+  } else {
+    // Columns 4j..4j+3 hold gate rows 2j, 2j+1 and up rows 2j, 2j+1;
+    // the up value of column n sits two lanes up.
+    const float up = __shfl(v, (lane + 2) & 63);
+    if ((n & 3) < 2) {
+      const uint32_t f = 2 * (n / 4) + (n & 3);
+      a.out[static_cast<uint64_t>(m) * (a.N / 2) + permuted(f, 32)] =
+          dl_f32_to_bf16(silu_times(dl_round_bf16(v), dl_round_bf16(up)));
+    }
+  }
+}
+
 // C[M x N] = A[M x K] W[N x K]^T over permuted positions.  Tile 128 x 128,
 // K chunks of 64 positions double-buffered through LDS, 32x32x16 BF16 MFMA.
 template <int EPI>
@@ -150,34 +181,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
     for (int j = 0; j < 2; ++j) {
       const int n = n0 + 64 * wn + 32 * j + lane % 32;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + 64 * wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-        const float v = acc[i][j][r];
-        if constexpr (EPI == kStore) {
-          a.out[static_cast<uint64_t>(m) * a.N + n] = dl_f32_to_bf16(v);
-        } else if constexpr (EPI == kResidual) {
-          uint16_t* o = a.out + static_cast<uint64_t>(m) * a.N + n;
-          *o = dl_f32_to_bf16(dl_bf16_to_f32(*o) + dl_round_bf16(v));
-        } else if constexpr (EPI == kStoreQkv) {
-          if (n < a.q_width) {
-            a.out[static_cast<uint64_t>(m) * a.q_width + n] = dl_f32_to_bf16(v);
-          } else if (n < a.q_width + a.kv_width) {
-            a.out2[static_cast<uint64_t>(m) * a.kv_width + (n - a.q_width)] = dl_f32_to_bf16(v);
-          } else if (m < a.m_valid) {
-            a.v_cache[static_cast<uint64_t>(n - a.q_width - a.kv_width) * a.cap + a.first_position + m] =
-                dl_f32_to_bf16(v);
-          }
-        } else {
-          // Columns 4j..4j+3 hold gate rows 2j, 2j+1 and up rows 2j, 2j+1;
-          // the up value of column n sits two lanes up.
-          const float up = __shfl(v, (lane + 2) & 63);
-          if ((n & 3) < 2) {
-            const uint32_t f = 2 * (n / 4) + (n & 3);
-            a.out[static_cast<uint64_t>(m) * (a.N / 2) + permuted(f, 32)] =
-                dl_f32_to_bf16(silu_times(dl_round_bf16(v), dl_round_bf16(up)));
-          }
-        }
-      }
+      for (int r = 0; r < 16; ++r)
+        gemm_epilogue<EPI>(a, m0 + 64 * wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + r % 4, n, acc[i][j][r], lane);
     }
   }
 }
@@ -293,17 +298,31 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
 
   const int last_row = min(q0 + kAttnRows, a.rows) - 1;
   const int key_end = a.first_position + last_row + 1;
+  // K and V tiles go through registers: the next tile's loads are issued
+  // before this tile's products, and stored to LDS once every wave is done
+  // with the previous tile.
+  u32x4 kr[4], vr[4];
+  auto load_tile = [&](int kt0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = tid + kAttnThreads * j;
+      const int key = i / 16, col = (i % 16) * 8;
+      const int kk = min(kt0 + key, a.cap - 1);
+      kr[j] = *reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(kk) * kHd + col);
+      const int d = i / 8, vcol = (i % 8) * 8;
+      vr[j] = *reinterpret_cast<const u32x4*>(vc + static_cast<uint64_t>(d) * a.cap + min(kt0 + vcol, a.cap - 8));
+    }
+  };
+  load_tile(0);
   for (int kt0 = 0; kt0 < key_end; kt0 += kKeyTile) {
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int i = tid + kAttnThreads * j;
       const int key = i / 16, col = (i % 16) * 8;
-      const int kk = min(kt0 + key, a.cap - 1);
-      *reinterpret_cast<u32x4*>(&Ks[key * kQRow + col]) =
-          *reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(kk) * kHd + col);
+      *reinterpret_cast<u32x4*>(&Ks[key * kQRow + col]) = kr[j];
       const int d = i / 8, vcol = (i % 8) * 8;
-      u32x4 vv = *reinterpret_cast<const u32x4*>(vc + static_cast<uint64_t>(d) * a.cap + kt0 + vcol);
+      u32x4 vv = vr[j];
       // Keys at or past key_end are masked for every row of this tile (p = 0);
       // zero them so stale cache contents cannot turn 0 * v into NaN.
       const int left = key_end - (kt0 + vcol);
@@ -317,6 +336,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
       *reinterpret_cast<u32x4*>(&Vs[d * kVRow + vcol]) = vv;
     }
     __syncthreads();
+    if (kt0 + kKeyTile < key_end) load_tile(kt0 + kKeyTile);
 
     floatx4 s[4];
 #pragma unroll

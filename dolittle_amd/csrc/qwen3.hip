@@ -299,6 +299,10 @@ struct AttnArgs {
   uint16_t* att;             // [B][Hq*128]
   int q_heads, kv_heads, cap;
   float eps, scale;
+  // Row b is at position ctl->position + b * pos_step: 0 when the rows are
+  // sequences at one position (decode), 1 when they are consecutive
+  // positions of one sequence (cache_seq_stride 0, chunked prompt pass).
+  int pos_step;
 };
 
 
@@ -309,9 +313,9 @@ __global__ __launch_bounds__(kBlock) void k_attn_qk(AttnArgs a) {
   __shared__ float qs[4][kHeadDim];
   __shared__ float ks[kHeadDim];
   if (!a.ctl->active) return;
-  const uint64_t pos = a.ctl->position;
-  const int count = static_cast<int>(pos) + 1;
   const int g = blockIdx.x, key0 = blockIdx.y * 64, b = blockIdx.z;
+  const uint64_t pos = a.ctl->position + static_cast<uint64_t>(b) * a.pos_step;
+  const int count = static_cast<int>(pos) + 1;
   if (key0 >= count) return;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int group = a.q_heads / a.kv_heads;
@@ -379,8 +383,8 @@ __global__ __launch_bounds__(kBlock) void k_attn_softmax(AttnArgs a) {
   __shared__ float wave_max[kBlock / 64];
   __shared__ float denominator_shared;
   if (!a.ctl->active) return;
-  const int count = static_cast<int>(a.ctl->position) + 1;
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int count = static_cast<int>(a.ctl->position + static_cast<uint64_t>(b) * a.pos_step) + 1;
   const uint64_t row = (static_cast<uint64_t>(b) * a.q_heads + h) * a.cap;
   const float* sc = a.scores + row;
   float m = sc[0];
@@ -482,10 +486,10 @@ constexpr int kPvBuffers = 4;
 __global__ __launch_bounds__(kPvThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_attn_pv(AttnArgs a) {
   __shared__ float second[64];
   if (!a.ctl->active) return;
-  const int count = static_cast<int>(a.ctl->position) + 1;
-  const int split = (count - 1) / 2 + 1;
   constexpr int kBlocksPerGroup = kHeadDim / kPvFeatures;
   const int g = blockIdx.x / kBlocksPerGroup, fb = blockIdx.x % kBlocksPerGroup, b = blockIdx.y;
+  const int count = static_cast<int>(a.ctl->position + static_cast<uint64_t>(b) * a.pos_step) + 1;
+  const int split = (count - 1) / 2 + 1;
   // Wave-uniform wave index: the key ranges and loop bounds below stay in
   // scalar registers, so the loops branch on scalars.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
@@ -597,9 +601,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
   __shared__ float wave_max[kAttnThreads / 64];
   __shared__ float denominator_shared;
   if (!a.ctl->active) return;
-  const uint64_t pos = a.ctl->position;
-  const int count = static_cast<int>(pos) + 1;
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const uint64_t pos = a.ctl->position + static_cast<uint64_t>(b) * a.pos_step;
+  const int count = static_cast<int>(pos) + 1;
   const int wave = tid / 64, lane = tid % 64;
   const int group = a.q_heads / a.kv_heads;
   const int g = h / group;
@@ -789,7 +793,11 @@ struct ResidualArgs {
   uint16_t* capture;     // [B][cap][D] or null
   const float* steer;    // [B][D] or null
   int I, D, cap, layer;
-  int row0;              // first sequence of this launch's row group
+  int row0;              // first row of this launch's row group
+  // Rows are sequences (decode: row r is sequence r at ctl->position), or,
+  // with same_sequence, consecutive positions of sequence `sequence`
+  // (row r at ctl->position + r; chunked prompt pass).
+  int same_sequence, sequence;
 };
 
 // y = round(x W^T); h = round(h + y); optionally h = round(h + steer) and a
@@ -822,12 +830,16 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual(ResidualArgs a)
       const int row = tile * RW + lane / P;
 #pragma unroll
       for (int b = 0; b < B; ++b) {
-        const int seq = a.row0 + b;
-        const uint64_t at = static_cast<uint64_t>(seq) * a.D + row;
+        const int r = a.row0 + b;
+        const int seq = a.same_sequence ? a.sequence : r;
+        const uint64_t at = static_cast<uint64_t>(r) * a.D + row;
         float value = rbf(dl_bf16_to_f32(a.h[at]) + rbf(acc[b]));
-        if (steer && ((steer_mask >> seq) & 1u)) value = rbf(value + a.steer[at]);
+        if (steer && ((steer_mask >> seq) & 1u)) value = rbf(value + a.steer[static_cast<uint64_t>(seq) * a.D + row]);
         a.h[at] = bf16_bits(value);
-        if (capture) a.capture[(static_cast<uint64_t>(seq) * a.cap + pos) * a.D + row] = bf16_bits(value);
+        if (capture) {
+          const uint64_t at_pos = a.same_sequence ? pos + r : pos;
+          a.capture[(static_cast<uint64_t>(seq) * a.cap + at_pos) * a.D + row] = bf16_bits(value);
+        }
       }
     }
   }
@@ -885,12 +897,16 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual_chunked(Residua
       const int row = tile * RW + lane / P;
 #pragma unroll
       for (int b = 0; b < B; ++b) {
-        const int seq = a.row0 + b;
-        const uint64_t at = static_cast<uint64_t>(seq) * a.D + row;
+        const int r = a.row0 + b;
+        const int seq = a.same_sequence ? a.sequence : r;
+        const uint64_t at = static_cast<uint64_t>(r) * a.D + row;
         float value = rbf(dl_bf16_to_f32(a.h[at]) + rbf(acc[b]));
-        if (steer && ((steer_mask >> seq) & 1u)) value = rbf(value + a.steer[at]);
+        if (steer && ((steer_mask >> seq) & 1u)) value = rbf(value + a.steer[static_cast<uint64_t>(seq) * a.D + row]);
         a.h[at] = bf16_bits(value);
-        if (capture) a.capture[(static_cast<uint64_t>(seq) * a.cap + pos) * a.D + row] = bf16_bits(value);
+        if (capture) {
+          const uint64_t at_pos = a.same_sequence ? pos + r : pos;
+          a.capture[(static_cast<uint64_t>(seq) * a.cap + at_pos) * a.D + row] = bf16_bits(value);
+        }
       }
     }
   }
@@ -1147,6 +1163,37 @@ __global__ void k_bench_control(const Control* live, Control* bench) {
   c.steer_layer = -1;
   if (c.position >= 1) c.position -= 1;
   *bench = c;
+}
+
+// Control of one chunk of the exact prompt pass: the live control with the
+// loop active at `position` and the plan's capture / steering settings.
+__global__ void k_chunk_control(const Control* live, Control* chunk, uint64_t position, int32_t capture_layer,
+                                int32_t steer_layer, uint32_t steer_mask) {
+  Control c = *live;
+  c.active = 1;
+  c.position = position;
+  c.capture_layer = capture_layer;
+  c.steer_layer = steer_layer;
+  c.steer_mask = steer_mask;
+  *chunk = c;
+}
+
+// Rotated keys of the rows of a chunk (consecutive positions of one
+// sequence) written to the cache before the chunk's attention, which reads
+// its predecessors' keys from there (rotary.cu:84-126).  Grid (kv head, row),
+// one wavefront.
+__global__ __launch_bounds__(64) void k_append_keys(AttnArgs a) {
+  __shared__ float ks[kHeadDim];
+  if (!a.ctl->active) return;
+  const int g = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const uint64_t pos = a.ctl->position + static_cast<uint64_t>(b) * a.pos_step;
+  const uint64_t kw = static_cast<uint64_t>(a.kv_heads) * kHeadDim;
+  head_norm_rope(a.k_raw + b * kw + static_cast<uint64_t>(g) * kHeadDim, a.k_norm, a.rope + pos * kHeadDim, lane,
+                 a.eps, ks);
+  __syncthreads();
+  uint16_t* kc = a.k_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g) * a.cap * kHeadDim;
+  kc[pos * kHeadDim + lane] = bf16_bits(ks[lane]);
+  kc[pos * kHeadDim + lane + 64] = bf16_bits(ks[lane + 64]);
 }
 
 __global__ void k_seek(Control* c, uint64_t position) {
@@ -1523,6 +1570,13 @@ struct dl_plan {
              *att = nullptr, *act = nullptr;
     uint32_t rows = 0;  // allocated rows (multiple of 128)
   } pf;
+  // Exact chunked prompt pass: row buffers for kMaxBatch consecutive
+  // positions of one sequence and the chunk's control (first use).
+  struct Chunk {
+    uint16_t *h = nullptr, *q = nullptr, *k = nullptr, *att = nullptr, *act = nullptr;
+    float *scores = nullptr, *probs = nullptr;
+    dl::Control* ctl = nullptr;
+  } ex;
   std::vector<uint32_t> prefilled_prompt;
   uint32_t prefilled = 0;
   uint64_t start_position = 0;  // position the prepared generation starts at
@@ -1652,26 +1706,45 @@ void launch_head(dl_plan* p, hipStream_t s, const dl::HeadArgs& a) {
   dl::k_lm_head<G><<<p->head_blocks, dl::gemv_waves(G) * 64, p16_lds(G, a.D), s>>>(a);
 }
 
+// The rows one step works on.  For the token loop they are the plan's
+// sequences at one position; for the exact chunked prompt pass they are up
+// to kMaxBatch consecutive positions of one sequence, in their own buffers.
+struct StepRows {
+  uint16_t *h, *q_raw, *k_raw, *att, *act;
+  float *scores, *probs;
+  uint32_t rows;
+  uint64_t cache_base;       // element offset of row 0's sequence in the K and V caches
+  uint64_t v_append_stride;  // QKV epilogue: V element offset from row r to row r + 1
+  uint64_t attn_seq_stride;  // attention: cache offset from row r to row r + 1
+  int pos_step;              // row r is at ctl->position + r * pos_step
+  int same_sequence, sequence;
+};
+
+StepRows plan_rows(const dl_plan* p) {
+  return StepRows{p->h, p->q_raw, p->k_raw, p->att, p->act, p->scores, p->probs, p->batch, 0,
+                  p->cache_seq_stride, p->cache_seq_stride, 0, 0, 0};
+}
+
 // Launches one decode-step kernel `which` of layer `l` with control `ctl`
-// over every sequence of the plan.
-void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Control* ctl) {
+// over the rows `r` (every sequence of the plan unless given).
+void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Control* ctl, const StepRows& r) {
   using namespace dl;
   const dl_qwen3* m = p->model;
   const auto& c = m->cfg;
   const int D = c.hidden, QW = c.q_heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
-  const uint32_t V = c.vocab, B = p->batch;
+  const uint32_t V = c.vocab, B = r.rows;
   const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));
-  uint16_t* kc = p->k_cache + uint64_t(l) * p->cache_layer_stride;
-  uint16_t* vc = p->v_cache + uint64_t(l) * p->cache_layer_stride;
-  AttnArgs aa{ctl, p->q_raw, p->k_raw, m->q_norm[l], m->k_norm[l], p->rope, kc, vc, p->cache_seq_stride,
-              p->scores, p->probs, p->att, static_cast<int>(c.q_heads), static_cast<int>(c.kv_heads),
-              static_cast<int>(p->cap), c.rms_eps, scale};
+  uint16_t* kc = p->k_cache + uint64_t(l) * p->cache_layer_stride + r.cache_base;
+  uint16_t* vc = p->v_cache + uint64_t(l) * p->cache_layer_stride + r.cache_base;
+  AttnArgs aa{ctl, r.q_raw, r.k_raw, m->q_norm[l], m->k_norm[l], p->rope, kc, vc, r.attn_seq_stride,
+              r.scores, r.probs, r.att, static_cast<int>(c.q_heads), static_cast<int>(c.kv_heads),
+              static_cast<int>(p->cap), c.rms_eps, scale, r.pos_step};
   switch (which) {
     case 0:
       for_row_groups(B, kQkvRows, [&](uint32_t r0, int g) {
-        QkvArgs qa{ctl, p->h + uint64_t(r0) * D, m->input_norm[l], reinterpret_cast<const u32x4*>(m->qkv[l]),
-                   p->q_raw + uint64_t(r0) * QW, p->k_raw + uint64_t(r0) * KW, vc + r0 * p->cache_seq_stride,
-                   p->cache_seq_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps};
+        QkvArgs qa{ctl, r.h + uint64_t(r0) * D, m->input_norm[l], reinterpret_cast<const u32x4*>(m->qkv[l]),
+                   r.q_raw + uint64_t(r0) * QW, r.k_raw + uint64_t(r0) * KW, vc + r0 * r.v_append_stride,
+                   r.v_append_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps};
         if (g == 8) {
           launch_qkv<8, kQkvQ>(p, s, qa);
           launch_qkv<8, kQkvKV>(p, s, qa);
@@ -1688,10 +1761,12 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
     case 2: k_attn_softmax<<<dim3(c.q_heads, B), kBlock, size_t(p->cap) * sizeof(float), s>>>(aa); break;
     case 3: k_attn_pv<<<dim3(c.kv_heads * (kHeadDim / kPvFeatures), B), kPvThreads, 0, s>>>(aa); break;
     case 8: k_attn_fused<<<dim3(c.q_heads, B), kAttnThreads, 0, s>>>(aa); break;
+    case 9: k_append_keys<<<dim3(c.kv_heads, B), 64, 0, s>>>(aa); break;
     case 4:
       for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
-        ResidualArgs oa{ctl, p->att, reinterpret_cast<const u32x4*>(m->o[l]), p->h, nullptr, nullptr, QW, D,
-                        static_cast<int>(p->cap), static_cast<int>(l), static_cast<int>(r0)};
+        ResidualArgs oa{ctl, r.att, reinterpret_cast<const u32x4*>(m->o[l]), r.h, nullptr, nullptr, QW, D,
+                        static_cast<int>(p->cap), static_cast<int>(l), static_cast<int>(r0), r.same_sequence,
+                        r.sequence};
         if (g == 8) launch_residual<16, 8>(p, s, 4, oa);
         else if (g == 4) launch_residual<16, 4>(p, s, 4, oa);
         else if (g == 2) launch_residual<16, 2>(p, s, 4, oa);
@@ -1700,8 +1775,8 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       break;
     case 5:
       for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
-        GateUpArgs ga{ctl, p->h + uint64_t(r0) * D, m->post_norm[l], reinterpret_cast<const u32x4*>(m->gu[l]),
-                      p->act + uint64_t(r0) * F, D, F, c.rms_eps};
+        GateUpArgs ga{ctl, r.h + uint64_t(r0) * D, m->post_norm[l], reinterpret_cast<const u32x4*>(m->gu[l]),
+                      r.act + uint64_t(r0) * F, D, F, c.rms_eps};
         if (g == 8) launch_gateup<8>(p, s, ga);
         else if (g == 4) launch_gateup<4>(p, s, ga);
         else if (g == 2) launch_gateup<2>(p, s, ga);
@@ -1712,8 +1787,9 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       // Staging in blocks needs whole blocks of inputs; other widths keep
       // two-row launches.
       for_row_groups(B, F % kChunkInputs == 0 ? kDownRows : 2, [&](uint32_t r0, int g) {
-        ResidualArgs da{ctl, p->act, reinterpret_cast<const u32x4*>(m->down[l]), p->h, p->capture, p->steer, F, D,
-                        static_cast<int>(p->cap), static_cast<int>(l), static_cast<int>(r0)};
+        ResidualArgs da{ctl, r.act, reinterpret_cast<const u32x4*>(m->down[l]), r.h, p->capture, p->steer, F, D,
+                        static_cast<int>(p->cap), static_cast<int>(l), static_cast<int>(r0), r.same_sequence,
+                        r.sequence};
         if (g == 8) launch_down_chunked<8>(p, s, da);
         else if (g == 4) launch_down_chunked<4>(p, s, da);
         else if (g == 2) launch_residual<32, 2>(p, s, 6, da);
@@ -1722,7 +1798,7 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       break;
     case 7:
       for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
-        HeadArgs ha{ctl, p->h, m->final_norm, reinterpret_cast<const u32x4*>(m->lm_head), p->logits,
+        HeadArgs ha{ctl, r.h, m->final_norm, reinterpret_cast<const u32x4*>(m->lm_head), p->logits,
                     p->partial_keys, p->partial_flags, D, V, c.rms_eps, static_cast<int>(r0)};
         if (g == 8) launch_head<8>(p, s, ha);
         else if (g == 4) launch_head<4>(p, s, ha);
@@ -1748,11 +1824,11 @@ void record_step_all(dl_plan* p, hipStream_t s, bool short_context) {
   static const int kLong[] = {0, 1, 2, 3, 4, 5, 6};
   for (uint32_t l = 0; l < c.layers; ++l) {
     if (short_context)
-      for (int which : kShort) launch_step_kernel(p, s, which, l, p->ctl);
+      for (int which : kShort) launch_step_kernel(p, s, which, l, p->ctl, plan_rows(p));
     else
-      for (int which : kLong) launch_step_kernel(p, s, which, l, p->ctl);
+      for (int which : kLong) launch_step_kernel(p, s, which, l, p->ctl, plan_rows(p));
   }
-  launch_step_kernel(p, s, 7, 0, p->ctl);
+  launch_step_kernel(p, s, 7, 0, p->ctl, plan_rows(p));
   if (p->sampling.mode == 1) {
     sampling::RowsArgs ra{};
     ra.logits = p->logits;
@@ -1925,7 +2001,7 @@ int dl_plan_launch_kernel(dl_plan* plan, uint32_t which, uint32_t first_layer, u
     require(first_layer < L, "layer out of range");
     for (uint32_t i = 0; i < count; ++i) {
       const uint32_t l = (first_layer + i) % L;
-      launch_step_kernel(plan, plan->queue->stream, static_cast<int>(which), l, plan->bench_ctl);
+      launch_step_kernel(plan, plan->queue->stream, static_cast<int>(which), l, plan->bench_ctl, plan_rows(plan));
     }
     dl::check_launch(plan->queue, "step kernel");
   });
@@ -2286,6 +2362,37 @@ int dl_plan_request_stop(dl_plan* plan) {
 }
 
 
+// True when the prompt pass differs between the plan's sequences (steering
+// or an embedding override applied to some of them, or capture, which writes
+// every sequence's arena), so each sequence needs its own pass.
+static bool sequences_differ(const dl_plan* plan) {
+  const uint32_t all = (1u << plan->batch) - 1u;
+  const bool override_differs =
+      plan->override_active && (plan->override_mask & all) != 0 && (plan->override_mask & all) != all;
+  return plan->batch > 1 && (plan->steer_mask != 0 || plan->capture_layer >= 0 || override_differs);
+}
+
+// Copies sequence 0's cached positions [0, rows) into the other sequences'
+// caches (a prompt shared by every sequence).
+static void copy_prefix_to_other_sequences(dl_plan* plan, uint32_t rows) {
+  const auto& c = plan->model->cfg;
+  const uint64_t KW = uint64_t(c.kv_heads) * c.head_dim;
+  hipStream_t s = plan->queue->stream;
+  for (uint32_t b = 1; b < plan->batch; ++b) {
+    const uint64_t off = uint64_t(b) * plan->cache_seq_stride;
+    // The cache of one sequence: for every layer, K [Hkv][cap][128] then the
+    // layer's V^T [Hkv*128][cap] at the same layer offset.
+    dl::check_hip(hipMemcpy2DAsync(plan->k_cache + off, uint64_t(plan->cap) * c.head_dim * 2, plan->k_cache,
+                                   uint64_t(plan->cap) * c.head_dim * 2, uint64_t(rows) * c.head_dim * 2,
+                                   uint64_t(c.layers) * c.kv_heads, hipMemcpyDeviceToDevice, s),
+                  "prefill K copy");
+    dl::check_hip(hipMemcpy2DAsync(plan->v_cache + off, uint64_t(plan->cap) * 2, plan->v_cache,
+                                   uint64_t(plan->cap) * 2, uint64_t(rows) * 2, uint64_t(c.layers) * KW,
+                                   hipMemcpyDeviceToDevice, s),
+                  "prefill V copy");
+  }
+}
+
 int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length) {
   return guard([&] {
     require(plan && prompt, "null argument");
@@ -2322,8 +2429,9 @@ int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_lengt
     dl::check_hip(hipMemcpyAsync(plan->tokens, prompt, prompt_length * 4ull, hipMemcpyHostToDevice, s), "prompt");
     const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));
     // Sequences share the prompt: prefill each separately only when
-    // steering or capture differs between them, else copy sequence 0.
-    const bool per_sequence = plan->batch > 1 && (plan->steer_mask != 0 || plan->capture_layer >= 0);
+    // steering, capture or an embedding override differs between them,
+    // else copy sequence 0.
+    const bool per_sequence = sequences_differ(plan);
     const uint32_t runs = per_sequence ? plan->batch : 1;
     for (uint32_t seq = 0; seq < runs; ++seq) {
       dl::PrefillEmbedArgs ea{plan->tokens, m->lm_head, m->embedding, plan->override_row, pf.h, rows, D, 0,
@@ -2407,21 +2515,77 @@ int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_lengt
       }
       dl::check_launch(plan->queue, "prefill");
     }
-    if (!per_sequence) {
-      // Copy sequence 0's prefilled rows into the other sequences' caches.
-      for (uint32_t b = 1; b < plan->batch; ++b) {
-        const uint64_t off = uint64_t(b) * plan->cache_seq_stride;
-        dl::check_hip(hipMemcpy2DAsync(plan->k_cache + off, uint64_t(plan->cap) * c.head_dim * 2, plan->k_cache,
-                                       uint64_t(plan->cap) * c.head_dim * 2, uint64_t(rows) * c.head_dim * 2,
-                                       uint64_t(c.layers) * c.kv_heads, hipMemcpyDeviceToDevice, s),
-                      "prefill K copy");
-        dl::check_hip(hipMemcpy2DAsync(plan->v_cache + off, uint64_t(plan->cap) * 2, plan->v_cache,
-                                       uint64_t(plan->cap) * 2, uint64_t(rows) * 2, uint64_t(c.layers) * KW,
-                                       hipMemcpyDeviceToDevice, s),
-                      "prefill V copy");
-      }
-    }
+    if (!per_sequence) copy_prefix_to_other_sequences(plan, rows);
     dl::check_hip(hipStreamSynchronize(s), "prefill");
+    plan->prefilled = rows;
+  });
+}
+
+// The exact prompt pass: positions [0, prompt_length - 1) in chunks of up to
+// kMaxBatch consecutive positions through the decode kernels, rows = positions
+// (StepRows with pos_step 1).  Every projection row is the same FMA chain as
+// a single-position step, the chunk's keys are in the cache before its
+// attention, and each row attends to keys [0, its position], so the caches
+// are bit-identical to consuming the prompt one position per step.
+int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length) {
+  return guard([&] {
+    require(plan && prompt, "null argument");
+    dl::enter(plan->queue);
+    const dl_qwen3* m = plan->model;
+    const auto& c = m->cfg;
+    require(prompt_length > 0, "empty prompt");
+    require(prompt_length <= plan->capacity, "prompt exceeds the cache capacity", DL_LENGTH_ERROR);
+    for (uint32_t i = 0; i < prompt_length; ++i) require(prompt[i] < c.vocab, "prompt id outside the vocabulary");
+    hipStream_t s = plan->queue->stream;
+    dl::check_hip(hipStreamSynchronize(s), "prefill wait");
+    plan->prefilled = 0;
+    plan->prefilled_prompt.assign(prompt, prompt + prompt_length);
+    const uint32_t rows = prompt_length - 1;
+    if (rows == 0) return;
+    const uint64_t D = c.hidden, QW = uint64_t(c.q_heads) * c.head_dim, KW = uint64_t(c.kv_heads) * c.head_dim,
+                   F = c.ffn, R = dl::kMaxBatch;
+    auto& ex = plan->ex;
+    if (!ex.ctl) {
+      ex.h = plan->alloc<uint16_t>(R * D);
+      ex.q = plan->alloc<uint16_t>(R * QW);
+      ex.k = plan->alloc<uint16_t>(R * KW);
+      ex.att = plan->alloc<uint16_t>(R * QW);
+      ex.act = plan->alloc<uint16_t>(R * F);
+      ex.scores = plan->alloc<float>(R * c.q_heads * plan->cap);
+      ex.probs = plan->alloc<float>(R * c.q_heads * plan->cap);
+      ex.ctl = plan->alloc<dl::Control>(1);
+    }
+    dl::check_hip(hipMemcpyAsync(plan->tokens, prompt, prompt_length * 4ull, hipMemcpyHostToDevice, s), "prompt");
+    const bool per_sequence = sequences_differ(plan);
+    const uint32_t runs = per_sequence ? plan->batch : 1;
+    for (uint32_t seq = 0; seq < runs; ++seq) {
+      for (uint32_t p0 = 0; p0 < rows; p0 += R) {
+        const uint32_t n = std::min<uint32_t>(static_cast<uint32_t>(R), rows - p0);
+        dl::k_chunk_control<<<1, 1, 0, s>>>(plan->ctl, ex.ctl, p0, plan->capture_layer, plan->steer_layer,
+                                            plan->steer_mask);
+        dl::PrefillEmbedArgs ea{plan->tokens, m->lm_head, m->embedding, plan->override_row, ex.h, n,
+                                static_cast<uint32_t>(D), p0, c.tied_embeddings ? 1 : 0,
+                                (plan->override_active && ((plan->override_mask >> seq) & 1u)) ? 1 : 0,
+                                plan->override_position};
+        dl::k_prefill_embed<<<n, dl::kBlock, 0, s>>>(ea);
+        const StepRows r{ex.h, ex.q, ex.k, ex.att, ex.act, ex.scores, ex.probs, n,
+                         uint64_t(seq) * plan->cache_seq_stride, 1, 0, 1, 1, static_cast<int>(seq)};
+        const bool short_context = p0 + n <= static_cast<uint32_t>(dl::kFusedKeys);
+        for (uint32_t l = 0; l < c.layers; ++l) {
+          launch_step_kernel(plan, s, 0, l, ex.ctl, r);  // Q, K, V (V into the cache)
+          launch_step_kernel(plan, s, 9, l, ex.ctl, r);  // rotated K into the cache
+          if (short_context) {
+            launch_step_kernel(plan, s, 8, l, ex.ctl, r);
+          } else {
+            for (int which : {1, 2, 3}) launch_step_kernel(plan, s, which, l, ex.ctl, r);
+          }
+          for (int which : {4, 5, 6}) launch_step_kernel(plan, s, which, l, ex.ctl, r);
+        }
+      }
+      dl::check_launch(plan->queue, "exact prefill");
+    }
+    if (!per_sequence) copy_prefix_to_other_sequences(plan, rows);
+    dl::check_hip(hipStreamSynchronize(s), "exact prefill");
     plan->prefilled = rows;
   });
 }

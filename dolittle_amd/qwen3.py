@@ -202,11 +202,14 @@ class Plan:
                   C.byref(s), seeds_a.ctypes.data_as(_lib.u64p), stops.ctypes.data_as(_lib.u32p), n)
         self.max_new = max_new
 
-    def prefill(self, prompt) -> None:
-        """MFMA prefill of positions [0, len(prompt) - 1); a following
-        generate() with the same prompt resumes at the last prompt position."""
+    def prefill(self, prompt, exact: bool = False) -> None:
+        """Prompt pass over positions [0, len(prompt) - 1); a following
+        generate() with the same prompt resumes at the last prompt position.
+        exact=False runs the MFMA GEMM path (tolerance), exact=True the
+        chunked exact path (caches bit-identical to the token loop's)."""
         p = np.ascontiguousarray(prompt, dtype=np.uint32)
-        _lib.call("dl_plan_prefill", self.handle, p.ctypes.data_as(_lib.u32p), p.size)
+        _lib.call("dl_plan_prefill_exact" if exact else "dl_plan_prefill", self.handle,
+                  p.ctypes.data_as(_lib.u32p), p.size)
 
     def decode_steps(self, steps: int) -> None:
         _lib.call("dl_plan_decode_steps", self.handle, steps)

@@ -322,6 +322,16 @@ int dl_plan_set_embedding_override(dl_plan* plan, uint64_t position, const uint1
  * (MFMA accumulation order), not bit for bit.  No reference counterpart:
  * the reference prefills with its exact row kernels (executor.cpp:285-716). */
 int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length);
+/* The exact prompt pass, replacing the reference's row-by-row forward of a
+ * prompt (executor.cpp:285-716 with the row kernels of projection.cu,
+ * attention.cu and normalization.cu): positions [0, prompt_length - 1) in
+ * chunks of up to 8 consecutive positions through the decode kernels, every
+ * row the same reduction chains as a single-position step.  The caches end
+ * bit-identical to consuming the prompt through dl_plan_generate; a
+ * following dl_plan_generate with the same prompt resumes at the last prompt
+ * position.  Capture and steering apply to the prompt positions as in the
+ * loop. */
+int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length);
 /* Diagnostic: residual-stream rows of the last prefill after its final
  * block (rows [first_row, first_row + count), BF16 [count][hidden]). */
 int dl_plan_read_prefill_hidden(dl_plan* plan, uint64_t first_row, uint64_t count, uint16_t* host);

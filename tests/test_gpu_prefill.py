@@ -26,7 +26,7 @@ def bf16_ulp(x):
 
 
 @pytest.mark.parametrize("rows,in_w,out_w", [(256, 4096, 4096), (128, 4096, 1024), (128, 12288, 4096),
-                                             (384, 4096, 6144)])
+                                             (384, 4096, 6144), (512, 12288, 4096), (512, 4096, 6144)])
 def test_prefill_projection_within_one_ulp(device, queue, oracle, rows, in_w, out_w):
     from dolittle_amd import _lib
     x = oracle.normal_bf16(rows * in_w, SEED, 1, 1.0)

@@ -1,0 +1,112 @@
+"""GPU checks of the exact chunked prompt pass (dl_plan_prefill_exact).
+
+The pass runs the prompt positions through the decode kernels up to eight
+positions at a time.  Parity is bit-exact: for every case the caches, the
+token streams and the last logits equal those of a plan that consumes the
+same prompt one position per step through the token loop (itself bit-exact
+with the CPU contract mirror, tests/test_gpu_model.py).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SEED = 9151
+
+
+def qwen_config(layers, vocab=151936):
+    from dolittle_amd.qwen3 import Qwen3Config
+    return Qwen3Config(layers=layers, vocab=vocab)
+
+
+@pytest.fixture(scope="module")
+def model2(device, queue):
+    from dolittle_amd.qwen3 import Qwen3Model
+    model = Qwen3Model(device, queue, qwen_config(layers=2))
+    model.fill_synthetic(SEED, 0.02)
+    return model
+
+
+@pytest.fixture(scope="module")
+def model1(device, queue):
+    from dolittle_amd.qwen3 import Qwen3Model
+    model = Qwen3Model(device, queue, qwen_config(layers=1, vocab=2048))
+    model.fill_synthetic(SEED + 1, 0.02)
+    return model
+
+
+def run_pair(model, prompt, max_new, batch=1, capacity=64, setup=None, sampling=None, seeds=None):
+    """(exact prefill + generate, generate only): tokens, results, plans."""
+    from dolittle_amd.qwen3 import Plan
+    out = []
+    for exact in (True, False):
+        plan = Plan(model, batch=batch, capacity=capacity)
+        if setup:
+            setup(plan)
+        if exact:
+            plan.prefill(prompt, exact=True)
+        plan.generate(prompt, max_new, sampling, seeds)
+        tokens, results = plan.collect()
+        out.append((tokens, results, plan))
+    return out
+
+
+def assert_same(model, a, b, prompt_len, batch=1):
+    (ta, ra, pa), (tb, rb, pb) = a, b
+    assert ta.tolist() == tb.tolist()
+    for x, y in zip(ra, rb):
+        assert x["generated"] == y["generated"] and x["position"] == y["position"]
+    for s in range(batch):
+        assert np.array_equal(pa.logits(s), pb.logits(s)), s
+        for layer in range(model.config.layers):
+            ka, va = pa.read_cache(layer, 0, prompt_len, s)
+            kb, vb = pb.read_cache(layer, 0, prompt_len, s)
+            assert np.array_equal(ka, kb) and np.array_equal(va, vb), (s, layer)
+
+
+@pytest.mark.parametrize("length", [1, 2, 9, 12, 17, 30])
+def test_exact_prefill_equals_token_loop(model2, length):
+    """Chunks of 8 with every remainder (1, 8 + 3, 8 + 8, ...), and prompts
+    too short to need a pass."""
+    prompt = [int(t) for t in np.random.default_rng(length).integers(0, 151936, length)]
+    a, b = run_pair(model2, prompt, 6, capacity=48)
+    assert_same(model2, a, b, length + 6)
+
+
+def test_exact_prefill_across_the_fused_attention_limit(model1):
+    """A 1100-id prompt: chunks below 1024 keys use the one-kernel attention,
+    the later ones the split long-context kernels."""
+    prompt = [int(t) for t in np.random.default_rng(77).integers(0, 2048, 1100)]
+    a, b = run_pair(model1, prompt, 4, capacity=1152)
+    assert_same(model1, a, b, 1104)
+
+
+def test_exact_prefill_batch_with_capture_and_steering(model2, device, queue):
+    """Batch 2 with block-1 capture and steering of sequence 1 (each sequence
+    gets its own pass) and batch 3 without hooks (one pass, copied)."""
+    from dolittle_amd.qwen3 import SamplingSettings
+    prompt = [int(t) for t in np.random.default_rng(5).integers(0, 151936, 19)]
+    vec = (np.random.default_rng(6).standard_normal(4096) * 0.5).astype(np.float32)
+
+    def hooks(plan):
+        plan.set_capture(1)
+        plan.set_steering(1, 1, vec)
+
+    a, b = run_pair(model2, prompt, 5, batch=2, capacity=40, setup=hooks)
+    assert_same(model2, a, b, 24, batch=2)
+    assert np.array_equal(a[2].read_capture(0, 0, 23), b[2].read_capture(0, 0, 23))
+    assert np.array_equal(a[2].read_capture(1, 0, 23), b[2].read_capture(1, 0, 23))
+    settings = SamplingSettings("categorical", 1.0, 0, 0.95)
+    a, b = run_pair(model2, prompt, 5, batch=3, capacity=40, sampling=settings, seeds=[1, 2, 3])
+    assert_same(model2, a, b, 24, batch=3)
+
+
+def test_exact_prefill_with_embedding_override(model2):
+    """A replaced embedding row inside the prompt (BASELINE config 5's
+    injection slot) is applied by the pass exactly as by the loop."""
+    prompt = [int(t) for t in np.random.default_rng(8).integers(0, 151936, 14)]
+    row = (np.random.default_rng(9).standard_normal(4096) * 40.0).astype(np.float32)
+    bits = ((row.view(np.uint32).astype(np.uint64) + 0x7FFF + ((row.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+    a, b = run_pair(model2, prompt, 4, batch=2, capacity=32,
+                    setup=lambda plan: plan.set_embedding_override(6, bits, 0b10))
+    assert_same(model2, a, b, 18, batch=2)
