@@ -80,106 +80,118 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int m, int n, f
   }
 }
 
-// C[M x N] = A[M x K] W[N x K]^T over permuted positions.  Tile 128 x 128,
-// K chunks of 64 positions double-buffered through LDS, 32x32x16 BF16 MFMA.
-template <int EPI>
-__global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
-  __shared__ __align__(16) uint16_t As[2][kTileM * kRow];
-  __shared__ __align__(16) uint16_t Bs[2][kTileN * kRow];
-  const int n0 = blockIdx.x * kTileN, m0 = blockIdx.y * kTileM;
+// C[M x N] = A[M x K] W[N x K]^T over permuted positions, 32x32x16 BF16
+// MFMA.  Four waves in a 2 x 2 grid; each wave owns a 64 x (32 WN) block of
+// 2 x WN MFMA tiles, so a 16-deep K step reads 2 + WN operand fragments
+// from LDS for 2 WN MFMAs.  WN = 2: tile 128 x 128 in K chunks of 64;
+// WN = 4: tile 128 x 256 in K chunks of 32 (two workgroups per CU still fit
+// in LDS), which halves the fragment reads per MFMA of the A side.  Chunks
+// are double-buffered through LDS and come through two register sets, so
+// each chunk's loads are issued two chunks before they are stored.
+template <int EPI, int WN>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(GemmArgs a) {
+  constexpr int TN = 64 * WN;
+  constexpr int TK = WN == 2 ? 64 : 32;
+  constexpr int RS = TK + 8;                  // LDS row stride in BF16 (staggers banks)
+  constexpr int PR = TK / 8;                  // 16-byte pieces per row per chunk
+  constexpr int NA = kTileM * PR / kGemmThreads, NB = TN * PR / kGemmThreads, NR = NA + NB;
+  __shared__ __align__(16) uint16_t As[2][kTileM * RS];
+  __shared__ __align__(16) uint16_t Bs[2][TN * RS];
+  const int n0 = blockIdx.x * TN, m0 = blockIdx.y * kTileM;
   const bool alt = n0 >= a.n_split;
   const uint16_t* A = alt ? a.a_alt : a.a;
   const uint16_t* W = alt ? a.w_alt : a.w;
   const int P = alt ? a.P_alt : a.P;
   const int nb = alt ? n0 - a.n_split : n0;
-  const int K = a.K, chunks = K / kTK;
+  const int K = a.K, chunks = K / TK;
   const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // Each thread moves four 16-byte pieces of each operand tile per chunk:
-  // piece i = tid + 256 j covers row i / 8, positions 8 (i % 8) .. + 7.
-  const u32x4* a_src[4];
-  const uint16_t* w_row[4];
-  int lds_off[4];
+  // Piece i = tid + 256 j of a tile covers row i / PR, positions 8 (i % PR)
+  // .. + 7 of the chunk.
+  const u32x4* a_src[NA];
+  const uint16_t* w_row[NB];
+  int a_off[NA], b_off[NB];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = tid + kGemmThreads * j, row = i >> 3, col = (i & 7) * 8;
+  for (int j = 0; j < NA; ++j) {
+    const int i = tid + kGemmThreads * j, row = i / PR, col = (i % PR) * 8;
     a_src[j] = reinterpret_cast<const u32x4*>(A + static_cast<uint64_t>(m0 + row) * K + col);
-    w_row[j] = W + packed_offset(nb + row, P, K, 0) + col;
-    lds_off[j] = row * kRow + col;
+    a_off[j] = row * RS + col;
   }
-  const int RW = 64 / P, block = 8 * P;
-  (void)RW;
-  // Packed position kpos of a row: block kpos / 8P sits 8P * RW ... apart.
-  const uint64_t block_stride = static_cast<uint64_t>(64) * 8;  // elements between consecutive blocks of a row
-  auto w_at = [&](int j, int kpos) {
-    return reinterpret_cast<const u32x4*>(w_row[j] + (kpos / block) * block_stride + (kpos % block));
-  };
-  u32x4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
-#define DL_GEMM_LOAD(c)                                      \
-  do {                                                       \
-    const int kp = (c) * kTK;                                \
-    ra0 = a_src[0][kp / 8]; ra1 = a_src[1][kp / 8];          \
-    ra2 = a_src[2][kp / 8]; ra3 = a_src[3][kp / 8];          \
-    rb0 = *w_at(0, kp); rb1 = *w_at(1, kp);                  \
-    rb2 = *w_at(2, kp); rb3 = *w_at(3, kp);                  \
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int i = tid + kGemmThreads * j, row = i / PR, col = (i % PR) * 8;
+    w_row[j] = W + packed_offset(nb + row, P, K, 0) + col;
+    b_off[j] = row * RS + col;
+  }
+  const int block = 8 * P;
+  // Packed position kpos of a row: consecutive 8P-blocks of a row sit
+  // 64 * 8 elements apart.
+  const uint64_t block_stride = static_cast<uint64_t>(64) * 8;
+  u32x4 r0[NR], r1[NR];
+#define DL_GEMM_LOAD(set, c)                                                                          \
+  do {                                                                                                \
+    const int kp = (c) * TK;                                                                          \
+    _Pragma("unroll") for (int j = 0; j < NA; ++j) set[j] = a_src[j][kp / 8];                         \
+    _Pragma("unroll") for (int j = 0; j < NB; ++j) set[NA + j] =                                      \
+        *reinterpret_cast<const u32x4*>(w_row[j] + (kp / block) * block_stride + (kp % block));       \
   } while (0)
-#define DL_GEMM_STORE(buf)                                                       \
-  do {                                                                           \
-    *reinterpret_cast<u32x4*>(&As[buf][lds_off[0]]) = ra0;                       \
-    *reinterpret_cast<u32x4*>(&As[buf][lds_off[1]]) = ra1;                       \
-    *reinterpret_cast<u32x4*>(&As[buf][lds_off[2]]) = ra2;                       \
-    *reinterpret_cast<u32x4*>(&As[buf][lds_off[3]]) = ra3;                       \
-    *reinterpret_cast<u32x4*>(&Bs[buf][lds_off[0]]) = rb0;                       \
-    *reinterpret_cast<u32x4*>(&Bs[buf][lds_off[1]]) = rb1;                       \
-    *reinterpret_cast<u32x4*>(&Bs[buf][lds_off[2]]) = rb2;                       \
-    *reinterpret_cast<u32x4*>(&Bs[buf][lds_off[3]]) = rb3;                       \
+#define DL_GEMM_STORE(set, buf)                                                                       \
+  do {                                                                                                \
+    _Pragma("unroll") for (int j = 0; j < NA; ++j) *reinterpret_cast<u32x4*>(&As[buf][a_off[j]]) = set[j]; \
+    _Pragma("unroll") for (int j = 0; j < NB; ++j) *reinterpret_cast<u32x4*>(&Bs[buf][b_off[j]]) = set[NA + j]; \
+  } while (0)
+#define DL_GEMM_COMPUTE(buf)                                                                          \
+  do {                                                                                                \
+    _Pragma("unroll") for (int ks = 0; ks < TK / 16; ++ks) {                                          \
+      bf16x8 af[2], bw[WN];                                                                           \
+      _Pragma("unroll") for (int i = 0; i < 2; ++i) af[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(   \
+          &As[buf][(64 * wm + 32 * i + lane % 32) * RS + ks * 16 + 8 * (lane / 32)]));                  \
+      _Pragma("unroll") for (int j = 0; j < WN; ++j) bw[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(  \
+          &Bs[buf][(32 * WN * wn + 32 * j + lane % 32) * RS + ks * 16 + 8 * (lane / 32)]));             \
+      _Pragma("unroll") for (int i = 0; i < 2; ++i)                                                   \
+      _Pragma("unroll") for (int j = 0; j < WN; ++j)                                                  \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bw[j], acc[i][j], 0, 0, 0);        \
+    }                                                                                                 \
   } while (0)
 
-  floatx16 acc[2][2];
+  floatx16 acc[2][WN];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < WN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  DL_GEMM_LOAD(0);
-  DL_GEMM_STORE(0);
+  DL_GEMM_LOAD(r0, 0);
+  if (chunks > 1) DL_GEMM_LOAD(r1, 1);
+  DL_GEMM_STORE(r0, 0);
   __syncthreads();
-  for (int c = 0; c < chunks; ++c) {
-    const int buf = c & 1;
-    if (c + 1 < chunks) DL_GEMM_LOAD(c + 1);
-#pragma unroll
-    for (int ks = 0; ks < kTK / 16; ++ks) {
-      bf16x8 af[2], bw[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(
-            &As[buf][(64 * wm + 32 * i + lane % 32) * kRow + ks * 16 + 8 * (lane / 32)]));
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bw[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(
-            &Bs[buf][(64 * wn + 32 * j + lane % 32) * kRow + ks * 16 + 8 * (lane / 32)]));
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bw[j], acc[i][j], 0, 0, 0);
-    }
-    if (c + 1 < chunks) DL_GEMM_STORE(buf ^ 1);
+  // Chunk c sits in LDS buffer c & 1 and came through register set c & 1.
+  // Loads past the last chunk reload the last one (never stored).
+  int c = 0;
+  for (; c + 1 < chunks; c += 2) {
+    DL_GEMM_LOAD(r0, min(c + 2, chunks - 1));
+    DL_GEMM_COMPUTE(0);
+    DL_GEMM_STORE(r1, 1);
+    __syncthreads();
+    DL_GEMM_LOAD(r1, min(c + 3, chunks - 1));
+    DL_GEMM_COMPUTE(1);
+    if (c + 2 < chunks) DL_GEMM_STORE(r0, 0);
     __syncthreads();
   }
+  if (c < chunks) DL_GEMM_COMPUTE(0);
 #undef DL_GEMM_LOAD
 #undef DL_GEMM_STORE
+#undef DL_GEMM_COMPUTE
 
   // Lane layout of a 32x32 accumulator: column lane % 32, row
   // 8 (r / 4) + 4 (lane / 32) + r % 4 for r < 16.
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + 64 * wn + 32 * j + lane % 32;
+    for (int j = 0; j < WN; ++j) {
+      const int n = n0 + 32 * WN * wn + 32 * j + lane % 32;
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         gemm_epilogue<EPI>(a, m0 + 64 * wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + r % 4, n, acc[i][j][r], lane);
@@ -453,12 +465,23 @@ void launch_permute(hipStream_t stream, const uint16_t* x, uint16_t* out, uint64
 }
 
 void launch_gemm(hipStream_t stream, const GemmArgs& a) {
+  // The 256-wide tile needs whole tiles on both sides of the Q | K/V split.
+  if (a.N % 256 == 0 && a.n_split % 256 == 0) {
+    const dim3 grid(a.N / 256, a.M / kTileM);
+    switch (a.epilogue) {
+      case kStore: hipLaunchKernelGGL((k_gemm<kStore, 4>), grid, dim3(kGemmThreads), 0, stream, a); break;
+      case kStoreQkv: hipLaunchKernelGGL((k_gemm<kStoreQkv, 4>), grid, dim3(kGemmThreads), 0, stream, a); break;
+      case kResidual: hipLaunchKernelGGL((k_gemm<kResidual, 4>), grid, dim3(kGemmThreads), 0, stream, a); break;
+      default: hipLaunchKernelGGL((k_gemm<kGateUp, 4>), grid, dim3(kGemmThreads), 0, stream, a); break;
+    }
+    return;
+  }
   const dim3 grid(a.N / kTileN, a.M / kTileM);
   switch (a.epilogue) {
-    case kStore: hipLaunchKernelGGL(k_gemm<kStore>, grid, dim3(kGemmThreads), 0, stream, a); break;
-    case kStoreQkv: hipLaunchKernelGGL(k_gemm<kStoreQkv>, grid, dim3(kGemmThreads), 0, stream, a); break;
-    case kResidual: hipLaunchKernelGGL(k_gemm<kResidual>, grid, dim3(kGemmThreads), 0, stream, a); break;
-    default: hipLaunchKernelGGL(k_gemm<kGateUp>, grid, dim3(kGemmThreads), 0, stream, a); break;
+    case kStore: hipLaunchKernelGGL((k_gemm<kStore, 2>), grid, dim3(kGemmThreads), 0, stream, a); break;
+    case kStoreQkv: hipLaunchKernelGGL((k_gemm<kStoreQkv, 2>), grid, dim3(kGemmThreads), 0, stream, a); break;
+    case kResidual: hipLaunchKernelGGL((k_gemm<kResidual, 2>), grid, dim3(kGemmThreads), 0, stream, a); break;
+    default: hipLaunchKernelGGL((k_gemm<kGateUp, 2>), grid, dim3(kGemmThreads), 0, stream, a); break;
   }
 }
 
