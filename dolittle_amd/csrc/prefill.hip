@@ -7,6 +7,7 @@
 // probability is rounded to BF16 (numerical-portability.md:8-10).
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "dl_device.h"
 #include "dl_internal.h"
@@ -27,9 +28,11 @@ constexpr int kGemmThreads = 256;    // 4 waves, each a 64 x 64 quarter of the t
 constexpr int kHd = 128;
 constexpr int kKeyTile = 64;
 constexpr int kQRow = kHd + 8;       // Q/K tile row stride in BF16 (272 B)
-constexpr int kVRow = kKeyTile + 8;  // V^T tile row stride in BF16
-constexpr int kPRow = kKeyTile + 4;  // probability tile row stride in floats
-constexpr int kAttnThreads = 256;    // 4 waves x 16 query rows
+// V^T tile row stride in BF16: 34 dwords, so the 16 rows one 8-byte read
+// instruction touches fall on distinct banks.
+constexpr int kVRow = kKeyTile + 4;
+constexpr int kXcds = 8;             // XCDs per MI355X; workgroups are dealt round-robin
+constexpr int kAttnThreads = 256;    // 4 waves x 16 queries
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
@@ -273,46 +276,61 @@ __global__ __launch_bounds__(64) void k_heads(HeadArgs a) {
 }
 
 // ------------------------------------------------------------- attention
-// Grid (query tiles of 64 rows, query heads); 4 waves of 16 rows each.
-// S = Q K^T with 16x16x32 MFMA, online softmax in FP32, O += P V with P
-// split exactly into three BF16 parts.
-__global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
-  __shared__ __align__(16) uint16_t Qs[kAttnRows * kQRow];
-  __shared__ __align__(16) uint16_t Ks[kKeyTile * kQRow];
-  __shared__ __align__(16) uint16_t Vs[kHd * kVRow];
-  __shared__ __align__(16) float Ps[4][16 * kPRow];
-  const int q0 = blockIdx.x * kAttnRows;
-  const int h = blockIdx.y, g = h / (a.q_heads / a.kv_heads);
+// One workgroup per (query tile of 64 rows, query head); 4 waves of 16
+// queries each.  Workgroups are dealt to the XCDs round-robin, so the flat
+// index is renumbered to give each XCD a contiguous run of query heads (one
+// GQA group per XCD when there are 8 KV heads, whose keys and values then stay
+// in that XCD's L2), each head's tiles heaviest (longest causal span) first.
+// Scores are computed transposed, S^T = K Q^T (16x16x32 MFMA), so each lane
+// owns one query: lane l holds keys 4 (l / 16) + t of every 16-key block for
+// query l % 16, the online softmax (FP32) reduces in-lane and across the
+// four lane groups, and O^T += V^T P^T takes P straight from registers.  In
+// the PV product the 32 keys of a K step are taken in the order the lane
+// holds them (keys 4g..4g+3 of two 16-key blocks for lane group g) on both
+// operands, and P is split exactly into three BF16 parts.
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_attention(AttnArgs a) {
+  __shared__ __align__(16) uint16_t Ks[2][kKeyTile * kQRow];
+  __shared__ __align__(16) uint16_t Vs[2][kHd * kVRow];
+  const int tiles = (a.rows + kAttnRows - 1) / kAttnRows;
+  const int total = tiles * a.q_heads;
+  int item = blockIdx.x;
+  if (total % kXcds == 0) item = (item % kXcds) * (total / kXcds) + item / kXcds;
+  const int h = item / tiles, g = h / (a.q_heads / a.kv_heads);
+  const int q0 = (tiles - 1 - item % tiles) * kAttnRows;
   const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  const int lg = lane / 16, lq = lane % 16;
   const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHd;
-  const u32x4 zero = {0u, 0u, 0u, 0u};
 
+  // The lane's B operand of S^T = K Q^T: query row 16 wave + lq, features
+  // 32 ks + 8 lg .. +7.
+  bf16x8 qb[kHd / 32];
+  {
+    const int row = q0 + 16 * wave + lq;
+    const uint16_t* src = a.q_rot + static_cast<uint64_t>(min(row, a.rows - 1)) * qw + h * kHd + 8 * lg;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = tid + kAttnThreads * j, row = i / 16, col = (i % 16) * 8;
-    *reinterpret_cast<u32x4*>(&Qs[row * kQRow + col]) =
-        q0 + row < a.rows
-            ? *reinterpret_cast<const u32x4*>(a.q_rot + static_cast<uint64_t>(q0 + row) * qw + h * kHd + col)
-            : zero;
+    for (int ks = 0; ks < kHd / 32; ++ks) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(src + 32 * ks);
+      qb[ks] = as_bf16x8(row < a.rows ? v : u32x4{0u, 0u, 0u, 0u});
+    }
   }
   const uint16_t* kc = a.k_cache + static_cast<uint64_t>(g) * a.cap * kHd;
   const uint16_t* vc = a.v_cache + static_cast<uint64_t>(g) * kHd * a.cap;
 
-  float m_run[4], l_run[4];
+  // This lane's query and its softmax state; o[d] holds O^T rows
+  // 16 d + 4 lg + t (features) for the lane's query.
+  const int qrow = 16 * wave + lq;
+  const int qpos = a.first_position + q0 + qrow;
+  const int wave_first = a.first_position + q0 + 16 * wave;
+  float m_run = -INFINITY, l_run = 0.0f;
   floatx4 o[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    m_run[j] = -INFINITY;
-    l_run[j] = 0.0f;
-  }
 #pragma unroll
   for (int d = 0; d < 8; ++d) o[d] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int last_row = min(q0 + kAttnRows, a.rows) - 1;
   const int key_end = a.first_position + last_row + 1;
-  // K and V tiles go through registers: the next tile's loads are issued
-  // before this tile's products, and stored to LDS once every wave is done
-  // with the previous tile.
+  // K and V tiles go through registers into two LDS buffers: the next tile's
+  // loads are issued before this tile's products and stored to the other
+  // buffer after them, so one barrier per tile covers both hazards.
   u32x4 kr[4], vr[4];
   auto load_tile = [&](int kt0) {
 #pragma unroll
@@ -325,18 +343,16 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
       vr[j] = *reinterpret_cast<const u32x4*>(vc + static_cast<uint64_t>(d) * a.cap + min(kt0 + vcol, a.cap - 8));
     }
   };
-  load_tile(0);
-  for (int kt0 = 0; kt0 < key_end; kt0 += kKeyTile) {
-    __syncthreads();
+  auto store_tile = [&](int kt0, int buf) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int i = tid + kAttnThreads * j;
       const int key = i / 16, col = (i % 16) * 8;
-      *reinterpret_cast<u32x4*>(&Ks[key * kQRow + col]) = kr[j];
+      *reinterpret_cast<u32x4*>(&Ks[buf][key * kQRow + col]) = kr[j];
       const int d = i / 8, vcol = (i % 8) * 8;
       u32x4 vv = vr[j];
-      // Keys at or past key_end are masked for every row of this tile (p = 0);
-      // zero them so stale cache contents cannot turn 0 * v into NaN.
+      // Keys at or past key_end are masked for every query of this tile
+      // (p = 0); zero them so stale cache contents cannot turn 0 * v into NaN.
       const int left = key_end - (kt0 + vcol);
       if (left < 8) {
         uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
@@ -345,102 +361,132 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
           if (e >= left) w[e / 2] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
         vv = u32x4{w[0], w[1], w[2], w[3]};
       }
-      *reinterpret_cast<u32x4*>(&Vs[d * kVRow + vcol]) = vv;
+      uint2* vdst = reinterpret_cast<uint2*>(&Vs[buf][d * kVRow + vcol]);  // rows are 8-byte aligned
+      vdst[0] = uint2{vv.x, vv.y};
+      vdst[1] = uint2{vv.z, vv.w};
     }
-    __syncthreads();
-    if (kt0 + kKeyTile < key_end) load_tile(kt0 + kKeyTile);
+  };
+  load_tile(0);
+  store_tile(0, 0);
+  __syncthreads();
+  int buf = 0;
+  for (int kt0 = 0; kt0 < key_end; kt0 += kKeyTile, buf ^= 1) {
+    const bool more = kt0 + kKeyTile < key_end;
+    if (more) load_tile(kt0 + kKeyTile);
+    const uint16_t* Kt = Ks[buf];
+    const uint16_t* Vt = Vs[buf];
 
+    // S^T for four 16-key blocks: s[sub][t] = score of key kt0 + 16 sub +
+    // 4 lg + t for the lane's query.
     floatx4 s[4];
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) s[sub] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int ks = 0; ks < kHd / 32; ++ks) {
-      const bf16x8 qa = as_bf16x8(
-          *reinterpret_cast<const u32x4*>(&Qs[(16 * wave + lane % 16) * kQRow + 32 * ks + 8 * (lane / 16)]));
+    for (int ks = 0; ks < kHd / 32; ++ks)
 #pragma unroll
       for (int sub = 0; sub < 4; ++sub) {
-        const bf16x8 kb = as_bf16x8(
-            *reinterpret_cast<const u32x4*>(&Ks[(16 * sub + lane % 16) * kQRow + 32 * ks + 8 * (lane / 16)]));
-        s[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, kb, s[sub], 0, 0, 0);
+        const bf16x8 ka = as_bf16x8(
+            *reinterpret_cast<const u32x4*>(&Kt[(16 * sub + lq) * kQRow + 32 * ks + 8 * lg]));
+        s[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[ks], s[sub], 0, 0, 0);
       }
-    }
 
-    // Lane holds key kt0 + 16 sub + lane % 16 of rows 4 (lane / 16) + j.
+    // Online softmax of the lane's query over the tile's 64 keys.  Only a
+    // tile that reaches past the wave's first query needs the causal mask:
+    // key kt0 + 16 sub + 4 lg + t is masked when 16 sub + t > lim.
+    auto scale_scores = [&](auto masked_tag) {
+      constexpr bool kMasked = decltype(masked_tag)::value;
+      const int lim = qpos - kt0 - 4 * lg;
+      float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int qpos = a.first_position + q0 + 16 * wave + 4 * (lane / 16) + j;
-      float tile_max = -INFINITY;
+      for (int sub = 0; sub < 4; ++sub)
 #pragma unroll
-      for (int sub = 0; sub < 4; ++sub) {
-        const int key = kt0 + 16 * sub + lane % 16;
-        const float v = key <= qpos ? s[sub][j] * a.scale : -INFINITY;
-        s[sub][j] = v;
-        tile_max = fmaxf(tile_max, v);
-      }
+        for (int t = 0; t < 4; ++t) {
+          float v = s[sub][t] * a.scale;
+          if constexpr (kMasked) v = 16 * sub + t > lim ? -INFINITY : v;
+          s[sub][t] = v;
+          mx = fmaxf(mx, v);
+        }
+      return mx;
+    };
+    float tile_max = kt0 + kKeyTile - 1 > wave_first ? scale_scores(std::true_type{})
+                                                     : scale_scores(std::false_type{});
+    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
+    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+    // Key 0 is unmasked for every query, so m_new is finite from the first
+    // tile on: masked scores give exp(-inf) = 0, and the first alpha is 0.
+    const float m_new = fmaxf(m_run, tile_max);
+    const float alpha = __expf(m_run - m_new);
+    float row_sum = 0.0f;
 #pragma unroll
-      for (int off = 1; off < 16; off <<= 1) tile_max = fmaxf(tile_max, __shfl_xor(tile_max, off));
-      const float m_new = fmaxf(m_run[j], tile_max);
-      const float alpha = m_new == -INFINITY ? 1.0f : __expf(m_run[j] - m_new);
-      float row_sum = 0.0f;
+    for (int sub = 0; sub < 4; ++sub)
 #pragma unroll
-      for (int sub = 0; sub < 4; ++sub) {
-        const float p = s[sub][j] == -INFINITY ? 0.0f : __expf(s[sub][j] - m_new);
-        s[sub][j] = p;
+      for (int t = 0; t < 4; ++t) {
+        const float p = __expf(s[sub][t] - m_new);
+        s[sub][t] = p;
         row_sum += p;
       }
+    row_sum += __shfl_xor(row_sum, 16);
+    row_sum += __shfl_xor(row_sum, 32);
+    l_run = l_run * alpha + row_sum;
+    m_run = m_new;
+    // The running maximum rarely moves once a few tiles are in; multiplying
+    // by exactly 1 changes nothing, so the wave skips it then.
+    if (__ballot(alpha != 1.0f) != 0) {
 #pragma unroll
-      for (int off = 1; off < 16; off <<= 1) row_sum += __shfl_xor(row_sum, off);
-      l_run[j] = l_run[j] * alpha + row_sum;
-      m_run[j] = m_new;
-#pragma unroll
-      for (int d = 0; d < 8; ++d) o[d][j] *= alpha;
-#pragma unroll
-      for (int sub = 0; sub < 4; ++sub) Ps[wave][(4 * (lane / 16) + j) * kPRow + 16 * sub + lane % 16] = s[sub][j];
+      for (int d = 0; d < 8; ++d) o[d] *= alpha;
     }
-    __syncthreads();
 
+    // O^T += V^T P^T, one 32-key K step per pair of 16-key blocks.
 #pragma unroll
     for (int ks = 0; ks < kKeyTile / 32; ++ks) {
-      const float* prow = &Ps[wave][(lane % 16) * kPRow + 32 * ks + 8 * (lane / 16)];
-      const float4 pa = *reinterpret_cast<const float4*>(prow);
-      const float4 pb = *reinterpret_cast<const float4*>(prow + 4);
-      const float p[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-      uint16_t hi[8], mid[8], lo[8];
+      const float p[8] = {s[2 * ks][0], s[2 * ks][1], s[2 * ks][2], s[2 * ks][3],
+                          s[2 * ks + 1][0], s[2 * ks + 1][1], s[2 * ks + 1][2], s[2 * ks + 1][3]};
+      // p = hi + mid + lo exactly: hi is p cut to its top 8 significant
+      // bits, mid the residual cut the same way, and lo the rest, which has
+      // at most 8 significant bits left; both subtractions are exact.  The
+      // parts are the upper halves of the FP32 words, packed by byte permute.
+      uint32_t hi[4], mid[4], lo[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        hi[e] = dl_f32_to_bf16(p[e]);
-        const float r1 = p[e] - dl_bf16_to_f32(hi[e]);
-        mid[e] = dl_f32_to_bf16(r1);
-        lo[e] = dl_f32_to_bf16(r1 - dl_bf16_to_f32(mid[e]));
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t b0 = __float_as_uint(p[2 * e]), b1 = __float_as_uint(p[2 * e + 1]);
+        hi[e] = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
+        const float r0 = p[2 * e] - __uint_as_float(b0 & 0xffff0000u);
+        const float r1 = p[2 * e + 1] - __uint_as_float(b1 & 0xffff0000u);
+        const uint32_t c0 = __float_as_uint(r0), c1 = __float_as_uint(r1);
+        mid[e] = __builtin_amdgcn_perm(c1, c0, 0x07060302u);
+        const float l0 = r0 - __uint_as_float(c0 & 0xffff0000u);
+        const float l1 = r1 - __uint_as_float(c1 & 0xffff0000u);
+        lo[e] = __builtin_amdgcn_perm(__float_as_uint(l1), __float_as_uint(l0), 0x07060302u);
       }
-      auto pack = [](const uint16_t (&x)[8]) {
-        const u32x4 u = {uint32_t(x[0]) | (uint32_t(x[1]) << 16), uint32_t(x[2]) | (uint32_t(x[3]) << 16),
-                         uint32_t(x[4]) | (uint32_t(x[5]) << 16), uint32_t(x[6]) | (uint32_t(x[7]) << 16)};
-        return as_bf16x8(u);
-      };
-      const bf16x8 ph = pack(hi), pm = pack(mid), pl = pack(lo);
+      const bf16x8 ph = as_bf16x8(u32x4{hi[0], hi[1], hi[2], hi[3]});
+      const bf16x8 pm = as_bf16x8(u32x4{mid[0], mid[1], mid[2], mid[3]});
+      const bf16x8 pl = as_bf16x8(u32x4{lo[0], lo[1], lo[2], lo[3]});
+      const int k0 = 32 * ks + 4 * lg;  // keys k0..k0+3 and k0+16..k0+19 of the tile
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
-        const bf16x8 vb = as_bf16x8(
-            *reinterpret_cast<const u32x4*>(&Vs[(16 * d + lane % 16) * kVRow + 32 * ks + 8 * (lane / 16)]));
-        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, vb, o[d], 0, 0, 0);
-        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pm, vb, o[d], 0, 0, 0);
-        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, vb, o[d], 0, 0, 0);
+        const uint16_t* vrow = &Vt[(16 * d + lq) * kVRow];
+        const uint2 va = *reinterpret_cast<const uint2*>(vrow + k0);
+        const uint2 vb = *reinterpret_cast<const uint2*>(vrow + k0 + 16);
+        const bf16x8 vt = as_bf16x8(u32x4{va.x, va.y, vb.x, vb.y});
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, ph, o[d], 0, 0, 0);
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pm, o[d], 0, 0, 0);
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pl, o[d], 0, 0, 0);
       }
     }
+    if (more) store_tile(kt0 + kKeyTile, buf ^ 1);
+    __syncthreads();
   }
 
+  const int row = q0 + qrow;
+  if (row < a.rows) {
+    uint16_t* dst = a.out + static_cast<uint64_t>(row) * qw;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = q0 + 16 * wave + 4 * (lane / 16) + j;
-    if (row < a.rows) {
-      uint16_t* dst = a.out + static_cast<uint64_t>(row) * qw;
+    for (int d = 0; d < 8; ++d)
 #pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        const uint32_t feature = h * kHd + 16 * d + lane % 16;
-        dst[permuted(feature, 16)] = dl_f32_to_bf16(o[d][j] / l_run[j]);
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t feature = h * kHd + 16 * d + 4 * lg + t;
+        dst[permuted(feature, 16)] = dl_f32_to_bf16(o[d][t] / l_run);
       }
-    }
   }
 }
 
@@ -494,7 +540,7 @@ void launch_heads(hipStream_t stream, const HeadArgs& a) {
 }
 
 void launch_attention(hipStream_t stream, const AttnArgs& a) {
-  hipLaunchKernelGGL(k_attention, dim3((a.rows + kAttnRows - 1) / kAttnRows, a.q_heads), dim3(kAttnThreads), 0,
+  hipLaunchKernelGGL(k_attention, dim3((a.rows + kAttnRows - 1) / kAttnRows * a.q_heads), dim3(kAttnThreads), 0,
                      stream, a);
 }
 
