@@ -75,7 +75,10 @@ struct HeadArgs {
   float eps;
 };
 
-// Causal attention of prefill rows over the cached keys [0, position].
+// Causal attention of prefill rows over the cached keys [0, position].  The
+// kernel addresses a head's K and V^T rows with 32-bit element offsets
+// (capacity x 128 < 2^31).
+constexpr uint64_t kMaxAttnCapacity = uint64_t(1) << 24;
 struct AttnArgs {
   const uint16_t* q_rot;    // [rows][q_heads*128]
   const uint16_t* k_cache;  // this layer: [kv_heads][cap][128]

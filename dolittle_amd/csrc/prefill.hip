@@ -27,14 +27,18 @@ constexpr int kRow = kTK + 8;        // LDS row stride in BF16 (144 B staggers b
 constexpr int kGemmThreads = 256;    // 4 waves, each a 64 x 64 quarter of the tile
 constexpr int kHd = 128;
 constexpr int kKeyTile = 64;
-constexpr int kQRow = kHd + 8;       // Q/K tile row stride in BF16 (272 B)
-// V^T tile row stride in BF16: 34 dwords, so the 16 rows one 8-byte read
-// instruction touches fall on distinct banks.
+// K tile rows are 256 bytes, unpadded, with 16-byte piece p of key row r at
+// p ^ key_swizzle(r % 16); V^T tile rows are 136 bytes (8-byte aligned,
+// written as 8-byte halves).  Both keep the fragment reads of the attention
+// kernel off shared banks (measured with the LDS bank-conflict counter on
+// gfx950).
+constexpr int kQRow = kHd;
 constexpr int kVRow = kKeyTile + 4;
 constexpr int kXcds = 8;             // XCDs per MI355X; workgroups are dealt round-robin
 constexpr int kAttnThreads = 256;    // 4 waves x 16 queries
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ int key_swizzle(int r) { return ((r & 3) << 1) | (r & 8); }
 
 // Element offset of packed position `kpos` of weight row n (P partials,
 // K inputs): the row's 8P positions of block kpos / 8P are contiguous.
@@ -44,19 +48,22 @@ __device__ __forceinline__ uint64_t packed_offset(int n, int P, int K, int kpos)
   return (static_cast<uint64_t>((n / RW) * S + s) * 64 + (n % RW) * P) * 8 + local;
 }
 
-// SiluMultiply on BF16-rounded operands (elementwise.cu:62-87).
-__device__ __forceinline__ float silu_times(float a, float b) {
-  const float e = dl_expf(a >= 0.0f ? -a : a);
-  const float sigmoid = a >= 0.0f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+// SiluMultiply on BF16-rounded operands (elementwise.cu:62-87), two-sided
+// as there, with the hardware exponential and reciprocal (a few ulp in FP32)
+// instead of the decode path's correctly rounded FP64-evaluated exponential:
+// the MFMA prefill is compared with a tolerance.
+__device__ __forceinline__ float silu_times_fast(float a, float b) {
+  const float e = __expf(-fabsf(a));
+  const float r = __builtin_amdgcn_rcpf(1.0f + e);
+  const float sigmoid = a >= 0.0f ? r : e * r;
   return dl_round_bf16(a * sigmoid) * b;
 }
 
 // ------------------------------------------------------------------ GEMM
-// Output element (m, n) of a GEMM tile through the epilogue EPI.  Every lane
-// of the wavefront calls it for the same r (the gate/up epilogue reads the
-// up value of its column from two lanes up).
+// Output element (m, n) of a GEMM tile through the store, residual or QKV
+// epilogue.
 template <int EPI>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int m, int n, float v, int lane) {
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int m, int n, float v) {
   if constexpr (EPI == kStore) {
     a.out[static_cast<uint64_t>(m) * a.N + n] = dl_f32_to_bf16(v);
   } else if constexpr (EPI == kResidual) {
@@ -71,14 +78,43 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int m, int n, f
       a.v_cache[static_cast<uint64_t>(n - a.q_width - a.kv_width) * a.cap + a.first_position + m] =
           dl_f32_to_bf16(v);
     }
-  } else {
-    // Columns 4j..4j+3 hold gate rows 2j, 2j+1 and up rows 2j, 2j+1;
-    // the up value of column n sits two lanes up.
-    const float up = __shfl(v, (lane + 2) & 63);
-    if ((n & 3) < 2) {
-      const uint32_t f = 2 * (n / 4) + (n & 3);
-      a.out[static_cast<uint64_t>(m) * (a.N / 2) + permuted(f, 32)] =
-          dl_f32_to_bf16(silu_times(dl_round_bf16(v), dl_round_bf16(up)));
+  }
+}
+
+// Epilogue of one wave's 64 x (32 WN) block of 32x32 accumulators, rows
+// from mb, columns from nb.  Lane layout of a 32x32 accumulator: column
+// lane % 32, row 8 (r / 4) + 4 (lane / 32) + r % 4 for r < 16.  For the
+// gate/up epilogue the four lanes of a quad hold gate 2j, gate 2j+1, up 2j,
+// up 2j+1 of the same rows; the gate lanes finish rows r < 8 and the up lanes
+// rows r >= 8, each taking the other operand from the lane two over.
+template <int EPI, int WN>
+__device__ __forceinline__ void gemm_tile_epilogue(const GemmArgs& a, const floatx16 (&acc)[2][WN], int mb, int nb,
+                                                   int lane) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int n = nb + 32 * j + lane % 32;
+      const int rows = mb + 32 * i + 4 * (lane / 32);
+      if constexpr (EPI == kGateUp) {
+        const bool gate_lane = (lane & 3) < 2;
+        const uint32_t f = 2 * (n / 4) + (lane & 1);
+        uint16_t* out = a.out + permuted(f, 32);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float send = gate_lane ? acc[i][j][8 + k] : acc[i][j][k];
+          const float recv = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0x4e, 0xf, 0xf, false));
+          const float gate = gate_lane ? acc[i][j][k] : recv;
+          const float up = gate_lane ? recv : acc[i][j][8 + k];
+          const int r = gate_lane ? k : 8 + k;
+          const int m = rows + 8 * (r / 4) + r % 4;
+          out[static_cast<uint64_t>(m) * (a.N / 2)] =
+              dl_f32_to_bf16(silu_times_fast(dl_round_bf16(gate), dl_round_bf16(up)));
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) gemm_epilogue<EPI>(a, rows + 8 * (r / 4) + r % 4, n, acc[i][j][r]);
+      }
     }
   }
 }
@@ -188,18 +224,149 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #undef DL_GEMM_STORE
 #undef DL_GEMM_COMPUTE
 
-  // Lane layout of a 32x32 accumulator: column lane % 32, row
-  // 8 (r / 4) + 4 (lane / 32) + r % 4 for r < 16.
+  gemm_tile_epilogue<EPI, WN>(a, acc, m0 + 64 * wm, n0 + 32 * WN * wn, lane);
+}
+
+// The 128 x 256 tile fed by direct global-to-LDS loads: each wave
+// instruction moves 64 lanes x 16 bytes into 1 KB of LDS, so chunks (32
+// positions) go through three LDS stages with no register staging and one
+// barrier per chunk; chunk c + 2 is in flight while chunk c is multiplied.
+// LDS rows are 64 bytes, unpadded; the four 16-byte pieces of row r sit at
+// piece p ^ ((r / 4) & 3), which puts the 16-byte fragment reads of a 32-row
+// block on distinct banks (measured with the LDS bank-conflict counter on
+// gfx950).  Each stage is its own LDS object, so the explicit vmcnt waits
+// below are the only ones the loads need.
+constexpr int kDmaTK = 32;
+constexpr int kDmaTN = 256;
+constexpr int kDmaLoads = (kTileM + kDmaTN) * kDmaTK / 8 / kGemmThreads;  // 16-byte loads per thread per chunk
+
+__device__ __forceinline__ int dma_swizzle(int r) { return (r >> 2) & 3; }
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void global_void;
+
+template <int EPI>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_dma(GemmArgs a) {
+  __shared__ __align__(1024) uint16_t A0[kTileM * kDmaTK], A1[kTileM * kDmaTK], A2[kTileM * kDmaTK];
+  __shared__ __align__(1024) uint16_t B0[kDmaTN * kDmaTK], B1[kDmaTN * kDmaTK], B2[kDmaTN * kDmaTK];
+  const int n0 = blockIdx.x * kDmaTN, m0 = blockIdx.y * kTileM;
+  const bool alt = n0 >= a.n_split;
+  const uint16_t* A = alt ? a.a_alt : a.a;
+  const uint16_t* W = alt ? a.w_alt : a.w;
+  const int P = alt ? a.P_alt : a.P;
+  const int nb = alt ? n0 - a.n_split : n0;
+  const int K = a.K, chunks = K / kDmaTK;
+  const int tid = threadIdx.x, lane = tid % 64;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // Load j of this wave fills rows 16 (4 j + wave) .. + 15 of its stage
+  // (j < 2: A, else B); lane L of it brings row + L / 4, physical piece L % 4.
+  const int lr = lane / 4, lp = lane % 4;
+  const uint16_t* src[2 + 4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int n = n0 + 32 * WN * wn + 32 * j + lane % 32;
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        gemm_epilogue<EPI>(a, m0 + 64 * wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + r % 4, n, acc[i][j][r], lane);
-    }
+  for (int j = 0; j < 2; ++j) {
+    const int r = 16 * (4 * j + wave) + lr;
+    src[j] = A + static_cast<uint64_t>(m0 + r) * K + 8 * (lp ^ dma_swizzle(r));
   }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 16 * (4 * j + wave) + lr;
+    src[2 + j] = W + packed_offset(nb + r, P, K, 0) + 8 * (lp ^ dma_swizzle(r));
+  }
+  // Packed position kp of a row: 8P-blocks sit 64 x 8 elements apart.
+  const int block_shift = __builtin_ctz(8 * P), block_mask = 8 * P - 1;
+  auto issue = [&](int c, uint16_t* As, uint16_t* Bs) {
+    const int kp = c * kDmaTK;
+    const uint64_t woff = (static_cast<uint64_t>(kp >> block_shift) << 9) + (kp & block_mask);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds((const global_void*)(src[j] + kp), (lds_void*)(As + 16 * (4 * j + wave) * kDmaTK),
+                                       16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds((const global_void*)(src[2 + j] + woff),
+                                       (lds_void*)(Bs + 16 * (4 * j + wave) * kDmaTK), 16, 0, 0);
+  };
+
+  // Fragment offsets: row base + lane % 32 (bases are multiples of 32, so
+  // the swizzle depends on lane % 32 only), logical piece 2 ks + lane / 32.
+  const int sw = dma_swizzle(lane % 32);
+  int frag[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) frag[ks] = (lane % 32) * kDmaTK + 8 * ((2 * ks + lane / 32) ^ sw);
+
+  floatx16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // Both 16-deep K steps' fragments are read before the first product.
+  auto compute = [&](const uint16_t* As, const uint16_t* Bs) {
+    bf16x8 af[2][2], bw[2][4];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[ks][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&As[(64 * wm + 32 * i) * kDmaTK + frag[ks]]));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        bw[ks][j] = as_bf16x8(*reinterpret_cast<const u32x4*>(&Bs[(128 * wn + 32 * j) * kDmaTK + frag[ks]]));
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][i], bw[ks][j], acc[i][j], 0, 0, 0);
+  };
+  // Schedule of one step: the 12 fragment reads, then the 16 products in
+  // fours with the next chunk's loads (two at a time) between them.
+  auto schedule = [] {
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // LDS reads
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // global-to-LDS loads
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  };
+
+  // Step c: wait for this thread's loads of chunk c (those of chunk c + 1
+  // may stay in flight), barrier (every wave's chunk c is in LDS and every
+  // wave is done with chunk c - 1, whose stage chunk c + 2 reuses), issue
+  // chunk c + 2, multiply chunk c.  Past the last chunk the loads repeat it
+  // into the free stage, so every step issues the same number of loads and
+  // waits with the same count.
+  issue(0, A0, B0);
+  issue(min(1, chunks - 1), A1, B1);
+  int c = 0;
+#define DL_DMA_STEP(Ac, Bc, An, Bn)                                      \
+  do {                                                                   \
+    __builtin_amdgcn_s_waitcnt(0x0f70 | kDmaLoads); /* vmcnt(kDmaLoads) */ \
+    __builtin_amdgcn_s_barrier();                                        \
+    __builtin_amdgcn_sched_barrier(0);                                   \
+    issue(min(c + 2, chunks - 1), An, Bn);                               \
+    compute(Ac, Bc);                                                     \
+    schedule();                                                          \
+    __builtin_amdgcn_sched_barrier(0);                                   \
+    ++c;                                                                 \
+  } while (0)
+  for (; c + 3 <= chunks;) {
+    DL_DMA_STEP(A0, B0, A2, B2);
+    DL_DMA_STEP(A1, B1, A0, B0);
+    DL_DMA_STEP(A2, B2, A1, B1);
+  }
+  if (c < chunks) DL_DMA_STEP(A0, B0, A2, B2);
+  if (c < chunks) DL_DMA_STEP(A1, B1, A0, B0);
+#undef DL_DMA_STEP
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no load outlives the wave
+#undef DL_DMA_STEP
+  gemm_tile_epilogue<EPI, 4>(a, acc, m0 + 64 * wm, n0 + 128 * wn, lane);
 }
 
 // ------------------------------------------------------------- row norms
@@ -288,9 +455,9 @@ __global__ __launch_bounds__(64) void k_heads(HeadArgs a) {
 // the PV product the 32 keys of a K step are taken in the order the lane
 // holds them (keys 4g..4g+3 of two 16-key blocks for lane group g) on both
 // operands, and P is split exactly into three BF16 parts.
-__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_attention(AttnArgs a) {
-  __shared__ __align__(16) uint16_t Ks[2][kKeyTile * kQRow];
-  __shared__ __align__(16) uint16_t Vs[2][kHd * kVRow];
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_attention(AttnArgs a) {
+  __shared__ __align__(16) uint16_t Ks[kKeyTile * kQRow];
+  __shared__ __align__(16) uint16_t Vs[kHd * kVRow];
   const int tiles = (a.rows + kAttnRows - 1) / kAttnRows;
   const int total = tiles * a.q_heads;
   int item = blockIdx.x;
@@ -300,6 +467,9 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2)
   const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
   const int lg = lane / 16, lq = lane % 16;
   const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHd;
+  // Physical piece of the lane's K fragment in step ks: (4 ks + lg) ^
+  // key_swizzle(lq), with 4 ks and lg on disjoint bits.
+  const int kpiece = lg ^ key_swizzle(lq);
 
   // The lane's B operand of S^T = K Q^T: query row 16 wave + lq, features
   // 32 ks + 8 lg .. +7.
@@ -328,9 +498,9 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2)
 
   const int last_row = min(q0 + kAttnRows, a.rows) - 1;
   const int key_end = a.first_position + last_row + 1;
-  // K and V tiles go through registers into two LDS buffers: the next tile's
-  // loads are issued before this tile's products and stored to the other
-  // buffer after them, so one barrier per tile covers both hazards.
+  // K and V tiles go through registers: the next tile's loads are issued
+  // before this tile's products and stored to LDS once every wave is done
+  // with this tile.  One 35 KB buffer lets three workgroups share a CU.
   u32x4 kr[4], vr[4];
   auto load_tile = [&](int kt0) {
 #pragma unroll
@@ -338,17 +508,17 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2)
       const int i = tid + kAttnThreads * j;
       const int key = i / 16, col = (i % 16) * 8;
       const int kk = min(kt0 + key, a.cap - 1);
-      kr[j] = *reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(kk) * kHd + col);
+      kr[j] = *reinterpret_cast<const u32x4*>(kc + (kk * kHd + col));  // offsets fit 32 bits
       const int d = i / 8, vcol = (i % 8) * 8;
-      vr[j] = *reinterpret_cast<const u32x4*>(vc + static_cast<uint64_t>(d) * a.cap + min(kt0 + vcol, a.cap - 8));
+      vr[j] = *reinterpret_cast<const u32x4*>(vc + (d * a.cap + min(kt0 + vcol, a.cap - 8)));
     }
   };
-  auto store_tile = [&](int kt0, int buf) {
+  auto store_tile = [&](int kt0) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int i = tid + kAttnThreads * j;
       const int key = i / 16, col = (i % 16) * 8;
-      *reinterpret_cast<u32x4*>(&Ks[buf][key * kQRow + col]) = kr[j];
+      *reinterpret_cast<u32x4*>(&Ks[key * kQRow + 8 * ((col / 8) ^ key_swizzle(key % 16))]) = kr[j];
       const int d = i / 8, vcol = (i % 8) * 8;
       u32x4 vv = vr[j];
       // Keys at or past key_end are masked for every query of this tile
@@ -361,20 +531,19 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2)
           if (e >= left) w[e / 2] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
         vv = u32x4{w[0], w[1], w[2], w[3]};
       }
-      uint2* vdst = reinterpret_cast<uint2*>(&Vs[buf][d * kVRow + vcol]);  // rows are 8-byte aligned
+      uint2* vdst = reinterpret_cast<uint2*>(&Vs[d * kVRow + vcol]);
       vdst[0] = uint2{vv.x, vv.y};
       vdst[1] = uint2{vv.z, vv.w};
     }
   };
   load_tile(0);
-  store_tile(0, 0);
-  __syncthreads();
-  int buf = 0;
-  for (int kt0 = 0; kt0 < key_end; kt0 += kKeyTile, buf ^= 1) {
-    const bool more = kt0 + kKeyTile < key_end;
-    if (more) load_tile(kt0 + kKeyTile);
-    const uint16_t* Kt = Ks[buf];
-    const uint16_t* Vt = Vs[buf];
+  for (int kt0 = 0; kt0 < key_end; kt0 += kKeyTile) {
+    if (kt0 > 0) __syncthreads();
+    store_tile(kt0);
+    __syncthreads();
+    if (kt0 + kKeyTile < key_end) load_tile(kt0 + kKeyTile);
+    const uint16_t* Kt = Ks;
+    const uint16_t* Vt = Vs;
 
     // S^T for four 16-key blocks: s[sub][t] = score of key kt0 + 16 sub +
     // 4 lg + t for the lane's query.
@@ -386,7 +555,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
       for (int sub = 0; sub < 4; ++sub) {
         const bf16x8 ka = as_bf16x8(
-            *reinterpret_cast<const u32x4*>(&Kt[(16 * sub + lq) * kQRow + 32 * ks + 8 * lg]));
+            *reinterpret_cast<const u32x4*>(&Kt[(16 * sub + lq) * kQRow + 8 * (kpiece ^ (4 * ks))]));
         s[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[ks], s[sub], 0, 0, 0);
       }
 
@@ -473,8 +642,6 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2)
         o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pl, o[d], 0, 0, 0);
       }
     }
-    if (more) store_tile(kt0 + kKeyTile, buf ^ 1);
-    __syncthreads();
   }
 
   const int row = q0 + qrow;
@@ -513,12 +680,12 @@ void launch_permute(hipStream_t stream, const uint16_t* x, uint16_t* out, uint64
 void launch_gemm(hipStream_t stream, const GemmArgs& a) {
   // The 256-wide tile needs whole tiles on both sides of the Q | K/V split.
   if (a.N % 256 == 0 && a.n_split % 256 == 0) {
-    const dim3 grid(a.N / 256, a.M / kTileM);
+    const dim3 grid(a.N / kDmaTN, a.M / kTileM);
     switch (a.epilogue) {
-      case kStore: hipLaunchKernelGGL((k_gemm<kStore, 4>), grid, dim3(kGemmThreads), 0, stream, a); break;
-      case kStoreQkv: hipLaunchKernelGGL((k_gemm<kStoreQkv, 4>), grid, dim3(kGemmThreads), 0, stream, a); break;
-      case kResidual: hipLaunchKernelGGL((k_gemm<kResidual, 4>), grid, dim3(kGemmThreads), 0, stream, a); break;
-      default: hipLaunchKernelGGL((k_gemm<kGateUp, 4>), grid, dim3(kGemmThreads), 0, stream, a); break;
+      case kStore: hipLaunchKernelGGL((k_gemm_dma<kStore>), grid, dim3(kGemmThreads), 0, stream, a); break;
+      case kStoreQkv: hipLaunchKernelGGL((k_gemm_dma<kStoreQkv>), grid, dim3(kGemmThreads), 0, stream, a); break;
+      case kResidual: hipLaunchKernelGGL((k_gemm_dma<kResidual>), grid, dim3(kGemmThreads), 0, stream, a); break;
+      default: hipLaunchKernelGGL((k_gemm_dma<kGateUp>), grid, dim3(kGemmThreads), 0, stream, a); break;
     }
     return;
   }
@@ -586,6 +753,8 @@ extern "C" int dl_prefill_attention(dl_queue* queue, const void* q_rot, const vo
     dl::require(queue && q_rot && k_cache && v_cache && output, "null argument");
     dl::require(rows > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0, "invalid attention shape");
     dl::require(capacity % 64 == 0 && first_position + rows <= capacity, "rows exceed the cache capacity",
+                DL_LENGTH_ERROR);
+    dl::require(capacity <= dl::prefill::kMaxAttnCapacity, "cache capacity too large for prefill attention",
                 DL_LENGTH_ERROR);
     dl::enter(queue);
     dl::prefill::AttnArgs a{static_cast<const uint16_t*>(q_rot), static_cast<const uint16_t*>(k_cache),
