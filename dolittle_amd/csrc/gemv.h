@@ -184,11 +184,10 @@ __device__ __forceinline__ void issue_first(const u32x4* __restrict__ tile, int 
   f.valid = true;
 }
 
-// Several rows (B >= 2) make every chunk worth B x 8 FMAs, so a wavefront
-// spends long enough on a batch to hide the next one's latency: the batches
-// of a tile are double-buffered (batch k + 1 is issued before batch k is
-// consumed), and the last one overlaps the first batch of the wavefront's
-// next tile, handed back through `first`.  Needs an even batch count.
+// The batches of a tile are double-buffered (batch k + 1 is issued before
+// batch k is consumed), so a wavefront keeps two batches in flight, and the
+// last one overlaps the first batch of the wavefront's next tile (if there is
+// one), handed back through `first`.  Needs an even batch count.
 template <int P, int B>
 __device__ __forceinline__ void chain_tile_pipelined(const u32x4* __restrict__ src, const float* __restrict__ xt,
                                                      int bstride, int batches, float (&acc)[B], FirstBatch* first,
@@ -198,6 +197,9 @@ __device__ __forceinline__ void chain_tile_pipelined(const u32x4* __restrict__ s
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) w[j] = load_stream(from + j * 64);
   };
+  // Whether a next tile follows is the same for the whole wavefront (only
+  // the lane offset differs).
+  const bool has_next = __builtin_amdgcn_readfirstlane(next_src != nullptr ? 1 : 0) != 0;
   if (first && first->valid) {
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) wa[j] = first->w[j];
@@ -210,7 +212,11 @@ __device__ __forceinline__ void chain_tile_pipelined(const u32x4* __restrict__ s
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) chain_step<B>(wa[j], xt, bstride, k * kBatch + j, acc);
     __builtin_amdgcn_sched_barrier(0);
-    load(wa, k + 2 < batches ? src + (k + 2) * kBatch * 64 : next_src);
+    // Past the tile's last batch: the next tile's first batch, or (no next
+    // tile) the batch just loaded again, which L2 still holds; a select, not
+    // a branch, so both register sets stay in place.
+    load(wa, k + 2 < batches ? src + (k + 2) * kBatch * 64
+                             : (has_next ? next_src : src + (k + 1) * kBatch * 64));
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) chain_step<B>(wb[j], xt, bstride, (k + 1) * kBatch + j, acc);
@@ -226,18 +232,20 @@ __device__ __forceinline__ void chain_tile_pipelined(const u32x4* __restrict__ s
 // (not reset).  `next` (optional) is where the wavefront's chain continues
 // (its next tile, or this tile's next block of inputs): with B >= 2 its
 // first batch is loaded during this call's last batch and left in `first`.
-template <int P, int B>
+// kDeep selects the double-buffered batches (the default for B >= 2; a
+// single-row caller that leaves few wavefronts per SIMD asks for it too, to
+// keep two batches in flight per wavefront).
+template <int P, int B, bool kDeep = (B >= 2)>
 __device__ __forceinline__ void chain_body(const u32x4* __restrict__ tile, const float* __restrict__ xs, int I,
                                            int lane, float (&acc)[B], FirstBatch* first = nullptr,
                                            const u32x4* __restrict__ next = nullptr) {
   const int L = I / P, S = L / 8, stride = L + kXsPad, bstride = P * stride;
   const float* xt = xs + (lane % P) * stride;
   const u32x4* src = tile + lane;
-  if constexpr (B >= 2) {
+  if constexpr (kDeep) {
     const int batches = S / kBatch;
     if (S % kBatch == 0 && batches % 2 == 0) {
-      // A missing next tile reloads this tile's first batch (never used).
-      chain_tile_pipelined<P, B>(src, xt, bstride, batches, acc, first, next ? next + lane : src);
+      chain_tile_pipelined<P, B>(src, xt, bstride, batches, acc, first, next ? next + lane : nullptr);
       if (first) first->valid = next != nullptr;
       return;
     }
@@ -270,13 +278,13 @@ __device__ __forceinline__ void chain_merge(float (&acc)[B]) {
   }
 }
 
-template <int P, int B>
+template <int P, int B, bool kDeep = (B >= 2)>
 __device__ __forceinline__ void chain_tile(const u32x4* __restrict__ tile, const float* __restrict__ xs,
                                            int I, int lane, float (&acc)[B], FirstBatch* first = nullptr,
                                            const u32x4* __restrict__ next = nullptr) {
 #pragma unroll
   for (int b = 0; b < B; ++b) acc[b] = 0.0f;
-  chain_body<P, B>(tile, xs, I, lane, acc, first, next);
+  chain_body<P, B, kDeep>(tile, xs, I, lane, acc, first, next);
   chain_merge<P, B>(acc);
 }
 

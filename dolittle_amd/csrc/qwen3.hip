@@ -825,7 +825,9 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual(ResidualArgs a)
   for (int tile = first; tile < tiles; tile += gridDim.x * W) {
     float acc[B];
     const int next = tile + gridDim.x * W;
-    chain_tile<P, B>(a.w + tile * chunks, xs, a.I, lane, acc, &fb, next < tiles ? a.w + next * chunks : nullptr);
+    // One tile per wavefront at B = 1 leaves one or two wavefronts per SIMD:
+    // two batches in flight per wavefront keep more of HBM busy.
+    chain_tile<P, B, true>(a.w + tile * chunks, xs, a.I, lane, acc, &fb, next < tiles ? a.w + next * chunks : nullptr);
     if (lane % P == 0) {
       const int row = tile * RW + lane / P;
 #pragma unroll
