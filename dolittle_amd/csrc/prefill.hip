@@ -81,17 +81,17 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int m, int n, f
   }
 }
 
-// Epilogue of one wave's 64 x (32 WN) block of 32x32 accumulators, rows
+// Epilogue of one wave's (32 WM) x (32 WN) block of 32x32 accumulators, rows
 // from mb, columns from nb.  Lane layout of a 32x32 accumulator: column
 // lane % 32, row 8 (r / 4) + 4 (lane / 32) + r % 4 for r < 16.  For the
 // gate/up epilogue the four lanes of a quad hold gate 2j, gate 2j+1, up 2j,
 // up 2j+1 of the same rows; the gate lanes finish rows r < 8 and the up lanes
 // rows r >= 8, each taking the other operand from the lane two over.
-template <int EPI, int WN>
-__device__ __forceinline__ void gemm_tile_epilogue(const GemmArgs& a, const floatx16 (&acc)[2][WN], int mb, int nb,
+template <int EPI, int WM, int WN>
+__device__ __forceinline__ void gemm_tile_epilogue(const GemmArgs& a, const floatx16 (&acc)[WM][WN], int mb, int nb,
                                                    int lane) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < WM; ++i) {
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
       const int n = nb + 32 * j + lane % 32;
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #undef DL_GEMM_STORE
 #undef DL_GEMM_COMPUTE
 
-  gemm_tile_epilogue<EPI, WN>(a, acc, m0 + 64 * wm, n0 + 32 * WN * wn, lane);
+  gemm_tile_epilogue<EPI, 2, WN>(a, acc, m0 + 64 * wm, n0 + 32 * WN * wn, lane);
 }
 
 // The 128 x 256 tile fed by direct global-to-LDS loads: each wave
@@ -241,6 +241,11 @@ constexpr int kDmaTN = 256;
 constexpr int kDmaLoads = (kTileM + kDmaTN) * kDmaTK / 8 / kGemmThreads;  // 16-byte loads per thread per chunk
 
 __device__ __forceinline__ int dma_swizzle(int r) { return (r >> 2) & 3; }
+
+// s_waitcnt immediate that waits until at most n vector-memory operations are
+// outstanding (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt
+// left at their no-wait maxima).
+constexpr unsigned vmcnt_wait(unsigned n) { return 0x0f70u | (n & 0xfu) | ((n >> 4) << 14); }
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void global_void;
@@ -347,7 +352,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   int c = 0;
 #define DL_DMA_STEP(Ac, Bc, An, Bn)                                      \
   do {                                                                   \
-    __builtin_amdgcn_s_waitcnt(0x0f70 | kDmaLoads); /* vmcnt(kDmaLoads) */ \
+    __builtin_amdgcn_s_waitcnt(vmcnt_wait(kDmaLoads));                  \
     __builtin_amdgcn_s_barrier();                                        \
     __builtin_amdgcn_sched_barrier(0);                                   \
     issue(min(c + 2, chunks - 1), An, Bn);                               \
@@ -364,9 +369,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   if (c < chunks) DL_DMA_STEP(A0, B0, A2, B2);
   if (c < chunks) DL_DMA_STEP(A1, B1, A0, B0);
 #undef DL_DMA_STEP
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no load outlives the wave
+  __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // no load outlives the wave
 #undef DL_DMA_STEP
-  gemm_tile_epilogue<EPI, 4>(a, acc, m0 + 64 * wm, n0 + 128 * wn, lane);
+  gemm_tile_epilogue<EPI, 2, 4>(a, acc, m0 + 64 * wm, n0 + 128 * wn, lane);
 }
 
 // ------------------------------------------------------------- row norms

@@ -800,12 +800,57 @@ struct ResidualArgs {
   int same_sequence, sequence;
 };
 
+// Orders one wavefront's LDS writes before its own later LDS reads (and the
+// reads before the next writes) when lanes exchange values through LDS.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Residual epilogue of one tile: output row tile * RW + i of sequence row b
+// is h = round(h + round(y)), then the optional steering and capture.  With
+// several rows the merged sums (in lanes i * P) go through the wavefront's
+// LDS area `ep` (RW * B floats) so that lane i * B + b finishes (i, b) and
+// all the h updates of a tile are issued together.
+template <int P, int B>
+__device__ __forceinline__ void residual_outputs(const ResidualArgs& a, const float (&acc)[B], int tile, int lane,
+                                                 float* ep, uint64_t pos, bool steer, bool capture,
+                                                 uint32_t steer_mask) {
+  constexpr int RW = 64 / P;
+  auto finish = [&](int i, int b, float y) {
+    const int row = tile * RW + i;
+    const int r = a.row0 + b;
+    const int seq = a.same_sequence ? a.sequence : r;
+    const uint64_t at = static_cast<uint64_t>(r) * a.D + row;
+    float value = rbf(dl_bf16_to_f32(a.h[at]) + rbf(y));
+    if (steer && ((steer_mask >> seq) & 1u)) value = rbf(value + a.steer[static_cast<uint64_t>(seq) * a.D + row]);
+    a.h[at] = bf16_bits(value);
+    if (capture) {
+      const uint64_t at_pos = a.same_sequence ? pos + r : pos;
+      a.capture[(static_cast<uint64_t>(seq) * a.cap + at_pos) * a.D + row] = bf16_bits(value);
+    }
+  };
+  if constexpr (B == 1) {
+    if (lane % P == 0) finish(lane / P, 0, acc[0]);
+  } else {
+    if (lane % P == 0) {
+#pragma unroll
+      for (int b = 0; b < B; ++b) ep[(lane / P) * B + b] = acc[b];
+    }
+    wave_lds_sync();
+    if (lane < RW * B) finish(lane / B, lane % B, ep[lane]);
+    wave_lds_sync();
+  }
+}
+
 // y = round(x W^T); h = round(h + y); optionally h = round(h + steer) and a
 // copy of h into the capture arena at the current position.
 template <int P, int B>
 __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual(ResidualArgs a) {
   constexpr int W = gemv_waves(B);
   extern __shared__ float xs[];
+  __shared__ float epi[W * (64 / P) * B];
   if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -828,22 +873,7 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual(ResidualArgs a)
     // One tile per wavefront at B = 1 leaves one or two wavefronts per SIMD:
     // two batches in flight per wavefront keep more of HBM busy.
     chain_tile<P, B, true>(a.w + tile * chunks, xs, a.I, lane, acc, &fb, next < tiles ? a.w + next * chunks : nullptr);
-    if (lane % P == 0) {
-      const int row = tile * RW + lane / P;
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        const int r = a.row0 + b;
-        const int seq = a.same_sequence ? a.sequence : r;
-        const uint64_t at = static_cast<uint64_t>(r) * a.D + row;
-        float value = rbf(dl_bf16_to_f32(a.h[at]) + rbf(acc[b]));
-        if (steer && ((steer_mask >> seq) & 1u)) value = rbf(value + a.steer[static_cast<uint64_t>(seq) * a.D + row]);
-        a.h[at] = bf16_bits(value);
-        if (capture) {
-          const uint64_t at_pos = a.same_sequence ? pos + r : pos;
-          a.capture[(static_cast<uint64_t>(seq) * a.cap + at_pos) * a.D + row] = bf16_bits(value);
-        }
-      }
-    }
+    residual_outputs<P, B>(a, acc, tile, lane, epi + wave * RW * B, pos, steer, capture, steer_mask);
   }
 }
 
@@ -860,6 +890,7 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual_chunked(Residua
   constexpr int W = gemv_waves(B);
   constexpr int kChunkSteps = kChunkInputs / (8 * P);
   extern __shared__ float xs[];
+  __shared__ float epi[W * (64 / P) * B];
   if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -895,22 +926,7 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual_chunked(Residua
       }
     }
     chain_merge<P, B>(acc);
-    if (active && lane % P == 0) {
-      const int row = tile * RW + lane / P;
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        const int r = a.row0 + b;
-        const int seq = a.same_sequence ? a.sequence : r;
-        const uint64_t at = static_cast<uint64_t>(r) * a.D + row;
-        float value = rbf(dl_bf16_to_f32(a.h[at]) + rbf(acc[b]));
-        if (steer && ((steer_mask >> seq) & 1u)) value = rbf(value + a.steer[static_cast<uint64_t>(seq) * a.D + row]);
-        a.h[at] = bf16_bits(value);
-        if (capture) {
-          const uint64_t at_pos = a.same_sequence ? pos + r : pos;
-          a.capture[(static_cast<uint64_t>(seq) * a.cap + at_pos) * a.D + row] = bf16_bits(value);
-        }
-      }
-    }
+    if (active) residual_outputs<P, B>(a, acc, tile, lane, epi + wave * RW * B, pos, steer, capture, steer_mask);
   }
 }
 
@@ -930,6 +946,7 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_gateup(GateUpArgs a) {
   constexpr int W = gemv_waves(B);
   extern __shared__ float xs[];
   __shared__ float scratch[W * 40];
+  __shared__ float epi[W * 4 * B];
   if (!a.ctl->active) return;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int tiles = a.F / 2;
@@ -946,13 +963,26 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_gateup(GateUpArgs a) {
     float acc[B];
     const int next = tile + gridDim.x * W;
     chain_tile<16, B>(a.w + tile * chunks, xs, a.D, lane, acc, &fb, next < tiles ? a.w + next * chunks : nullptr);
+    // Lanes 0, 16, 32, 48 hold gate 2t, gate 2t+1, up 2t, up 2t+1.  With
+    // several rows the sums go through LDS so that lane o * B + b evaluates
+    // SiLU(gate) * up of output 2t + o for row b: one SiLU per lane.
+    if constexpr (B == 1) {
+      const float up = __shfl_down(acc[0], 32, 64);
+      if (lane == 0 || lane == 16)
+        a.act[tile * 2 + lane / 16] = bf16_bits(silu_times(rbf(acc[0]), rbf(up)));
+    } else {
+      float* ep = epi + wave * 4 * B;
+      if (lane % 16 == 0) {
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const float up = __shfl_down(acc[b], 32, 64);
-      if (lane == 0 || lane == 16) {
-        const int o = tile * 2 + lane / 16;
-        a.act[static_cast<uint64_t>(b) * a.F + o] = bf16_bits(silu_times(rbf(acc[b]), rbf(up)));
+        for (int b = 0; b < B; ++b) ep[(lane / 16) * B + b] = acc[b];
       }
+      wave_lds_sync();
+      if (lane < 2 * B) {
+        const int o = lane / B, b = lane % B;
+        a.act[static_cast<uint64_t>(b) * a.F + tile * 2 + o] =
+            bf16_bits(silu_times(rbf(ep[o * B + b]), rbf(ep[(2 + o) * B + b])));
+      }
+      wave_lds_sync();
     }
   }
 }
