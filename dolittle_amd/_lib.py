@@ -134,6 +134,12 @@ SIGNATURES = {
     "dl_sampler_result": [vp, u32p, u32p],
     "dl_sampler_set_exact": [vp, cint],
     "dl_sampler_exact_replays": [vp, C.POINTER(u64)],
+    "dl_injection_bytes": [u64, cint, u64p],
+    "dl_injection_submit": [vp, vp, cint, cint, u64, C.c_float, vp],
+    "dl_direction_bytes": [u64, u64p],
+    "dl_direction_submit": [vp, vp, vp, cint, u64, vp],
+    "dl_intervention_initialize": [vp, vp],
+    "dl_intervention_submit": [vp, vp, cint, u64, u64, vp, vp, u64, C.c_float, vp],
 }
 
 

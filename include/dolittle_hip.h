@@ -20,6 +20,8 @@
  *   steering    DeviceIntervention (all-position form)  src/inference/steering/device.h:30-68
  *   capture     DeviceSequence::capture                 src/inference/decoding/device.h:112
  *   injection   EmbeddingOverride                       src/inference/executor.h:129-135
+ *   NLA vectors DeviceInjection                         src/inference/injection/device.h:29-47,
+ *               DeviceDirection, DeviceIntervention     src/inference/steering/device.h:30-68
  *
  * Conventions kept from the reference (src/gpu/device.h:18-25,
  * src/kernels/cuda/launch.h:10-14): launches only enqueue work; they allocate
@@ -379,6 +381,39 @@ int dl_plan_collect(dl_plan* plan, uint32_t* tokens, uint32_t max_new,
 /* Requests cancellation of the running loop (may be called from another
  * thread; DeviceSequence::request_stop, decoding/device.h:126). */
 int dl_plan_request_stop(dl_plan* plan);
+
+/* ------------------------------------------ NLA injection and steering */
+/* DeviceInjection (src/inference/injection/device.h:29-47; kernel
+ * src/kernels/cuda/injection.cu:49-98; law H2 of
+ * docs/architecture/execution-boundary.md:489-498).  storage holds
+ * [norm FP32][status uint32][output row]: the row norm is eight strided FP32
+ * square sums (separate multiply and add, ascending index) added left to
+ * right, then sqrt; out[i] = narrow((h[i] / norm) * scale).  status is 0 on
+ * success and 1 if the source or the norm is not finite, the norm is zero or
+ * an output overflows; an invalid source writes no output.  The source is
+ * never changed.  dl_injection_bytes gives the storage size
+ * (DeviceInjection::required_bytes). */
+int dl_injection_bytes(uint64_t width, int output_dtype, uint64_t* bytes);
+int dl_injection_submit(dl_queue* queue, const void* source, int source_dtype, int output_dtype, uint64_t width,
+                        float scale, void* storage);
+/* DeviceDirection::submit (src/kernels/cuda/steering.cu:69-100): storage holds
+ * [status uint32][uint32][FP32 direction]; the direction is
+ * (edited - original) / ||edited - original|| with the same reduction;
+ * status 1 (and no direction) for a zero or nonfinite norm. */
+int dl_direction_bytes(uint64_t width, uint64_t* bytes);
+int dl_direction_submit(dl_queue* queue, const void* original, const void* edited, int dtype, uint64_t width,
+                        void* storage);
+/* DeviceIntervention (src/kernels/cuda/steering.cu:100-159): state holds
+ * [status uint32][count uint32].  initialize zeroes both.  submit updates
+ * the row of absolute position `selected` when the residual chunk
+ * [rows][width] holds positions [*position, *position + rows) (position is
+ * a device uint64): beta = strength * ||h||, h[i] = narrow(h[i] + beta u[i]),
+ * count += 1; a second application, a prior failure or a nonfinite value
+ * sets status 1 (a row already intervened on is left unchanged). */
+int dl_intervention_initialize(dl_queue* queue, uint32_t* state);
+int dl_intervention_submit(dl_queue* queue, void* residual, int dtype, uint64_t rows, uint64_t width,
+                           const float* direction, const uint64_t* position, uint64_t selected, float strength,
+                           uint32_t* state);
 
 /* ------------------------------------------------------- device sampler */
 /* DeviceCategorical (src/inference/sampling/device.h:58-85) over one BF16

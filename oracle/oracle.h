@@ -8,9 +8,10 @@
  *
  * Three independent restatements live here:
  *
- *  1. The contract mirror (contract.c, prefix `orc_`): the reference CUDA
- *     operators restated on the CPU with their exact reduction trees and
- *     BF16 rounding points, so the GPU path can be compared bit for bit.
+ *  1. The contract mirror (contract.c and nla.c, prefix `orc_`): the
+ *     reference CUDA operators restated on the CPU with their exact
+ *     reduction trees and BF16 rounding points, so the GPU path can be
+ *     compared bit for bit.
  *     Transcendentals come from dolittle_amd/csrc/dl_math.h because the
  *     reference leaves them to each backend's native library (unpinned); the
  *     shared implementation is itself pinned against glibc by the tests.
@@ -91,6 +92,18 @@ void orc_qwen3_block_forward(const orc_qwen3_dims* dims, const orc_qwen3_block* 
 /* Final RMSNorm of one residual row followed by the LM head projection. */
 void orc_qwen3_logits(const orc_qwen3_dims* dims, const uint16_t* final_norm,
                       const uint16_t* lm_head, const uint16_t* h_row, uint16_t* logits);
+
+/* ---- NLA vectors (nla.c): injection.cu:49-98, steering.cu:69-159 ----
+ * Element arrays are BF16 bits (bf16 != 0) or FP32.  orc_inject returns the
+ * status word (writes no output when the source or norm is invalid);
+ * orc_direction returns the status and writes the FP32 direction only when
+ * it is 0; orc_intervene returns 1 when `selected` lies in the chunk (then
+ * state[0] is the status latch and state[1] the application count). */
+uint32_t orc_inject(const void* source, int source_bf16, void* output, int output_bf16, size_t width, float scale,
+                    float* norm);
+uint32_t orc_direction(const void* original, const void* edited, int bf16, size_t width, float* direction);
+int orc_intervene(void* residual, int bf16, size_t rows, size_t width, const float* direction, size_t first,
+                  size_t selected, float strength, uint32_t* state);
 
 /* Greedy choice over BF16 logits: maximum value, lowest id on ties
  * (categorical.cpp:168-173).  Returns 0 on success, 1 on NaN/+inf, 2 when no

@@ -74,6 +74,12 @@ def lib():
                                               u16p, u16p]
         L.orc_qwen3_logits.argtypes = [C.POINTER(Dims), u16p, u16p, u16p, u16p]
         L.orc_greedy_bf16.argtypes = [u16p, sz, C.POINTER(C.c_uint32)]
+        L.orc_inject.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, sz, C.c_float, f32p]
+        L.orc_inject.restype = C.c_uint32
+        L.orc_direction.argtypes = [C.c_void_p, C.c_void_p, C.c_int, sz, f32p]
+        L.orc_direction.restype = C.c_uint32
+        L.orc_intervene.argtypes = [C.c_void_p, C.c_int, sz, sz, f32p, sz, sz, C.c_float, u32p]
+        L.orc_intervene.restype = C.c_int
         L.orc_greedy_bf16.restype = C.c_int
         L.or_mt64_seed.argtypes = [C.POINTER(MT64), C.c_uint64]
         L.or_mt64_next.argtypes = [C.POINTER(MT64)]
@@ -205,6 +211,37 @@ def silu_multiply(g, u, serial=False):
     (lib().ors_silu_multiply if serial else lib().orc_silu_multiply)(
         np.ascontiguousarray(g, np.uint16), np.ascontiguousarray(u, np.uint16), y, len(g))
     return y
+
+
+def _typed(a, bf16):
+    return np.ascontiguousarray(a, np.uint16 if bf16 else np.float32)
+
+
+def inject(source, source_bf16: bool, output_bf16: bool, scale: float):
+    """orc_inject (injection.cu:49-98): returns (status, norm, output); the
+    output holds zeros where the oracle wrote nothing."""
+    src = _typed(source, source_bf16)
+    out = np.zeros(src.size, dtype=np.uint16 if output_bf16 else np.float32)
+    norm = np.zeros(1, np.float32)
+    status = lib().orc_inject(src.ctypes.data, int(source_bf16), out.ctypes.data, int(output_bf16), src.size,
+                              scale, norm)
+    return int(status), float(norm[0]), out
+
+
+def direction(original, edited, bf16: bool):
+    """orc_direction (steering.cu:69-100): returns (status, FP32 direction)."""
+    a, b = _typed(original, bf16), _typed(edited, bf16)
+    out = np.zeros(a.size, dtype=np.float32)
+    status = lib().orc_direction(a.ctypes.data, b.ctypes.data, int(bf16), a.size, out)
+    return int(status), out
+
+
+def intervene(residual, bf16: bool, rows: int, width: int, u, first: int, selected: int, strength: float, state):
+    """orc_intervene (steering.cu:107-159) in place on `residual` and `state`
+    (uint32[2]); returns whether the chunk held the selected row."""
+    assert residual.dtype == (np.uint16 if bf16 else np.float32) and residual.flags.c_contiguous
+    return bool(lib().orc_intervene(residual.ctypes.data, int(bf16), rows, width,
+                                    np.ascontiguousarray(u, np.float32), first, selected, strength, state))
 
 
 def greedy(logits_bf16) -> tuple[int, int]:
