@@ -107,6 +107,9 @@ SIGNATURES = {
     "dl_plan_read_capture": [vp, u32, u64, u64, u16p],
     "dl_plan_set_steering": [vp, u32, i32, C.POINTER(C.c_float)],
     "dl_plan_set_embedding_override": [vp, u64, u16p, u32],
+    "dl_plan_set_injection": [vp, u64, vp, cint, u32],
+    "dl_plan_set_intervention": [vp, u32, i32, u64, vp, C.c_float],
+    "dl_plan_read_intervention": [vp, u32p, u32p],
     "dl_plan_generate": [vp, u32p, u32, u32, C.POINTER(Sampling), u64p, u32p, u32],
     "dl_plan_prepare_generation": [vp, u32p, u32, u32, C.POINTER(Sampling), u64p, u32p, u32],
     "dl_plan_decode_steps": [vp, u32],

@@ -20,7 +20,8 @@ struct Control {
   uint32_t stop_pending;    // last selection made; the next step only consumes
   uint32_t finished_mask;   // sequences that emitted a stop id
   uint32_t all_mask;        // (1 << batch) - 1
-  uint32_t status;          // 0 ok, 1 NaN/+inf logit, 2 no finite logit, 4 bad token
+  uint32_t status;          // 0 ok, 1 NaN/+inf logit, 2 no finite logit, 4 bad token,
+                            // 8 invalid injection, 16 invalid residual intervention
   uint32_t reason;          // 0 limit, 1 eos, 2 cancelled, 3 failure
   uint32_t mode;            // 0 greedy, 1 categorical
   uint32_t override_active;

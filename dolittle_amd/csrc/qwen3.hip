@@ -36,6 +36,7 @@
 #include "dl_synth.h"
 #include "gemv.h"
 #include "heads.h"
+#include "nla.h"
 #include "prefill.h"
 #include "sampler.h"
 
@@ -171,20 +172,35 @@ struct BeginArgs {
   const uint16_t* embedding;    // untied: row-major [V][D]
   const uint16_t* override_row; // [D]
   const uint32_t* cancel;       // host-mapped cancel word
+  const uint32_t* injection_status;    // installed injection's status word, or null
+  const uint32_t* intervention_state;  // [status, count] of the plan's intervention, or null
   int D;
   uint32_t V;
   int tied;
 };
 
 // Embedding (embedding.cu:60-80), the embedding override, and the step's
-// selection decision.  Grid: one block per sequence.
+// selection decision.  Grid: one block per sequence.  An invalid injection
+// (decode.cu decide_stage: the injection status gates the prompt) or a
+// latched intervention failure ends the loop with reason failure before the
+// step consumes anything.
 __global__ __launch_bounds__(kBlock) void k_step_begin(BeginArgs a) {
   Control* c = a.ctl;
   if (!c->active) return;
   const uint64_t pos = c->position;
   const int b = blockIdx.x;
   if (b == 0 && threadIdx.x == 0) {
-    c->select_row = (pos + 1 >= c->prompt_length && !c->stop_pending) ? 1u : 0u;
+    uint32_t failed = 0;
+    if (a.injection_status && *a.injection_status) failed |= 8u;
+    if (a.intervention_state && a.intervention_state[0]) failed |= 16u;
+    if (failed) {
+      c->status |= failed;
+      c->select_row = 0;
+      c->active = 0;
+      c->reason = 3;
+    } else {
+      c->select_row = (pos + 1 >= c->prompt_length && !c->stop_pending) ? 1u : 0u;
+    }
   }
   const uint32_t token = pos < c->prompt_length ? a.tokens[pos] : a.selected[b];
   uint16_t* out = a.h + static_cast<uint64_t>(b) * a.D;
@@ -1107,6 +1123,7 @@ struct EndArgs {
   uint32_t out_capacity;
   const uint8_t* stop_mask; // [V]
   const uint32_t* cancel;   // host-mapped cancel word
+  const uint32_t* intervention_state;  // [status, count], or null
   int batch;
 };
 
@@ -1166,13 +1183,19 @@ __global__ __launch_bounds__(kBlock) void k_step_end(EndArgs a) {
     c->active = 0;
     c->reason = (c->max_new > 0 && (c->finished_mask & c->all_mask) == c->all_mask) ? 1u : 0u;
   }
-  if (c->status) {
-    c->active = 0;
-    c->reason = 3;
-  }
   if (c->active && __hip_atomic_load(a.cancel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
     c->active = 0;
     c->reason = 2;
+  }
+  // decode.cu finish_consumption / finish_sequence: a latched intervention
+  // failure ends the loop, and a loop that ends with its whole prompt
+  // consumed must have applied the intervention exactly once.
+  if (const uint32_t* iv = a.intervention_state) {
+    if (iv[0] || (!c->active && c->position + 1 >= c->prompt_length && iv[1] != 1)) c->status |= 16u;
+  }
+  if (c->status) {
+    c->active = 0;
+    c->reason = 3;
   }
   c->position += 1;
 }
@@ -1302,6 +1325,67 @@ __global__ __launch_bounds__(kBlock) void k_prefill_steer_capture(uint16_t* h, c
       row[k] = bf16_bits(value);
     }
     if (capture) capture[(first + r) * D + k] = bf16_bits(value);
+  }
+}
+
+// The plan's residual intervention (steering.cu:107-159) on the block output
+// of `layer`, the Qwen3 intervention boundary after the second residual add
+// (src/models/qwen3/model.h:7): of the launch's rows, the one holding
+// sequence `sequence` at absolute position `position` gets
+// h <- BF16(h + (strength * ||h||) * u).  Row r is at first + r * pos_step of
+// sequence (same_sequence ? row_sequence : r), with first the control's
+// position when a control is given (the loop must then be active).  A
+// capture of the same layer is rewritten with the intervened row, as the
+// reference copies captures after the boundary's producer step.  A failed
+// application also latches the control's status and cancels the step's
+// selection.  One workgroup.
+struct InterveneArgs {
+  Control* ctl;            // null: a prompt pass without a control
+  uint16_t* h;             // [rows][D]
+  const float* direction;  // [D] unit FP32 direction
+  uint32_t* state;         // [status, count]
+  uint16_t* capture;       // [batch][cap][D] or null
+  uint64_t first, position, cap;
+  uint32_t rows, D, sequence;
+  int pos_step, same_sequence, row_sequence, layer, capture_layer;
+  float strength;
+};
+
+__global__ __launch_bounds__(nla::kThreads) void k_plan_intervene(InterveneArgs a) {
+  __shared__ float sums[nla::kLanes + 2];
+  __shared__ uint32_t invalid;
+  uint64_t first = a.first;
+  int capture_layer = a.capture_layer;
+  if (a.ctl) {
+    if (!a.ctl->active) return;
+    first = a.ctl->position;
+    capture_layer = a.ctl->capture_layer;
+  }
+  uint64_t r;
+  if (a.same_sequence) {
+    if (static_cast<uint32_t>(a.row_sequence) != a.sequence || a.position < first) return;
+    const uint64_t offset = a.position - first;
+    if (a.pos_step == 0) {
+      if (offset != 0) return;
+      r = 0;
+    } else {
+      if (offset % a.pos_step != 0 || offset / a.pos_step >= a.rows) return;
+      r = offset / a.pos_step;
+    }
+  } else {
+    r = a.sequence;
+    if (r >= a.rows || first + r * a.pos_step != a.position) return;
+  }
+  uint16_t* row = a.h + r * a.D;
+  nla::intervene_row(row, a.direction, a.state, a.D, a.strength, sums, &invalid);
+  if (a.capture && capture_layer == a.layer) {
+    // Each thread reads back the elements it wrote in intervene_row.
+    uint16_t* dst = a.capture + (static_cast<uint64_t>(a.sequence) * a.cap + a.position) * a.D;
+    for (uint32_t k = threadIdx.x; k < a.D; k += blockDim.x) dst[k] = row[k];
+  }
+  if (a.ctl && threadIdx.x == 0 && a.state[0]) {
+    a.ctl->status |= 16u;
+    a.ctl->select_row = 0;
   }
 }
 
@@ -1594,6 +1678,24 @@ struct dl_plan {
   bool override_active = false;
   uint32_t override_mask = 0;
   uint64_t override_position = 0;
+  // An installed injection replaces the override row with its BF16 output
+  // (storage + 8) and gates the loop on its status word (storage + 4); the
+  // storage belongs to the caller and must outlive its use.
+  const uint16_t* injection_row = nullptr;
+  const uint32_t* injection_status = nullptr;
+  // One-row residual intervention (steering.cu:107-159) on the output of
+  // block `layer` for sequence `sequence` at `position`.
+  struct Intervention {
+    bool active = false;
+    uint32_t sequence = 0;
+    int32_t layer = -1;
+    uint64_t position = 0;
+    float strength = 0.0f;
+    float* direction = nullptr;  // [D], plan-owned copy
+    uint32_t* state = nullptr;   // [status, count]
+  } intervention;
+  const uint16_t* override_source() const { return injection_row ? injection_row : override_row; }
+  const uint32_t* intervention_state() const { return intervention.active ? intervention.state : nullptr; }
   uint32_t max_new = 0;
   // MFMA prefill: row buffers (allocated on first use for the capacity) and
   // the prompt whose positions [0, prefilled) the caches hold.
@@ -1842,6 +1944,19 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
   }
 }
 
+// The plan's intervention after block `l` over the rows `r` (nothing when
+// no intervention is set or `l` is not its layer).  Without a control the
+// rows start at `first` and the plan's capture layer applies.
+void launch_intervention(dl_plan* p, hipStream_t s, uint32_t l, dl::Control* ctl, const StepRows& r,
+                         uint64_t first = 0) {
+  const auto& iv = p->intervention;
+  if (!iv.active || static_cast<int32_t>(l) != iv.layer) return;
+  dl::InterveneArgs a{ctl, r.h, iv.direction, iv.state, p->capture, first, iv.position, p->cap, r.rows,
+                      p->model->cfg.hidden, iv.sequence, r.pos_step, r.same_sequence, r.sequence,
+                      static_cast<int>(l), p->capture_layer, iv.strength};
+  dl::k_plan_intervene<<<1, dl::nla::kThreads, 0, s>>>(a);
+}
+
 // Records one decode step.  `short_context` selects the fused attention
 // kernel (positions below kFusedKeys) instead of the three-kernel split;
 // categorical generation adds the device sampler after the LM head.
@@ -1849,8 +1964,9 @@ void record_step_all(dl_plan* p, hipStream_t s, bool short_context) {
   using namespace dl;
   const dl_qwen3* m = p->model;
   const auto& c = m->cfg;
-  BeginArgs begin{p->ctl, p->tokens, p->selected, p->h, m->lm_head, m->embedding, p->override_row,
-                  p->cancel_device, static_cast<int>(c.hidden), c.vocab, c.tied_embeddings ? 1 : 0};
+  BeginArgs begin{p->ctl, p->tokens, p->selected, p->h, m->lm_head, m->embedding, p->override_source(),
+                  p->cancel_device, p->injection_status, p->intervention_state(), static_cast<int>(c.hidden),
+                  c.vocab, c.tied_embeddings ? 1 : 0};
   k_step_begin<<<p->batch, kBlock, 0, s>>>(begin);
   static const int kShort[] = {0, 8, 4, 5, 6};
   static const int kLong[] = {0, 1, 2, 3, 4, 5, 6};
@@ -1859,6 +1975,7 @@ void record_step_all(dl_plan* p, hipStream_t s, bool short_context) {
       for (int which : kShort) launch_step_kernel(p, s, which, l, p->ctl, plan_rows(p));
     else
       for (int which : kLong) launch_step_kernel(p, s, which, l, p->ctl, plan_rows(p));
+    launch_intervention(p, s, l, p->ctl, plan_rows(p));
   }
   launch_step_kernel(p, s, 7, 0, p->ctl, plan_rows(p));
   if (p->sampling.mode == 1) {
@@ -1875,7 +1992,7 @@ void record_step_all(dl_plan* p, hipStream_t s, bool short_context) {
     sampling::launch_select(s, ra);
   }
   EndArgs ea{p->ctl, p->partial_keys, p->partial_flags, p->head_blocks, p->selected, p->out_tokens, p->cap,
-             p->stop_mask, p->cancel_device, static_cast<int>(p->batch)};
+             p->stop_mask, p->cancel_device, p->intervention_state(), static_cast<int>(p->batch)};
   k_step_end<<<1, kBlock, 0, s>>>(ea);
 }
 
@@ -1921,6 +2038,11 @@ namespace {
 // position advances by one per step while the loop is active) and picks the
 // short-context graph below kFusedKeys.  A step launched after the loop
 // stopped exits at once in either graph.
+// Zeroes the intervention's status and count (a new pass over the prompt).
+void reset_intervention(dl_plan* p) {
+  dl::check_hip(hipMemsetAsync(p->intervention.state, 0, 8, p->queue->stream), "intervention reset");
+}
+
 void launch_steps(dl_plan* p, uint32_t steps) {
   for (uint32_t i = 0; i < steps; ++i) {
     const bool short_context = p->host_position < static_cast<uint64_t>(dl::kFusedKeys);
@@ -1935,8 +2057,11 @@ void launch_steps(dl_plan* p, uint32_t steps) {
 
 void init_control(dl_plan* p, uint64_t position, uint32_t prompt_length, uint32_t max_new, uint32_t mode) {
   p->host_position = position;
+  // An injection replaces a prompt row only (executor.cpp: the embedding
+  // replacement is submitted with the prompt body).
+  const bool override_on = p->override_active && !(p->injection_row && p->override_position >= prompt_length);
   dl::InitArgs a{p->ctl, position, prompt_length, max_new, p->batch, mode, p->capture_layer, p->steer_layer,
-                 p->steer_mask, p->override_active ? 1u : 0u, p->override_mask, p->override_position};
+                 p->steer_mask, override_on ? 1u : 0u, p->override_mask, p->override_position};
   dl::k_init_control<<<1, 1, 0, p->queue->stream>>>(a);
   dl::check_launch(p->queue, "init control");
 }
@@ -1992,6 +2117,9 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
     p->stop_mask = p->alloc<uint8_t>(V);
     p->override_row = p->alloc<uint16_t>(D);
     p->steer = p->alloc<float>(B * D);
+    p->intervention.direction = p->alloc<float>(D);
+    p->intervention.state = p->alloc<uint32_t>(2);
+    dl::check_hip(hipMemsetAsync(p->intervention.state, 0, 8, queue->stream), "intervention clear");
     p->sampler = dl::sampling::carve_workspace(p->alloc<uint8_t>(dl::sampling::workspace_bytes(batch, 0)),
                                                static_cast<int>(batch), 0);
     dl::sampling::launch_clear(queue->stream, p->sampler, static_cast<int>(batch));
@@ -2104,6 +2232,7 @@ int dl_plan_forward(dl_plan* plan, const uint32_t* tokens, uint32_t rows) {
     // All sequences consume the same rows in this diagnostic path.
     dl::check_hip(hipMemcpyAsync(plan->tokens + pos, tokens, rows * 4, hipMemcpyHostToDevice, s), "token upload");
     plan->max_new = 1;
+    if (pos == 0) reset_intervention(plan);
     init_control(plan, pos, static_cast<uint32_t>(pos + rows), 1, 0);
     launch_steps(plan, rows);
     dl::check_hip(hipStreamSynchronize(s), "forward");
@@ -2184,10 +2313,22 @@ int dl_plan_set_steering(dl_plan* plan, uint32_t seq, int32_t layer, const float
   });
 }
 
+// Drops an installed injection; the recorded steps hold its pointers, so
+// they are recorded again.
+static void clear_injection(dl_plan* plan) {
+  if (!plan->injection_row) return;
+  plan->injection_row = nullptr;
+  plan->injection_status = nullptr;
+  plan->override_active = false;
+  dl::check_hip(hipStreamSynchronize(plan->queue->stream), "injection clear");
+  plan->capture_step();
+}
+
 int dl_plan_set_embedding_override(dl_plan* plan, uint64_t position, const uint16_t* row, uint32_t seq_mask) {
   return guard([&] {
     require(plan != nullptr, "null plan");
     dl::enter(plan->queue);
+    clear_injection(plan);
     if (!row || seq_mask == 0) {
       plan->override_active = false;
       return;
@@ -2200,6 +2341,78 @@ int dl_plan_set_embedding_override(dl_plan* plan, uint64_t position, const uint1
     plan->override_active = true;
     plan->override_position = position;
     plan->override_mask = seq_mask;
+  });
+}
+
+int dl_plan_set_injection(dl_plan* plan, uint64_t position, const void* storage, int output_dtype,
+                          uint32_t seq_mask) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    dl::enter(plan->queue);
+    if (!storage || seq_mask == 0) {
+      clear_injection(plan);
+      return;
+    }
+    require(output_dtype == DL_BF16, "injection type differs from the activation storage");
+    require(reinterpret_cast<uintptr_t>(storage) % 4 == 0, "misaligned injection region");
+    require(position < plan->capacity, "injection position outside the cache", DL_LENGTH_ERROR);
+    const auto* base = static_cast<const uint8_t*>(storage);
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "injection setup");
+    plan->injection_status = reinterpret_cast<const uint32_t*>(base + sizeof(float));
+    plan->injection_row = reinterpret_cast<const uint16_t*>(base + sizeof(float) + sizeof(uint32_t));
+    plan->override_active = true;
+    plan->override_position = position;
+    plan->override_mask = seq_mask;
+    plan->prefilled = 0;  // a prefilled prompt did not see the injection
+    plan->capture_step();
+  });
+}
+
+int dl_plan_set_intervention(dl_plan* plan, uint32_t seq, int32_t layer, uint64_t position, const float* direction,
+                             float strength) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    dl::enter(plan->queue);
+    const auto& c = plan->model->cfg;
+    auto& iv = plan->intervention;
+    const bool was_active = iv.active;
+    require(std::isfinite(strength) && strength >= 0.0f, "intervention preparation state");
+    if (!direction || layer < 0 || strength == 0.0f) {
+      // executor.cpp prepare_intervention: strength zero prepares nothing.
+      iv.active = false;
+    } else {
+      require(seq < plan->batch, "sequence out of range");
+      require(layer < static_cast<int32_t>(c.layers), "unsupported intervention boundary");
+      require(position < plan->capacity, "intervention preparation state", DL_LENGTH_ERROR);
+      require(reinterpret_cast<uintptr_t>(direction) % 4 == 0, "misaligned direction region");
+      // Stream order places the copy after the kernel that wrote the direction.
+      dl::check_hip(hipMemcpyAsync(iv.direction, direction, uint64_t(c.hidden) * 4, hipMemcpyDefault,
+                                   plan->queue->stream),
+                    "direction copy");
+      iv.active = true;
+      iv.sequence = seq;
+      iv.layer = layer;
+      iv.position = position;
+      iv.strength = strength;
+    }
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "intervention setup");
+    reset_intervention(plan);
+    plan->prefilled = 0;  // a prefilled prompt did not see the intervention
+    if (iv.active || was_active) plan->capture_step();
+  });
+}
+
+int dl_plan_read_intervention(dl_plan* plan, uint32_t* status, uint32_t* count) {
+  return guard([&] {
+    require(plan && status && count, "null argument");
+    dl::enter(plan->queue);
+    uint32_t state[2];
+    dl::check_hip(hipMemcpyAsync(state, plan->intervention.state, sizeof state, hipMemcpyDeviceToHost,
+                                 plan->queue->stream),
+                  "read intervention");
+    dl::check_hip(hipStreamSynchronize(plan->queue->stream), "read intervention wait");
+    *status = state[0];
+    *count = state[1];
   });
 }
 
@@ -2313,6 +2526,8 @@ int dl_plan_prepare_generation(dl_plan* plan, const uint32_t* prompt, uint32_t p
     require(law.top_k <= V, "sampling shape or top-k mismatch");
     for (uint32_t i = 0; i < prompt_length; ++i) require(prompt[i] < V, "prompt id outside the vocabulary");
     for (uint32_t i = 0; i < stop_count; ++i) require(stop_ids && stop_ids[i] < V, "stop id outside the vocabulary");
+    require(!plan->intervention.active || plan->intervention.position < prompt_length,
+            "intervention must belong to replay prefix");
     hipStream_t s = plan->queue->stream;
     dl::check_hip(hipStreamSynchronize(s), "generate wait");
     const dl::sampling::Settings& had = plan->sampling;
@@ -2343,7 +2558,10 @@ int dl_plan_prepare_generation(dl_plan* plan, const uint32_t* prompt, uint32_t p
     const bool resume = plan->prefilled > 0 && plan->prefilled_prompt.size() == prompt_length &&
                         std::equal(prompt, prompt + prompt_length, plan->prefilled_prompt.begin());
     plan->start_position = resume ? plan->prefilled : 0;
-    if (!resume) plan->prefilled = 0;
+    if (!resume) {
+      plan->prefilled = 0;
+      reset_intervention(plan);
+    }
     init_control(plan, plan->start_position, prompt_length, max_new, mode);
   });
 }
@@ -2394,14 +2612,16 @@ int dl_plan_request_stop(dl_plan* plan) {
 }
 
 
-// True when the prompt pass differs between the plan's sequences (steering
-// or an embedding override applied to some of them, or capture, which writes
-// every sequence's arena), so each sequence needs its own pass.
+// True when the prompt pass differs between the plan's sequences (steering,
+// an intervention or an embedding override applied to some of them, or
+// capture, which writes every sequence's arena), so each sequence needs its
+// own pass.
 static bool sequences_differ(const dl_plan* plan) {
   const uint32_t all = (1u << plan->batch) - 1u;
   const bool override_differs =
       plan->override_active && (plan->override_mask & all) != 0 && (plan->override_mask & all) != all;
-  return plan->batch > 1 && (plan->steer_mask != 0 || plan->capture_layer >= 0 || override_differs);
+  return plan->batch > 1 &&
+         (plan->steer_mask != 0 || plan->capture_layer >= 0 || override_differs || plan->intervention.active);
 }
 
 // Copies sequence 0's cached positions [0, rows) into the other sequences'
@@ -2436,8 +2656,11 @@ int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_lengt
     for (uint32_t i = 0; i < prompt_length; ++i) require(prompt[i] < c.vocab, "prompt id outside the vocabulary");
     hipStream_t s = plan->queue->stream;
     dl::check_hip(hipStreamSynchronize(s), "prefill wait");
+    require(!plan->intervention.active || plan->intervention.position < prompt_length,
+            "intervention must belong to replay prefix");
     plan->prefilled = 0;
     plan->prefilled_prompt.assign(prompt, prompt + prompt_length);
+    reset_intervention(plan);
     // The last prompt position is consumed by the exact decode step, which
     // also selects the first token.
     const uint32_t rows = prompt_length - 1;
@@ -2466,7 +2689,7 @@ int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_lengt
     const bool per_sequence = sequences_differ(plan);
     const uint32_t runs = per_sequence ? plan->batch : 1;
     for (uint32_t seq = 0; seq < runs; ++seq) {
-      dl::PrefillEmbedArgs ea{plan->tokens, m->lm_head, m->embedding, plan->override_row, pf.h, rows, D, 0,
+      dl::PrefillEmbedArgs ea{plan->tokens, m->lm_head, m->embedding, plan->override_source(), pf.h, rows, D, 0,
                               c.tied_embeddings ? 1 : 0,
                               (plan->override_active && ((plan->override_mask >> seq) & 1u)) ? 1 : 0,
                               plan->override_position};
@@ -2544,6 +2767,9 @@ int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_lengt
           dl::k_prefill_steer_capture<<<rows, dl::kBlock, 0, s>>>(
               pf.h, steer ? plan->steer + uint64_t(seq) * D : nullptr,
               capture ? plan->capture + uint64_t(seq) * plan->cap * D : nullptr, D, 0);
+        const StepRows pr{pf.h, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, rows, 0, 0, 0, 1, 1,
+                          static_cast<int>(seq)};
+        launch_intervention(plan, s, l, nullptr, pr, 0);
       }
       dl::check_launch(plan->queue, "prefill");
     }
@@ -2570,8 +2796,11 @@ int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt
     for (uint32_t i = 0; i < prompt_length; ++i) require(prompt[i] < c.vocab, "prompt id outside the vocabulary");
     hipStream_t s = plan->queue->stream;
     dl::check_hip(hipStreamSynchronize(s), "prefill wait");
+    require(!plan->intervention.active || plan->intervention.position < prompt_length,
+            "intervention must belong to replay prefix");
     plan->prefilled = 0;
     plan->prefilled_prompt.assign(prompt, prompt + prompt_length);
+    reset_intervention(plan);
     const uint32_t rows = prompt_length - 1;
     if (rows == 0) return;
     const uint64_t D = c.hidden, QW = uint64_t(c.q_heads) * c.head_dim, KW = uint64_t(c.kv_heads) * c.head_dim,
@@ -2595,7 +2824,7 @@ int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt
         const uint32_t n = std::min<uint32_t>(static_cast<uint32_t>(R), rows - p0);
         dl::k_chunk_control<<<1, 1, 0, s>>>(plan->ctl, ex.ctl, p0, plan->capture_layer, plan->steer_layer,
                                             plan->steer_mask);
-        dl::PrefillEmbedArgs ea{plan->tokens, m->lm_head, m->embedding, plan->override_row, ex.h, n,
+        dl::PrefillEmbedArgs ea{plan->tokens, m->lm_head, m->embedding, plan->override_source(), ex.h, n,
                                 static_cast<uint32_t>(D), p0, c.tied_embeddings ? 1 : 0,
                                 (plan->override_active && ((plan->override_mask >> seq) & 1u)) ? 1 : 0,
                                 plan->override_position};
@@ -2612,6 +2841,7 @@ int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt
             for (int which : {1, 2, 3}) launch_step_kernel(plan, s, which, l, ex.ctl, r);
           }
           for (int which : {4, 5, 6}) launch_step_kernel(plan, s, which, l, ex.ctl, r);
+          launch_intervention(plan, s, l, ex.ctl, r);
         }
       }
       dl::check_launch(plan->queue, "exact prefill");

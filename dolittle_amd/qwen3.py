@@ -180,6 +180,43 @@ class Plan:
         r = np.ascontiguousarray(row, dtype=np.uint16)
         _lib.call("dl_plan_set_embedding_override", self.handle, position, r.ctypes.data_as(_lib.u16p), seq_mask)
 
+    def set_injection(self, injection, position: int, seq_mask: int = 1) -> None:
+        """Live injection (executor.cpp:1583-1632): the output row of a
+        DeviceInjection (dolittle_amd.interventions) replaces the embedding
+        of prompt position `position` for the sequences in `seq_mask`; its
+        status gates the loop.  None removes it."""
+        if injection is None:
+            _lib.call("dl_plan_set_injection", self.handle, 0, None, 0, 0)
+            return
+        from .interventions import _DTYPE
+        self._injection = injection  # the plan reads its storage until replaced
+        _lib.call("dl_plan_set_injection", self.handle, position, injection.storage.ptr(),
+                  _DTYPE[injection.output_type], seq_mask)
+
+    def set_intervention(self, seq: int, layer: int, position: int, direction, strength: float) -> None:
+        """Residual intervention (executor.cpp:1717-1748) on block `layer`'s
+        output row of sequence `seq` at `position`.  `direction` is a device
+        Region of `hidden` FP32 values (DeviceDirection.finish()) or a host
+        FP32 array; None or strength 0 removes it."""
+        if direction is None:
+            _lib.call("dl_plan_set_intervention", self.handle, seq, -1, 0, None, C.c_float(0.0))
+            return
+        if isinstance(direction, np.ndarray):
+            v = np.ascontiguousarray(direction, dtype=np.float32)
+            if v.size != self.model.config.hidden:
+                raise ValueError("direction width")
+            ptr = v.ctypes.data_as(C.c_void_p)
+        else:
+            if direction.bytes != self.model.config.hidden * 4:
+                raise ValueError("direction width")
+            ptr = direction.ptr()
+        _lib.call("dl_plan_set_intervention", self.handle, seq, layer, position, ptr, C.c_float(strength))
+
+    def read_intervention(self) -> tuple[int, int]:
+        status, count = C.c_uint32(), C.c_uint32()
+        _lib.call("dl_plan_read_intervention", self.handle, C.byref(status), C.byref(count))
+        return status.value, count.value
+
     # -- device-owned loop
     def _args(self, prompt, sampling, seeds, stop_ids):
         p = np.ascontiguousarray(prompt, dtype=np.uint32)

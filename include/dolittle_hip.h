@@ -19,7 +19,9 @@
  *   sampling    DeviceCategorical                       src/inference/sampling/device.h:58-85
  *   steering    DeviceIntervention (all-position form)  src/inference/steering/device.h:30-68
  *   capture     DeviceSequence::capture                 src/inference/decoding/device.h:112
- *   injection   EmbeddingOverride                       src/inference/executor.h:129-135
+ *   injection   EmbeddingOverride                       src/inference/executor.h:129-135,
+ *               live Injection + DeviceSequence::replace executor.cpp:1583-1632, decode.cu:221-230
+ *   intervention CachedForwardPlan::prepare_intervention src/inference/executor.cpp:1717-1748
  *   NLA vectors DeviceInjection                         src/inference/injection/device.h:29-47,
  *               DeviceDirection, DeviceIntervention     src/inference/steering/device.h:30-68
  *
@@ -263,7 +265,8 @@ typedef struct dl_sampling {
 typedef struct dl_generation_result {
   uint32_t generated; /* tokens produced */
   uint32_t reason;    /* 0 limit, 1 eos/stop id, 2 cancelled, 3 failure (device.h:93) */
-  uint32_t status;    /* sampler status latch: 0 ok, 1 NaN/+inf logit, 2 no finite logit */
+  uint32_t status;    /* failure latch (bits): 1 NaN/+inf logit, 2 no finite logit, 4 token outside
+                         the vocabulary, 8 invalid injection, 16 invalid intervention */
   uint32_t reserved;
   uint64_t position;  /* next position */
 } dl_generation_result;
@@ -314,6 +317,36 @@ int dl_plan_set_steering(dl_plan* plan, uint32_t seq, int32_t layer, const float
  * bits) for the sequences in `seq_mask` (bit i = sequence i). */
 int dl_plan_set_embedding_override(dl_plan* plan, uint64_t position, const uint16_t* row,
                                    uint32_t seq_mask);
+/* Live injection (CachedForwardPlan with Injection::device,
+ * executor.cpp:1583-1632; DeviceSequence::replace, decode.cu:221-230):
+ * `storage` is a DeviceInjection region (dl_injection_bytes(hidden, DL_BF16)
+ * bytes, BF16 output) that the caller keeps alive and submits on the plan's
+ * queue before the prompt runs.  Its output row replaces the embedding of
+ * prompt position `position` of the sequences in `seq_mask`; a nonzero
+ * injection status ends the next generation before it consumes anything,
+ * with status bit 8 and reason failure (decode.cu decide_stage).  Replaces
+ * any embedding override; a null storage or empty mask removes it. */
+int dl_plan_set_injection(dl_plan* plan, uint64_t position, const void* storage, int output_dtype,
+                          uint32_t seq_mask);
+/* Residual intervention (CachedForwardPlan::prepare_intervention,
+ * executor.cpp:1717-1748; DeviceIntervention::submit after the boundary's
+ * producer step, executor.cpp:1633-1643): after block `layer`'s output,
+ * the row of sequence `seq` at prompt position `position` gets
+ * h <- BF16(h + (strength * ||h||) * direction) (steering.cu:107-159).
+ * `direction` is `hidden` FP32 values (a DeviceDirection region or host
+ * memory), copied at this call.  Every prompt pass (generation from
+ * position 0, prefill, forward from position 0) zeroes the plan's
+ * [status, count]; a failed application latches status bit 16 and ends the
+ * loop, and a loop that finishes with its prompt consumed needs count == 1
+ * (decode.cu finish_sequence), else status bit 16 and reason failure.
+ * Generation requires position < prompt length.  strength 0, layer < 0 or a
+ * null direction removes the intervention; strength must be finite and
+ * nonnegative. */
+int dl_plan_set_intervention(dl_plan* plan, uint32_t seq, int32_t layer, uint64_t position, const float* direction,
+                             float strength);
+/* The intervention's device status and application count (the regions of
+ * DeviceIntervention::status() and count()). */
+int dl_plan_read_intervention(dl_plan* plan, uint32_t* status, uint32_t* count);
 
 /* MFMA prefill of a long prompt: positions
  * [0, prompt_length - 1) of every sequence run as BF16 MFMA GEMMs and causal
