@@ -49,6 +49,29 @@ class GenerationResult(C.Structure):
                 ("reserved", C.c_uint32), ("position", C.c_uint64)]
 
 
+class ArchiveLimits(C.Structure):
+    _fields_ = [("max_header_bytes", C.c_uint64), ("max_metadata_bytes", C.c_uint64),
+                ("max_tensor_count", C.c_uint64)]
+
+
+class Artifact(C.Structure):
+    _fields_ = [("relative_path", C.c_char_p), ("byte_size", C.c_uint64), ("sha256", C.c_char_p)]
+
+
+class ArchiveRequest(C.Structure):
+    _fields_ = [("root", C.c_char_p), ("repository", C.c_char_p), ("revision", C.c_char_p),
+                ("artifacts", C.POINTER(Artifact)), ("shards", C.POINTER(C.c_char_p)), ("index", C.c_char_p),
+                ("max_header_bytes", C.c_uint64), ("max_metadata_bytes", C.c_uint64),
+                ("max_tensor_count", C.c_uint64), ("artifact_count", C.c_uint32), ("shard_count", C.c_uint32),
+                ("verification_workers", C.c_uint32), ("integrity", C.c_int32)]
+
+
+class TensorInfo(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("shape", C.POINTER(C.c_uint64)), ("payload", C.c_void_p),
+                ("data_offset", C.c_uint64), ("byte_count", C.c_uint64), ("rank", C.c_uint32),
+                ("dtype", C.c_int32)]
+
+
 # name -> argument types (all return int status)
 SIGNATURES = {
     "dl_device_open": [cint, vpp],
@@ -143,6 +166,20 @@ SIGNATURES = {
     "dl_direction_submit": [vp, vp, vp, cint, u64, vp],
     "dl_intervention_initialize": [vp, vp],
     "dl_intervention_submit": [vp, vp, cint, u64, u64, vp, vp, u64, C.c_float, vp],
+    "dl_safetensors_parse_header": [C.c_char_p, u64, u64, C.POINTER(ArchiveLimits), vpp],
+    "dl_safetensors_open": [C.POINTER(ArchiveRequest), vpp],
+    "dl_archive_destroy": [vp],
+    "dl_archive_tensor_count": [vp, u64p],
+    "dl_archive_tensor_info": [vp, u64, C.POINTER(TensorInfo)],
+    "dl_archive_find": [vp, C.c_char_p, C.POINTER(TensorInfo)],
+    "dl_archive_identity": [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.POINTER(C.c_char_p)],
+    "dl_archive_artifact": [vp, C.c_char_p, vpp, u64p],
+    "dl_sha256_hex": [vp, u64, C.c_char_p],
+    "dl_qwen3_parse_config": [C.c_char_p, u64, cint, u64, C.POINTER(Qwen3Config), u64p],
+    "dl_qwen3_tensor_name": [cint, u32, C.c_char_p, u64],
+    "dl_qwen3_bind_parameters": [C.POINTER(Qwen3Config), cint, vp],
+    "dl_qwen3_bind_archive": [vp, C.c_char_p, C.POINTER(Qwen3Config), u64p, u64p],
+    "dl_qwen3_load": [vp, vp, vp, C.c_char_p],
 }
 
 

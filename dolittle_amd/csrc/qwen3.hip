@@ -27,9 +27,11 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <thread>
 #include <utility>
 #include <vector>
 
+#include "archive.h"
 #include "dl_control.h"
 #include "dl_device.h"
 #include "dl_internal.h"
@@ -1614,6 +1616,115 @@ static int transfer_tensor(dl_qwen3* model, dl_queue* queue, int role, uint32_t 
     (void)hipFree(tmp);
     dl::check_hip(e, "tensor transfer");
     dl::check_hip(w, "tensor transfer wait");
+  });
+}
+
+// Places one row-major BF16 parameter held in device memory at `src` into
+// its resident form: a copy for vectors and tables, the packing kernel for
+// GEMV operands.
+static void place_parameter(dl_qwen3* model, hipStream_t s, int role, uint32_t layer, const uint16_t* src,
+                            uint64_t elements) {
+  if (role == DL_ROLE_EMBEDDING && model->cfg.tied_embeddings) role = DL_ROLE_LM_HEAD;
+  uint64_t n = 0;
+  if (uint16_t* p = model->plain(role, layer, &n)) {
+    require(elements == n, "element count does not match the parameter", DL_LENGTH_ERROR);
+    dl::check_hip(hipMemcpyAsync(p, src, n * 2, hipMemcpyDeviceToDevice, s), "parameter copy");
+    return;
+  }
+  uint64_t rows, cols;
+  const dl::PackedView v = model->view(role, layer, &rows, &cols);
+  require(elements == rows * cols, "element count does not match the parameter", DL_LENGTH_ERROR);
+  dl::k_pack_view<<<fill_grid(elements), 256, 0, s>>>(v, rows, const_cast<uint16_t*>(src), 0, nullptr);
+  dl::check_hip(hipGetLastError(), "parameter packing");
+}
+
+namespace {
+// Bounded transfer staging of a checkpoint upload: one device buffer for the
+// largest tensor and two pinned host chunks that alternate, so the host copy
+// out of the file mapping overlaps the previous chunk's DMA.
+struct UploadStaging {
+  static constexpr uint64_t kChunk = uint64_t{64} << 20;
+  hipStream_t stream = nullptr;
+  void* device = nullptr;
+  void* host[2] = {nullptr, nullptr};
+  hipEvent_t done[2] = {nullptr, nullptr};
+  explicit UploadStaging(hipStream_t s, uint64_t largest) : stream(s) {
+    dl::check_hip(hipMalloc(&device, std::max<uint64_t>(largest, 2)), "upload staging");
+    for (int i = 0; i < 2; ++i) {
+      dl::check_hip(hipHostMalloc(&host[i], kChunk, hipHostMallocDefault), "pinned upload staging");
+      dl::check_hip(hipEventCreateWithFlags(&done[i], hipEventDisableTiming), "upload event");
+    }
+  }
+  ~UploadStaging() {
+    (void)hipStreamSynchronize(stream);
+    for (int i = 0; i < 2; ++i) {
+      if (done[i]) (void)hipEventDestroy(done[i]);
+      if (host[i]) (void)hipHostFree(host[i]);
+    }
+    if (device) (void)hipFree(device);
+  }
+};
+
+// memcpy split over a few host threads (the mapped pages fault in from the
+// file as they are read).
+void parallel_copy(void* dst, const void* src, uint64_t bytes) {
+  constexpr uint64_t kPiece = uint64_t{8} << 20;
+  const uint64_t parts = std::min<uint64_t>(8, std::max<uint64_t>(1, bytes / kPiece));
+  if (parts == 1) {
+    std::memcpy(dst, src, bytes);
+    return;
+  }
+  std::vector<std::thread> threads;
+  const uint64_t step = dl::ceil_div(bytes, parts);
+  for (uint64_t k = 0; k < parts; ++k) {
+    const uint64_t begin = k * step, end = std::min(bytes, begin + step);
+    if (begin >= end) break;
+    threads.emplace_back([=] {
+      std::memcpy(static_cast<uint8_t*>(dst) + begin, static_cast<const uint8_t*>(src) + begin, end - begin);
+    });
+  }
+  for (auto& t : threads) t.join();
+}
+}  // namespace
+
+int dl_qwen3_load(dl_qwen3* model, dl_queue* queue, const dl_archive* archive, const char* configuration_artifact) {
+  return guard([&] {
+    require(model && archive && configuration_artifact, "null argument");
+    dl::enter(queue);
+    std::vector<dl::qwen3::Binding> bindings;
+    const auto settings = dl::qwen3::bind_causal_lm(*archive, configuration_artifact, &bindings);
+    const auto& c = model->cfg;
+    const auto& a = settings.config;
+    require(settings.weight_dtype == DL_BF16, "this backend holds BF16 weights (no type conversion)");
+    require(!c.tied_embeddings, "a Qwen3 checkpoint binds an untied embedding and LM head");
+    require(c.layers == a.layers && c.hidden == a.hidden && c.q_heads == a.q_heads && c.kv_heads == a.kv_heads &&
+                c.head_dim == a.head_dim && c.ffn == a.ffn && c.vocab == a.vocab && c.rms_eps == a.rms_eps &&
+                c.rope_theta == a.rope_theta,
+            "archive configuration differs from the resident model");
+    uint64_t largest = 0;
+    for (const auto& b : bindings) {
+      require(b.tensor->payload != nullptr || b.tensor->byte_count == 0, "archive holds no tensor payloads");
+      largest = std::max(largest, b.tensor->byte_count);
+    }
+    hipStream_t stream = queue->stream;
+    UploadStaging staging(stream, largest);
+    uint64_t chunk = 0;
+    for (const auto& b : bindings) {
+      const uint8_t* src = b.tensor->payload;
+      const uint64_t n = b.tensor->byte_count;
+      for (uint64_t off = 0; off < n; off += UploadStaging::kChunk, ++chunk) {
+        const uint64_t len = std::min(UploadStaging::kChunk, n - off);
+        const int slot = static_cast<int>(chunk % 2);
+        if (chunk >= 2) dl::check_hip(hipEventSynchronize(staging.done[slot]), "upload staging wait");
+        parallel_copy(staging.host[slot], src + off, len);
+        dl::check_hip(hipMemcpyAsync(static_cast<uint8_t*>(staging.device) + off, staging.host[slot], len,
+                                     hipMemcpyHostToDevice, stream),
+                      "parameter upload");
+        dl::check_hip(hipEventRecord(staging.done[slot], stream), "upload event");
+      }
+      place_parameter(model, stream, b.role, b.layer, static_cast<const uint16_t*>(staging.device), n / 2);
+    }
+    dl::check_hip(hipStreamSynchronize(stream), "checkpoint upload");
   });
 }
 

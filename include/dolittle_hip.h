@@ -57,7 +57,7 @@ typedef enum dl_status {
 const char* dl_last_error(void);
 
 /* Storage element types (src/tensors/representations/representation.h). */
-typedef enum dl_dtype { DL_BF16 = 1, DL_F32 = 2 } dl_dtype;
+typedef enum dl_dtype { DL_BF16 = 1, DL_F32 = 2, DL_U32 = 3 /* archive catalogs only */ } dl_dtype;
 
 /* ----------------------------------------------------------------- runtime */
 typedef struct dl_device dl_device;
@@ -246,6 +246,99 @@ int dl_qwen3_read_tensor(dl_qwen3* model, dl_queue* queue, int role, uint32_t la
                          uint16_t* host, uint64_t elements);
 /* Bytes of resident parameter storage. */
 int dl_qwen3_resident_bytes(dl_qwen3* model, uint64_t* bytes);
+
+/* ------------------------------------------------- checkpoint archives */
+/* Safetensors archives (src/tensors/formats/safetensors.h:101-117) and the
+ * Qwen3 checkpoint binding (src/models/qwen3/checkpoint.h:104-123).  Host
+ * code only: these calls touch no GPU.  Malformed or unsupported data is
+ * DL_INVALID_ARGUMENT, a limit or overflow DL_LENGTH_ERROR, an I/O or digest
+ * mismatch DL_RUNTIME_ERROR.  JSON metadata is read strictly: duplicate keys
+ * at any depth, nesting beyond 64 containers, nonfinite numbers and trailing
+ * text are rejected. */
+typedef struct dl_archive dl_archive;
+
+typedef struct dl_archive_limits { /* safetensors::HeaderLimits */
+  uint64_t max_header_bytes;
+  uint64_t max_metadata_bytes;
+  uint64_t max_tensor_count;
+} dl_archive_limits;
+
+typedef struct dl_artifact { /* formats::Artifact: a declared file of the archive */
+  const char* relative_path;   /* normalized, relative, inside the root */
+  uint64_t byte_size;
+  const char* sha256;          /* 64 hex characters */
+} dl_artifact;
+
+enum { DL_INTEGRITY_SHA256 = 0, DL_INTEGRITY_PREPARED = 1 };
+
+typedef struct dl_archive_request { /* safetensors::OpenRequest */
+  const char* root;
+  const char* repository;
+  const char* revision;
+  const dl_artifact* artifacts;
+  const char* const* shards;   /* declared artifacts holding tensors */
+  const char* index;           /* declared non-shard index artifact, or null */
+  uint64_t max_header_bytes;
+  uint64_t max_metadata_bytes;
+  uint64_t max_tensor_count;
+  uint32_t artifact_count;
+  uint32_t shard_count;
+  uint32_t verification_workers; /* 1..8 concurrent file hashes */
+  int32_t integrity;             /* DL_INTEGRITY_SHA256 or DL_INTEGRITY_PREPARED (sizes only) */
+} dl_archive_request;
+
+typedef struct dl_tensor_info {
+  const char* name;        /* owned by the archive */
+  const uint64_t* shape;   /* owned by the archive; `rank` entries */
+  const void* payload;     /* mapped host bytes, or null for a decoded header */
+  uint64_t data_offset;    /* within the shard's payload region */
+  uint64_t byte_count;
+  uint32_t rank;
+  int32_t dtype;           /* DL_BF16, DL_F32 or DL_U32 */
+} dl_tensor_info;
+
+/* safetensors::parse_header: decodes one header (the JSON alone, without the
+ * eight-byte prefix) against a payload region of `data_bytes`: unique names,
+ * BF16/F32/U32 types, shapes matching their byte ranges, and a complete,
+ * non-overlapping payload partition.  The result is a catalog without
+ * payloads, sorted by name; destroy it with dl_archive_destroy. */
+int dl_safetensors_parse_header(const char* json, uint64_t json_bytes, uint64_t data_bytes,
+                                const dl_archive_limits* limits, dl_archive** out);
+/* safetensors::open: maps every declared artifact (sizes checked, SHA-256
+ * checked unless DL_INTEGRITY_PREPARED), decodes each shard's header, checks
+ * the optional index's weight_map against the shards, and publishes the
+ * source identity {repository, revision, artifact digest v1}. */
+int dl_safetensors_open(const dl_archive_request* request, dl_archive** out);
+int dl_archive_destroy(dl_archive* archive);
+int dl_archive_tensor_count(const dl_archive* archive, uint64_t* count);
+int dl_archive_tensor_info(const dl_archive* archive, uint64_t index, dl_tensor_info* out);
+int dl_archive_find(const dl_archive* archive, const char* name, dl_tensor_info* out);
+int dl_archive_identity(const dl_archive* archive, const char** repository, const char** revision,
+                        const char** digest);
+int dl_archive_artifact(const dl_archive* archive, const char* path, const void** bytes, uint64_t* size);
+/* SHA-256 (FIPS 180-4) as 64 lowercase hex characters and a terminator. */
+int dl_sha256_hex(const void* data, uint64_t bytes, char* out);
+
+/* qwen3::parse_config (checkpoint.cpp): a Hugging Face Qwen3 config with the
+ * actual weight type (DL_BF16 or DL_F32); unknown behavioural settings, tied
+ * heads, biases, scaled RoPE and sliding windows are rejected.  `out` gets
+ * tied_embeddings 0; context_limit is max_position_embeddings. */
+int dl_qwen3_parse_config(const char* json, uint64_t json_bytes, int actual_weight_dtype,
+                          uint64_t max_metadata_bytes, dl_qwen3_config* out, uint64_t* context_limit);
+/* Serialized tensor name of a role (checkpoint.cpp:113-149). */
+int dl_qwen3_tensor_name(int role, uint32_t layer, char* out, uint64_t capacity);
+/* qwen3::bind_parameters: the catalog holds exactly the 3 + 11 L tensors of
+ * `config`, each with its dense shape and `weight_dtype`. */
+int dl_qwen3_bind_parameters(const dl_qwen3_config* config, int weight_dtype, const dl_archive* catalog);
+/* qwen3::bind_causal_lm without the upload: the configuration artifact
+ * parsed with the first tensor's type, then the parameter binding. */
+int dl_qwen3_bind_archive(const dl_archive* archive, const char* configuration_artifact, dl_qwen3_config* out,
+                          uint64_t* context_limit, uint64_t* parameter_bytes);
+/* Binds `archive` as bind_causal_lm does and uploads every parameter into
+ * `model`, whose config must equal the archive's (untied, BF16 weights: no
+ * type conversion).  Payloads stream from the mapped shards through bounded
+ * pinned staging into the packed resident layout. */
+int dl_qwen3_load(dl_qwen3* model, dl_queue* queue, const dl_archive* archive, const char* configuration_artifact);
 
 /* ---------------------------------------------------------------- the plan */
 /* A cached forward plan for `batch` (1..8) independent sequences sharing
