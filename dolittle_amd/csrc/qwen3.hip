@@ -247,8 +247,6 @@ __global__ __launch_bounds__(qkv_waves(B, Part) * 64) void k_qkv(QkvArgs a) {
   float* xs16 = lds;
   float* xs32 = Part == kQkvKV ? lds : xs16 + B * staged_floats(16, a.D);
   __shared__ float scratch[W * 40];
-  if (!a.ctl->active) return;
-  const uint64_t pos = a.ctl->position;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int q_tiles = a.QW / 4, k_tiles = a.KW / 2, total = q_tiles + 2 * k_tiles;
   const int S16 = a.D / 128, S32 = a.D / 256;
@@ -269,6 +267,10 @@ __global__ __launch_bounds__(qkv_waves(B, Part) * 64) void k_qkv(QkvArgs a) {
     if (first < tile_end) issue_first(tile_src(first), lane, fb);
   });
   __syncthreads();
+  // The loop state is read after the prologue's loads are in flight (the
+  // prologue writes nothing outside LDS); the flag is grid-uniform.
+  if (!a.ctl->active) return;
+  const uint64_t pos = a.ctl->position;
   for (int tile = first; tile < tile_end; tile += gridDim.x * W) {
     const bool is_q = tile < q_tiles;
     int kt = tile - q_tiles;
@@ -869,8 +871,6 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual(ResidualArgs a)
   constexpr int W = gemv_waves(B);
   extern __shared__ float xs[];
   __shared__ float epi[W * (64 / P) * B];
-  if (!a.ctl->active) return;
-  const uint64_t pos = a.ctl->position;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   constexpr int RW = 64 / P;
   const int tiles = a.D / RW;
@@ -882,6 +882,10 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual(ResidualArgs a)
     if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
   });
   __syncthreads();
+  // Read after the prologue's loads are in flight (grid-uniform flag; the
+  // prologue writes only LDS).
+  if (!a.ctl->active) return;
+  const uint64_t pos = a.ctl->position;
   const bool steer = a.steer != nullptr && a.layer == a.ctl->steer_layer;
   const bool capture = a.capture != nullptr && a.layer == a.ctl->capture_layer;
   const uint32_t steer_mask = a.ctl->steer_mask;
@@ -965,7 +969,6 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_gateup(GateUpArgs a) {
   extern __shared__ float xs[];
   __shared__ float scratch[W * 40];
   __shared__ float epi[W * 4 * B];
-  if (!a.ctl->active) return;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int tiles = a.F / 2;
   const int S = a.D / 128;
@@ -976,6 +979,9 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_gateup(GateUpArgs a) {
     if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
   });
   __syncthreads();
+  // Read after the prologue's loads are in flight (grid-uniform flag; the
+  // prologue writes only LDS).
+  if (!a.ctl->active) return;
   (void)S;
   for (int tile = first; tile < tiles; tile += gridDim.x * W) {
     float acc[B];
