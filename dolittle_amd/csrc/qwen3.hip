@@ -240,9 +240,15 @@ struct QkvArgs {
 enum QkvPart : int { kQkvAll = 0, kQkvQ = 1, kQkvKV = 2 };
 constexpr int qkv_waves(int rows, int part) { return part == kQkvAll ? kWaves : gemv_waves(rows); }
 
-template <int B, int Part = kQkvAll>
+// Split > 1 divides each tile's B rows into Split work items of B / Split
+// rows (the same tile's weights, read by Split wavefronts): with one tile
+// per wavefront the chain length per wavefront, not the CU count, bounds
+// these launches at eight rows.
+template <int B, int Part = kQkvAll, int Split = 1>
 __global__ __launch_bounds__(qkv_waves(B, Part) * 64) void k_qkv(QkvArgs a) {
   constexpr int W = qkv_waves(B, Part);
+  constexpr int BR = B / Split;
+  static_assert(B % Split == 0, "rows split evenly");
   extern __shared__ float lds[];
   float* xs16 = lds;
   float* xs32 = Part == kQkvKV ? lds : xs16 + B * staged_floats(16, a.D);
@@ -261,42 +267,44 @@ __global__ __launch_bounds__(qkv_waves(B, Part) * 64) void k_qkv(QkvArgs a) {
     return a.w + q_tiles * q_chunks + (is_v ? k_tiles : 0) * k_chunks + kt * k_chunks;
   };
   const int tile_begin = Part == kQkvKV ? q_tiles : 0, tile_end = Part == kQkvQ ? q_tiles : total;
-  const int first = tile_begin + blockIdx.x * W + wave;
+  const int items = (tile_end - tile_begin) * Split;
+  const int first = blockIdx.x * W + wave;
   FirstBatch fb{};
   norm_stage<B, Part != kQkvKV, Part != kQkvQ, W / 2>(a.h, a.norm, a.eps, xs16, xs32, scratch, [&] {
-    if (first < tile_end) issue_first(tile_src(first), lane, fb);
+    if (first < items) issue_first(tile_src(tile_begin + first / Split), lane, fb);
   });
   __syncthreads();
   // The loop state is read after the prologue's loads are in flight (the
   // prologue writes nothing outside LDS); the flag is grid-uniform.
   if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
-  for (int tile = first; tile < tile_end; tile += gridDim.x * W) {
+  for (int item = first; item < items; item += gridDim.x * W) {
+    const int tile = tile_begin + item / Split, b0 = (item % Split) * BR;
     const bool is_q = tile < q_tiles;
     int kt = tile - q_tiles;
     const bool is_v = !is_q && kt >= k_tiles;
     if (is_v) kt -= k_tiles;
     const u32x4* src = tile_src(tile);
-    const int next = tile + gridDim.x * W;
-    const u32x4* next_src = next < tile_end ? tile_src(next) : nullptr;
-    float acc[B];
+    const int next = item + gridDim.x * W;
+    const u32x4* next_src = next < items ? tile_src(tile_begin + next / Split) : nullptr;
+    float acc[BR];
     if (Part == kQkvQ || (Part == kQkvAll && is_q)) {
-      chain_tile<16, B>(src, xs16, a.D, lane, acc, &fb, next_src);
+      chain_tile<16, BR>(src, xs16 + b0 * staged_floats(16, a.D), a.D, lane, acc, &fb, next_src);
       if (lane % 16 == 0) {
         const int row = tile * 4 + lane / 16;
 #pragma unroll
-        for (int b = 0; b < B; ++b) a.q_out[b * a.QW + row] = bf16_bits(acc[b]);
+        for (int b = 0; b < BR; ++b) a.q_out[(b0 + b) * a.QW + row] = bf16_bits(acc[b]);
       }
     } else {
-      chain_tile<32, B>(src, xs32, a.D, lane, acc, &fb, next_src);
+      chain_tile<32, BR>(src, xs32 + b0 * staged_floats(32, a.D), a.D, lane, acc, &fb, next_src);
       if (lane % 32 == 0) {
         const int row = kt * 2 + lane / 32;
 #pragma unroll
-        for (int b = 0; b < B; ++b) {
+        for (int b = 0; b < BR; ++b) {
           if (is_v)
-            a.v_cache[b * a.cache_seq_stride + static_cast<uint64_t>(row) * a.cap + pos] = bf16_bits(acc[b]);
+            a.v_cache[(b0 + b) * a.cache_seq_stride + static_cast<uint64_t>(row) * a.cap + pos] = bf16_bits(acc[b]);
           else
-            a.k_out[b * a.KW + row] = bf16_bits(acc[b]);
+            a.k_out[(b0 + b) * a.KW + row] = bf16_bits(acc[b]);
         }
       }
     }
@@ -866,20 +874,24 @@ __device__ __forceinline__ void residual_outputs(const ResidualArgs& a, const fl
 
 // y = round(x W^T); h = round(h + y); optionally h = round(h + steer) and a
 // copy of h into the capture arena at the current position.
-template <int P, int B>
+// Split as in k_qkv: each tile's rows as Split work items of B / Split rows.
+template <int P, int B, int Split = 1>
 __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual(ResidualArgs a) {
   constexpr int W = gemv_waves(B);
+  constexpr int BR = B / Split;
+  static_assert(B % Split == 0, "rows split evenly");
   extern __shared__ float xs[];
-  __shared__ float epi[W * (64 / P) * B];
+  __shared__ float epi[W * (64 / P) * BR];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   constexpr int RW = 64 / P;
   const int tiles = a.D / RW;
+  const int items = tiles * Split;
   const int S = a.I / (8 * P);
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
   const int first = blockIdx.x * W + wave;
   FirstBatch fb{};
   stage_rows<P>(a.x + static_cast<uint64_t>(a.row0) * a.I, a.I, B, xs, [&] {
-    if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
+    if (first < items) issue_first(a.w + (first / Split) * chunks, lane, fb);
   });
   __syncthreads();
   // Read after the prologue's loads are in flight (grid-uniform flag; the
@@ -889,13 +901,21 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual(ResidualArgs a)
   const bool steer = a.steer != nullptr && a.layer == a.ctl->steer_layer;
   const bool capture = a.capture != nullptr && a.layer == a.ctl->capture_layer;
   const uint32_t steer_mask = a.ctl->steer_mask;
-  for (int tile = first; tile < tiles; tile += gridDim.x * W) {
-    float acc[B];
-    const int next = tile + gridDim.x * W;
+  for (int item = first; item < items; item += gridDim.x * W) {
+    const int tile = item / Split, b0 = (item % Split) * BR;
+    float acc[BR];
+    const int next = item + gridDim.x * W;
     // One tile per wavefront at B = 1 leaves one or two wavefronts per SIMD:
     // two batches in flight per wavefront keep more of HBM busy.
-    chain_tile<P, B, true>(a.w + tile * chunks, xs, a.I, lane, acc, &fb, next < tiles ? a.w + next * chunks : nullptr);
-    residual_outputs<P, B>(a, acc, tile, lane, epi + wave * RW * B, pos, steer, capture, steer_mask);
+    chain_tile<P, BR, true>(a.w + tile * chunks, xs + b0 * staged_floats(P, a.I), a.I, lane, acc, &fb,
+                            next < items ? a.w + (next / Split) * chunks : nullptr);
+    if constexpr (Split == 1) {
+      residual_outputs<P, BR>(a, acc, tile, lane, epi + wave * RW * BR, pos, steer, capture, steer_mask);
+    } else {
+      ResidualArgs part = a;
+      part.row0 += b0;
+      residual_outputs<P, BR>(part, acc, tile, lane, epi + wave * RW * BR, pos, steer, capture, steer_mask);
+    }
   }
 }
 
@@ -1907,14 +1927,14 @@ void prepare_kernels_all(dl_plan* p) {
   allow_lds(k_qkv<1>, qkv_lds(1, D));
   allow_lds(k_qkv<2>, qkv_lds(2, D));
   allow_lds(k_qkv<4>, qkv_lds(4, D));
-  allow_lds(k_qkv<8, kQkvQ>, qkv_lds(8, D, kQkvQ));
-  allow_lds(k_qkv<8, kQkvKV>, qkv_lds(8, D, kQkvKV));
+  allow_lds(k_qkv<8, kQkvQ, 2>, qkv_lds(8, D, kQkvQ));
+  allow_lds(k_qkv<8, kQkvKV, 2>, qkv_lds(8, D, kQkvKV));
   allow_lds(k_residual_chunked<32, 4>, p32_lds(4, kChunkInputs));
   allow_lds(k_residual_chunked<32, 8>, p32_lds(8, kChunkInputs));
   allow_lds(k_residual<16, 1>, p16_lds(1, QW));
   allow_lds(k_residual<16, 2>, p16_lds(2, QW));
   allow_lds(k_residual<16, 4>, p16_lds(4, QW));
-  allow_lds(k_residual<16, 8>, p16_lds(8, QW));
+  allow_lds(k_residual<16, 8, 2>, p16_lds(8, QW));
   allow_lds(k_gateup<1>, p16_lds(1, D));
   allow_lds(k_gateup<2>, p16_lds(2, D));
   allow_lds(k_gateup<4>, p16_lds(4, D));
@@ -1928,12 +1948,18 @@ void prepare_kernels_all(dl_plan* p) {
   allow_lds(k_attn_softmax, size_t(p->cap) * sizeof(float));
 }
 
+// Row groups per tile for launches with one tile per wavefront (O and the
+// split Q, K/V launches, 1024 tiles each): at eight rows two groups of four,
+// so 256 workgroups cover the chip and each chain is half as long.
+constexpr int kRowSplit(int rows, int one_tile_per_wave) { return rows == 8 && one_tile_per_wave ? 2 : 1; }
+
 template <int G, int Part = dl::kQkvAll>
 void launch_qkv(dl_plan* p, hipStream_t s, const dl::QkvArgs& a) {
   const uint64_t tiles = Part == dl::kQkvQ ? a.QW / 4 : Part == dl::kQkvKV ? a.KW : a.QW / 4 + a.KW;
   const size_t lds = qkv_lds(G, a.D, Part);
   constexpr int waves = dl::qkv_waves(G, Part);
-  dl::k_qkv<G, Part><<<p->grid_for(0, tiles, lds, waves), waves * 64, lds, s>>>(a);
+  constexpr int split = kRowSplit(G, Part == dl::kQkvAll ? 0 : 1);
+  dl::k_qkv<G, Part, split><<<p->grid_for(0, tiles * split, lds, waves), waves * 64, lds, s>>>(a);
 }
 template <int G>
 void launch_down_chunked(dl_plan* p, hipStream_t s, const dl::ResidualArgs& a) {
@@ -1944,8 +1970,9 @@ void launch_down_chunked(dl_plan* p, hipStream_t s, const dl::ResidualArgs& a) {
 template <int P, int G>
 void launch_residual(dl_plan* p, hipStream_t s, int which, const dl::ResidualArgs& a) {
   const size_t lds = P == 16 ? p16_lds(G, a.I) : p32_lds(G, a.I);
-  dl::k_residual<P, G><<<p->grid_for(which, a.D / (64 / P), lds, dl::gemv_waves(G)), dl::gemv_waves(G) * 64, lds,
-                         s>>>(a);
+  constexpr int split = kRowSplit(G, P == 16 ? 1 : 0);
+  dl::k_residual<P, G, split><<<p->grid_for(which, a.D / (64 / P) * split, lds, dl::gemv_waves(G)),
+                                dl::gemv_waves(G) * 64, lds, s>>>(a);
 }
 template <int G>
 void launch_gateup(dl_plan* p, hipStream_t s, const dl::GateUpArgs& a) {
