@@ -628,25 +628,38 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
   __shared__ float red[kAttnThreads];
   __shared__ float wave_max[kAttnThreads / 64];
   __shared__ float denominator_shared;
-  if (!a.ctl->active) return;
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const uint64_t pos = a.ctl->position + static_cast<uint64_t>(b) * a.pos_step;
-  const int count = static_cast<int>(pos) + 1;
   const int wave = tid / 64, lane = tid % 64;
   const int group = a.q_heads / a.kv_heads;
   const int g = h / group;
-  const float* rope_pos = a.rope + pos * kHeadDim;
   const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHeadDim, kw = static_cast<uint64_t>(a.kv_heads) * kHeadDim;
+  // This token's q/k rows and their norm gains do not depend on the loop
+  // state: they are issued before the control block is read, and the rope
+  // row of the position right after it.  Loads retire in order, so anything
+  // issued before them would delay the head norms.
+  HeadOperands head{};
+  if (wave < 2) {
+    const uint16_t* x = wave == 0 ? a.q_raw + b * qw + static_cast<uint64_t>(h) * kHeadDim
+                                  : a.k_raw + b * kw + static_cast<uint64_t>(g) * kHeadDim;
+    const uint16_t* gain = wave == 0 ? a.q_norm : a.k_norm;
+    head.xa = dl_bf16_to_f32(x[lane]);
+    head.xb = dl_bf16_to_f32(x[lane + 64]);
+    head.ga = dl_bf16_to_f32(gain[lane]);
+    head.gb = dl_bf16_to_f32(gain[lane + 64]);
+  }
+  if (!a.ctl->active) return;
+  const uint64_t pos = a.ctl->position + static_cast<uint64_t>(b) * a.pos_step;
+  const int count = static_cast<int>(pos) + 1;
+  const float* rope_pos = a.rope + pos * kHeadDim;
   uint16_t* kc = a.k_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g) * a.cap * kHeadDim;
+  if (wave < 2) {
+    head.cosine = rope_pos[2 * lane];
+    head.sine = rope_pos[2 * lane + 1];
+  }
 
   // Cached K rows and V blocks do not depend on this token: issue the first
   // kAttnKeyPasses passes of key rows and kAttnValueBlocks 8-key blocks of
   // each PV chain before the head norms, so their latency overlaps them.
-  // This token's q/k head operands go first: loads retire in order, so
-  // anything issued before them would delay the head norms.
-  HeadOperands head{};
-  if (wave == 0) head = head_load(a.q_raw + b * qw + static_cast<uint64_t>(h) * kHeadDim, a.q_norm, rope_pos, lane);
-  if (wave == 1) head = head_load(a.k_raw + b * kw + static_cast<uint64_t>(g) * kHeadDim, a.k_norm, rope_pos, lane);
   __builtin_amdgcn_sched_barrier(0);
   const int kg = tid / 8, l = tid % 8;
   u32x4 kpre[kAttnKeyPasses][2];
