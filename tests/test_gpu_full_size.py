@@ -111,3 +111,44 @@ def test_topp_batch_invariance_full_size(full_model):
         alone.generate(p, new, settings, seeds=[seeds[b]])
         got, _ = alone.collect()
         assert got[0].tolist() == tokens[b].tolist(), b
+
+
+def test_nla_steps_full_size(full_model, device, queue):
+    """The NLA steps around the block-24 capture at full size: a captured
+    row normalized by DeviceInjection (scale 150) replaces a prompt
+    embedding, and a one-row intervention at block 24 hits sequence 1 of a
+    batch of two.  Sequence 0 equals the plain batch-1 run, sequence 1 its
+    own batch-1 run with the same injection and intervention; the count is
+    one and no status is latched."""
+    from dolittle_amd.interventions import DeviceInjection, Region
+    from dolittle_amd.qwen3 import Plan
+    p, new, layer = prompt(6, 24), 6, 24
+    source = Plan(full_model, batch=1, capacity=64)
+    source.set_capture(layer)
+    source.generate(p, new)
+    source.collect()
+    row = source.read_capture(0, 10, 1).reshape(-1)
+    buf = device.upload_array(queue, row)
+    inj = DeviceInjection(device, queue, Region(buf, 0, row.nbytes), "bfloat16", "bfloat16", 4096, 150.0)
+    inj.submit()
+    u = np.random.default_rng(8).standard_normal(4096).astype(np.float32)
+    u = (u / np.float32(np.linalg.norm(u.astype(np.float64)))).astype(np.float32)
+
+    def run(batch, seq_mask, seq):
+        plan = Plan(full_model, batch=batch, capacity=64)
+        plan.set_injection(inj, 5, seq_mask)
+        plan.set_intervention(seq, layer, 12, u, 0.5)
+        plan.generate(p, new)
+        tokens, results = plan.collect()
+        assert all(r["status"] == 0 for r in results), results
+        assert plan.read_intervention() == (0, 1)
+        return tokens, plan
+
+    plain = Plan(full_model, batch=1, capacity=64)
+    plain.generate(p, new)
+    plain_tokens, _ = plain.collect()
+    alone, alone_plan = run(1, 1, 0)
+    both, both_plan = run(2, 0b10, 1)
+    assert both[0].tolist() == plain_tokens[0].tolist()
+    assert both[1].tolist() == alone[0].tolist()
+    assert np.array_equal(both_plan.logits(1), alone_plan.logits(0))
