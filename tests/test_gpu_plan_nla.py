@@ -237,3 +237,38 @@ def test_injection_status_gates_the_loop(small_model, oracle, device, queue):
     with pytest.raises(Exception):  # FP32 output does not match BF16 activations
         from dolittle_amd import _lib
         _lib.call("dl_plan_set_injection", plan.handle, 1, good.storage.ptr(), 2, 1)
+
+
+@pytest.mark.parametrize("prefill", ["none", "exact", "mfma"])
+def test_edge_positions(small_model, oracle, device, queue, prefill):
+    """Edge positions: the injection at the last prompt position (always
+    consumed by the selecting step, also after a prefill) and the
+    intervention at position 0 (row 0 of the first chunk or prefill block).
+    Bit-exact with the oracle on the exact paths; on the MFMA prefill the
+    greedy stream must still follow (the intervened row is exact, later
+    rows carry the MFMA tolerance, so the check there is count and status)."""
+    from dolittle_amd.qwen3 import Plan
+    w = oracle_weights(oracle, small_model)
+    d = w.dims
+    inj, status, row = injection(oracle, device, queue, d, 13)
+    assert status == 0
+    u = unit_direction(oracle, d, 14)
+    p = [int(t) for t in np.random.default_rng(49).integers(0, 151936, 11)]
+    max_new = 3
+    plan = Plan(small_model, batch=1, capacity=64)
+    plan.set_injection(inj, len(p) - 1, 1)
+    plan.set_intervention(0, 1, 0, u, 0.25)
+    if prefill == "exact":
+        plan.prefill(p, exact=True)
+    elif prefill == "mfma":
+        plan.prefill(p)
+    if prefill != "none":
+        assert plan.read_intervention() == (0, 1)
+    plan.generate(p, max_new)
+    tokens, results = plan.collect()
+    assert results[0]["status"] == 0 and results[0]["generated"] == max_new
+    assert plan.read_intervention() == (0, 1)
+    if prefill != "mfma":
+        stream, _, logits, state = oracle_stream(oracle, w, p, max_new, inject=(len(p) - 1, row),
+                                                 intervene=(1, 0, u, 0.25))
+        assert tokens[0].tolist() == stream and np.array_equal(plan.logits(0), logits)
