@@ -95,7 +95,7 @@ def other_configs(device, queue, model, cfg, seed, pplan, long_prompt):
         ea, eb = Event(device), Event(device)
         queue.drain()
         ea.record(queue)
-        pplan.prefill(long_prompt, exact=True)
+        pplan.prefill(long_prompt)
         eb.record(queue)
         queue.drain()
         exact_ms = ea.elapsed_ms(eb)
@@ -103,7 +103,7 @@ def other_configs(device, queue, model, cfg, seed, pplan, long_prompt):
                                         "tokens_per_s": round((n - 1) / (exact_ms * 1e-3), 1)}
         log(f"config 3: exact prefill of {n - 1} positions in {exact_ms:.1f} ms = "
             f"{(n - 1) / (exact_ms * 1e-3):.0f} tok/s")
-        pplan.prefill(long_prompt)
+        pplan.prefill(long_prompt, mfma=True)
         ms, _, _ = timed_loop(device, queue, pplan, long_prompt, max_new, 1)
         mean_ctx = n + 1 + (max_new - 2) / 2.0
         gbs = step_bytes(cfg, mean_ctx) / (ms * 1e-3) / 1e9
@@ -268,11 +268,11 @@ def main() -> int:
     capacity = args.prompt + max_new + 1
     plan = Plan(model, batch=1, capacity=capacity)
     prompt = np.random.default_rng(args.seed).integers(0, cfg.vocab, args.prompt).astype(np.uint32)
-    plan.prefill(prompt[:8], exact=True)  # warm (allocates the chunk buffers)
+    plan.prefill(prompt[:8])  # warm (allocates the chunk buffers)
     e_p0, e_p1, e_a, e_b = Event(device), Event(device), Event(device), Event(device)
     queue.drain()
     e_p0.record(queue)
-    plan.prefill(prompt, exact=True)  # exact prompt pass over positions [0, prompt - 1)
+    plan.prefill(prompt)  # exact prompt pass over positions [0, prompt - 1)
     e_p1.record(queue)
     queue.drain()
     plan.prepare_generation(prompt, max_new)  # resumes at the last prompt position
@@ -349,13 +349,13 @@ def main() -> int:
         n = args.mfma_prompt
         pplan = Plan(model, batch=1, capacity=n + 512 + 1)
         long_prompt = np.random.default_rng(args.seed + 3).integers(0, cfg.vocab, n).astype(np.uint32)
-        pplan.prefill(long_prompt)  # warm (allocates the row buffers)
+        pplan.prefill(long_prompt, mfma=True)  # warm (allocates the row buffers)
         queue.drain()
         runs = 3
         ea, eb = Event(device), Event(device)
         ea.record(queue)
         for _ in range(runs):
-            pplan.prefill(long_prompt)
+            pplan.prefill(long_prompt, mfma=True)
         eb.record(queue)
         queue.drain()
         ms = ea.elapsed_ms(eb) / runs

@@ -5,6 +5,7 @@ module raises at import of the first entry point that needs it.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
 import re
@@ -14,6 +15,23 @@ LIBRARY = os.path.join(HERE, "libdlhip.so")
 HEADER = os.path.join(HERE, "..", "include", "dolittle_hip.h")
 
 _lib = None
+_finalizing = False
+
+
+def _mark_finalizing() -> None:
+    global _finalizing
+    _finalizing = True
+
+
+atexit.register(_mark_finalizing)
+
+
+def releasing() -> bool:
+    """False once the interpreter is shutting down.  Objects still alive then
+    (for example held by a stored traceback) are finalized in no particular
+    order, so a plan could be destroyed after its queue; their destructors
+    leave native handles to the process exit instead."""
+    return not _finalizing
 
 u8p = C.POINTER(C.c_uint8)
 u16p = C.POINTER(C.c_uint16)

@@ -97,6 +97,8 @@ class Archive:
             self.handle = None
 
     def __del__(self):
+        if not _lib.releasing():
+            return
         try:
             self.close()
         except Exception:

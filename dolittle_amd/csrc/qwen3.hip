@@ -2428,6 +2428,8 @@ int dl_plan_set_capture(dl_plan* plan, int32_t layer) {
       dl::check_hip(hipStreamSynchronize(plan->queue->stream), "capture setup");
       plan->capture_step();
     }
+    // A prefilled prompt wrote no capture rows for a layer chosen after it.
+    if (layer != plan->capture_layer) plan->prefilled = 0;
     plan->capture_layer = layer;
   });
 }
@@ -2437,7 +2439,8 @@ int dl_plan_read_capture(dl_plan* plan, uint32_t seq, uint64_t first_position, u
     require(plan && host, "null argument");
     require(plan->capture != nullptr, "capture is not enabled");
     require(seq < plan->batch, "sequence out of range");
-    require(first_position + count <= plan->cap, "capture range outside the cache", DL_LENGTH_ERROR);
+    require(count <= plan->cap && first_position <= plan->cap - count, "capture range outside the cache",
+            DL_LENGTH_ERROR);
     dl::enter(plan->queue);
     const uint64_t D = plan->model->cfg.hidden;
     dl::check_hip(hipMemcpyAsync(host, plan->capture + (uint64_t(seq) * plan->cap + first_position) * D,
@@ -2453,6 +2456,8 @@ int dl_plan_set_steering(dl_plan* plan, uint32_t seq, int32_t layer, const float
     require(seq < plan->batch, "sequence out of range");
     dl::enter(plan->queue);
     const auto& c = plan->model->cfg;
+    // A prefilled prompt's caches hold the steering state of its pass.
+    plan->prefilled = 0;
     if (!vector) {
       plan->steer_mask &= ~(1u << seq);
       return;
@@ -2486,6 +2491,8 @@ int dl_plan_set_embedding_override(dl_plan* plan, uint64_t position, const uint1
     require(plan != nullptr, "null plan");
     dl::enter(plan->queue);
     clear_injection(plan);
+    // A prefilled prompt's caches hold the embedding rows of its pass.
+    plan->prefilled = 0;
     if (!row || seq_mask == 0) {
       plan->override_active = false;
       return;
@@ -2580,7 +2587,8 @@ static int cache_transfer(dl_plan* plan, uint32_t seq, uint32_t layer, uint64_t 
     dl::enter(plan->queue);
     const auto& c = plan->model->cfg;
     require(seq < plan->batch && layer < c.layers, "sequence or layer out of range");
-    require(count > 0 && first + count <= plan->capacity, "cache rows outside the capacity", DL_LENGTH_ERROR);
+    require(count > 0 && count <= plan->capacity && first <= plan->capacity - count,
+            "cache rows outside the capacity", DL_LENGTH_ERROR);
     const uint64_t elements = count * c.kv_heads * c.head_dim;
     void* tk = nullptr;
     void* tv = nullptr;
@@ -3011,8 +3019,14 @@ int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt
 
 
 int dl_plan_read_prefill_hidden(dl_plan* plan, uint64_t first_row, uint64_t count, uint16_t* host) {
-  return dl_plan_read_prefill_buffer(plan, 0, first_row * plan->model->cfg.hidden,
-                                     count * plan->model->cfg.hidden, host);
+  uint64_t D = 0;
+  const int status = guard([&] {
+    require(plan && host, "null argument");
+    D = plan->model->cfg.hidden;
+    require(count <= plan->pf.rows && first_row <= plan->pf.rows - count, "no prefill rows", DL_LENGTH_ERROR);
+  });
+  if (status != DL_OK) return status;
+  return dl_plan_read_prefill_buffer(plan, 0, first_row * D, count * D, host);
 }
 
 int dl_plan_read_prefill_buffer(dl_plan* plan, uint32_t which, uint64_t first, uint64_t count, uint16_t* host) {
@@ -3026,7 +3040,8 @@ int dl_plan_read_prefill_buffer(dl_plan* plan, uint32_t which, uint64_t first, u
                                plan->pf.k, plan->pf.q_rot, plan->pf.att, plan->pf.act};
     const uint64_t sizes[8] = {R * D, R * D, R * D, R * QW, R * KW, R * QW, R * QW, R * F};
     require(which < 8, "unknown prefill buffer");
-    require(bufs[which] != nullptr && first + count <= sizes[which], "no prefill rows", DL_LENGTH_ERROR);
+    require(bufs[which] != nullptr && count <= sizes[which] && first <= sizes[which] - count, "no prefill rows",
+            DL_LENGTH_ERROR);
     dl::check_hip(hipMemcpyAsync(host, bufs[which] + first, count * 2, hipMemcpyDeviceToHost, plan->queue->stream),
                   "read prefill buffer");
     dl::check_hip(hipStreamSynchronize(plan->queue->stream), "read prefill buffer wait");

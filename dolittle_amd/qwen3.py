@@ -100,6 +100,8 @@ class Qwen3Model:
         return n.value
 
     def __del__(self):
+        if not _lib.releasing():
+            return
         try:
             _lib.call("dl_qwen3_destroy", self.handle)
         except Exception:
@@ -239,13 +241,19 @@ class Plan:
                   C.byref(s), seeds_a.ctypes.data_as(_lib.u64p), stops.ctypes.data_as(_lib.u32p), n)
         self.max_new = max_new
 
-    def prefill(self, prompt, exact: bool = False) -> None:
+    def prefill(self, prompt, mfma: bool = False) -> None:
         """Prompt pass over positions [0, len(prompt) - 1); a following
         generate() with the same prompt resumes at the last prompt position.
-        exact=False runs the MFMA GEMM path (tolerance), exact=True the
-        chunked exact path (caches bit-identical to the token loop's)."""
+
+        The default is the chunked exact pass: its caches, logits and tokens
+        are bit-identical to consuming the prompt one position per step.
+        mfma=True opts into the MFMA GEMM pass, a tolerance path: the MFMA
+        units accumulate in their own order, so one projection is within one
+        BF16 ulp of the exact chain and the flips compound over the blocks
+        (at 36 Qwen3-8B blocks the first logits move by a few tenths and a
+        greedy stream can leave the exact one after a few tokens)."""
         p = np.ascontiguousarray(prompt, dtype=np.uint32)
-        _lib.call("dl_plan_prefill_exact" if exact else "dl_plan_prefill", self.handle,
+        _lib.call("dl_plan_prefill" if mfma else "dl_plan_prefill_exact", self.handle,
                   p.ctypes.data_as(_lib.u32p), p.size)
 
     def decode_steps(self, steps: int) -> None:
@@ -266,6 +274,8 @@ class Plan:
         _lib.call("dl_plan_request_stop", self.handle)
 
     def __del__(self):
+        if not _lib.releasing():
+            return
         try:
             _lib.call("dl_plan_destroy", self.handle)
         except Exception:

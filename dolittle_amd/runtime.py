@@ -40,6 +40,8 @@ class DeviceBuffer:
             self.handle = None
 
     def __del__(self):
+        if not _lib.releasing():
+            return
         try:
             self.free()
         except Exception:
@@ -72,6 +74,8 @@ class Event:
         return float(ms.value)
 
     def __del__(self):
+        if not _lib.releasing():
+            return
         try:
             _lib.call("dl_event_destroy", self.handle)
         except Exception:
@@ -117,6 +121,8 @@ class Queue:
         _lib.call("dl_queue_drain", self.handle)
 
     def __del__(self):
+        if not _lib.releasing():
+            return
         try:
             _lib.call("dl_queue_destroy", self.handle)
         except Exception:

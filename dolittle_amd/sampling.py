@@ -104,6 +104,8 @@ class DeviceCategorical:
             self.handle = None
 
     def __del__(self):
+        if not _lib.releasing():
+            return
         try:
             self.close()
         except Exception:

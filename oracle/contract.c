@@ -7,7 +7,7 @@
  * this build are required to reproduce these bits exactly.  Only the
  * transcendental kernels are shared with the product (dl_math.h): the
  * reference leaves them to the platform library, and the shared versions are
- * pinned against glibc by tests/test_oracle_math.py.
+ * pinned against glibc by tests/test_oracle_kat.py (the math cases).
  *
  * Compile with -ffp-contract=off: every FMA below is an explicit fmaf().
  */
@@ -64,6 +64,30 @@ void or_set_threads(int threads) {
     for (int off = P / 2; off; off >>= 1)                                            \
       for (int t = 0; t < off; ++t) acc[t] = acc[t] + acc[t + off];                  \
     return acc[0];                                                                   \
+  }                                                                                  \
+  /* Four output rows' chains side by side: each acc[i][t] is the same       */      \
+  /* chain as chain_P on row i (same operands, same order); the rows are     */      \
+  /* interleaved only so that independent FMAs overlap on the CPU.           */      \
+  static void chain4_##P(const float* x, const float* w, size_t in_w, float* out) {  \
+    float acc[4][P];                                                                 \
+    for (int i = 0; i < 4; ++i)                                                      \
+      for (int t = 0; t < P; ++t) acc[i][t] = 0.0f;                                  \
+    const size_t full = in_w / P * P;                                                \
+    for (size_t base = 0; base < full; base += P)                                    \
+      for (int i = 0; i < 4; ++i)                                                    \
+        for (int t = 0; t < P; ++t)                                                  \
+          acc[i][t] = fmaf(x[base + t], w[i * in_w + base + t], acc[i][t]);          \
+    for (int i = 0; i < 4; ++i) {                                                    \
+      for (size_t t = 0; t < in_w - full; ++t)                                       \
+        acc[i][t] = fmaf(x[full + t], w[i * in_w + full + t], acc[i][t]);            \
+      const size_t padded = (in_w + 15) / 16 * 16;                                   \
+      if (padded != in_w) {                                                          \
+        for (size_t t = in_w % P; t < (padded - 1) % P + 1; ++t) acc[i][t] = fmaf(0.0f, 0.0f, acc[i][t]); \
+      }                                                                              \
+      for (int off = P / 2; off; off >>= 1)                                          \
+        for (int t = 0; t < off; ++t) acc[i][t] = acc[i][t] + acc[i][t + off];       \
+      out[i] = acc[i][0];                                                            \
+    }                                                                                \
   }
 DEFINE_CHAIN(16)
 DEFINE_CHAIN(32)
@@ -77,16 +101,33 @@ void orc_projection(const uint16_t* x, const uint16_t* w, uint16_t* y, size_t ro
   const int P = projection_partials(in_w, out_w);
   float* xf = (float*)malloc(rows * in_w * sizeof(float));
   for (size_t i = 0; i < rows * in_w; ++i) xf[i] = or_f32_from_bf16(x[i]);
+  const long groups = (long)((out_w + 3) / 4);
 #pragma omp parallel
   {
-    float* wf = (float*)malloc(in_w * sizeof(float));
+    float* wf = (float*)malloc(4 * in_w * sizeof(float));
 #pragma omp for schedule(static)
-    for (long o = 0; o < (long)out_w; ++o) {
-      const uint16_t* wr = w + (size_t)o * in_w;
-      for (size_t i = 0; i < in_w; ++i) wf[i] = or_f32_from_bf16(wr[i]);
+    for (long gi = 0; gi < groups; ++gi) {
+      const size_t o0 = (size_t)gi * 4;
+      const size_t n = out_w - o0 < 4 ? out_w - o0 : 4;
+      for (size_t i = 0; i < n; ++i) {
+        const uint16_t* wr = w + (o0 + i) * in_w;
+        for (size_t k = 0; k < in_w; ++k) wf[i * in_w + k] = or_f32_from_bf16(wr[k]);
+      }
       for (size_t r = 0; r < rows; ++r) {
-        const float s = P == 16 ? chain_16(xf + r * in_w, wf, in_w) : chain_32(xf + r * in_w, wf, in_w);
-        y[r * out_w + (size_t)o] = or_bf16_from_f32(s);
+        const float* xr = xf + r * in_w;
+        if (n == 4) {
+          float s[4];
+          if (P == 16)
+            chain4_16(xr, wf, in_w, s);
+          else
+            chain4_32(xr, wf, in_w, s);
+          for (size_t i = 0; i < 4; ++i) y[r * out_w + o0 + i] = or_bf16_from_f32(s[i]);
+        } else {
+          for (size_t i = 0; i < n; ++i) {
+            const float s = P == 16 ? chain_16(xr, wf + i * in_w, in_w) : chain_32(xr, wf + i * in_w, in_w);
+            y[r * out_w + o0 + i] = or_bf16_from_f32(s);
+          }
+        }
       }
     }
     free(wf);
@@ -244,14 +285,20 @@ void orc_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint
     for (size_t j = 0; j < count; ++j) scores[j] = scores[j] / l;
     const size_t split = (count - 1) / 2 + 1;
     uint16_t* yr = y + (p * q_heads + h) * width;
-    for (size_t f = 0; f < width; ++f) {
-      float first = 0.0f, second = 0.0f;
-      for (size_t j = 0; j < split; ++j)
-        first = fmaf(scores[j], or_f32_from_bf16(v[j * pos_stride + g * head_stride + f]), first);
-      for (size_t j = split; j < count; ++j)
-        second = fmaf(scores[j], or_f32_from_bf16(v[j * pos_stride + g * head_stride + f]), second);
-      yr[f] = or_bf16_from_f32(first + second);
+    /* Feature f's two chains: first over keys [0, split), second over
+     * [split, count), each in ascending key order.  The key loop is outside
+     * the feature loop only so that the width chains advance side by side. */
+    float* first = (float*)calloc(width, sizeof(float));
+    float* second = (float*)calloc(width, sizeof(float));
+    for (size_t j = 0; j < count; ++j) {
+      const uint16_t* vr = v + j * pos_stride + g * head_stride;
+      float* acc = j < split ? first : second;
+      const float pj = scores[j];
+      for (size_t f = 0; f < width; ++f) acc[f] = fmaf(pj, or_f32_from_bf16(vr[f]), acc[f]);
     }
+    for (size_t f = 0; f < width; ++f) yr[f] = or_bf16_from_f32(first[f] + second[f]);
+    free(first);
+    free(second);
     free(qf);
     free(scores);
   }

@@ -1,0 +1,184 @@
+"""Full-depth parity of BASELINE configs 2 and 3 against the CPU oracle.
+
+- Config 2 at its real depth: Qwen3-8B (36 blocks, tied 151,936-row head,
+  seeded N(0, 0.02) BF16 weights), a 128-id seeded prompt and 64 greedy
+  tokens.  The token stream and the last selection's logits are bit-exact
+  with the oracle, both when the loop consumes the prompt one position per
+  step and after the exact chunked prompt pass (the bench's path).  This is
+  the north star's "greedy token streams identical for the first 64 tokens"
+  at full size.
+- Config 3's 4096-id prompt at 2 blocks against the oracle: the exact
+  chunked prompt pass is bit-exact (caches, logits, tokens); the MFMA
+  prefill is held to the north star's logits bound (2e-2 absolute + 1e-2
+  relative, every logit), which it misses (an expected failure, below).
+- Config 3 at 36 blocks: the MFMA prefill's first logits against the
+  oracle-pinned exact pass, reported against the north star's bound and
+  asserted against the reference's own 36-block acceptance budget
+  (scripts/validation/README.md:128-142: max |d| <= max(1e-4, peak / 16),
+  relative L2 <= 0.03), which it misses on relative L2 (an expected
+  failure); and greedy decode grown to 4608 keys, where the
+  exact prompt pass then 512 tokens equals consuming all 4096 prompt ids
+  through the loop (tokens, logits, caches of blocks 0, 24, 35).
+"""
+import numpy as np
+import pytest
+
+from parity_helpers import OracleLoop, logit_errors, read_weights
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow]
+
+SEED = 20261201
+
+
+def prompt(seed, n):
+    return [int(t) for t in np.random.default_rng(seed).integers(0, 151936, n)]
+
+
+@pytest.fixture(scope="module")
+def full_model(device, queue):
+    from dolittle_amd.qwen3 import Qwen3Config, Qwen3Model
+    model = Qwen3Model(device, queue, Qwen3Config())
+    model.fill_synthetic(SEED, 0.02)
+    return model
+
+
+@pytest.mark.timeout(900)
+def test_config2_full_depth_matches_oracle(full_model, oracle):
+    from dolittle_amd.qwen3 import Plan
+    p, new = prompt(128, 128), 64
+    loop = Plan(full_model, batch=1, capacity=len(p) + new + 1)
+    loop.generate(p, new)
+    loop_tokens, results = loop.collect()
+    assert results[0]["generated"] == new and results[0]["status"] == 0
+    pre = Plan(full_model, batch=1, capacity=len(p) + new + 1)
+    pre.prefill(p)
+    pre.generate(p, new)
+    pre_tokens, pre_results = pre.collect()
+    assert pre_results[0]["generated"] == new and pre_results[0]["status"] == 0
+
+    w = read_weights(oracle, full_model, seed=SEED)
+    run = OracleLoop(oracle, w, len(p) + new + 1)
+    want_tokens, want_logits = run.generate(p, new)
+    assert loop_tokens[0].tolist() == want_tokens
+    assert np.array_equal(loop.logits(0), want_logits)
+    assert pre_tokens[0].tolist() == want_tokens
+    assert np.array_equal(pre.logits(0), want_logits)
+    for layer in (0, 35):
+        k, v = pre.read_cache(layer, 0, len(p) + new - 1)
+        wk, wv = run.cache_rows(layer, len(p) + new - 1)
+        assert np.array_equal(k, wk) and np.array_equal(v, wv), layer
+
+
+@pytest.fixture(scope="module")
+def two_blocks(device, queue):
+    from dolittle_amd.qwen3 import Qwen3Config, Qwen3Model
+    model = Qwen3Model(device, queue, Qwen3Config(layers=2))
+    model.fill_synthetic(SEED + 3, 0.02)
+    return model
+
+
+@pytest.fixture(scope="module")
+def config3_oracle(two_blocks, oracle):
+    """The oracle over config 3's 4096-id prompt at 2 blocks: the prompt
+    positions before the last as one chunk, then 4 greedy steps."""
+    p, new = prompt(4096, 4096), 4
+    w = read_weights(oracle, two_blocks, seed=SEED + 3)
+    run = OracleLoop(oracle, w, len(p) + new + 1)
+    run.prompt(p[:-1])
+    first_logits = None
+    seq, tokens, logits = list(p), [], None
+    for position in range(len(p) - 1, len(p) - 1 + new):
+        logits = run.step(seq[position], position)
+        first_logits = logits if first_logits is None else first_logits
+        status, token = oracle.greedy(logits)
+        assert status == 0
+        tokens.append(token)
+        seq.append(token)
+    return p, new, run, tokens, first_logits, logits
+
+
+@pytest.mark.timeout(900)
+def test_config3_exact_prefill_4096_two_blocks_matches_oracle(two_blocks, config3_oracle):
+    from dolittle_amd.qwen3 import Plan
+    p, new, run, tokens, _, logits = config3_oracle
+    plan = Plan(two_blocks, batch=1, capacity=len(p) + new + 1)
+    plan.prefill(p)
+    plan.generate(p, new)
+    got, results = plan.collect()
+    assert results[0]["generated"] == new and results[0]["status"] == 0
+    assert got[0].tolist() == tokens
+    assert np.array_equal(plan.logits(0), logits)
+    for layer in (0, 1):
+        k, v = plan.read_cache(layer, 0, len(p) + new - 1)
+        wk, wv = run.cache_rows(layer, len(p) + new - 1)
+        assert np.array_equal(k, wk) and np.array_equal(v, wv), layer
+
+
+# The MFMA prefill is the tolerance path and does not meet the north star's
+# logits bound on this synthetic model (measured on MI355X: 99.5% of the
+# 151,936 logits inside 2e-2 + 1e-2 |x| at 2 blocks, max |d| 0.047); the
+# assertion is kept as stated and the test is an expected failure: config 3's
+# parity path is the exact prompt pass
+# (test_config3_exact_prefill_4096_two_blocks_matches_oracle).  strict: a
+# pass would report as a failure, so a change that meets the bound shows.
+MFMA_MISSES_NORTH_STAR = pytest.mark.xfail(
+    strict=True, reason="MFMA accumulation order: the tolerance prefill misses the north star's logits bound; "
+                        "the exact prompt pass is config 3's parity path")
+
+
+@MFMA_MISSES_NORTH_STAR
+@pytest.mark.timeout(900)
+def test_config3_mfma_prefill_4096_two_blocks_north_star_bound(two_blocks, config3_oracle, oracle):
+    from dolittle_amd.qwen3 import Plan
+    p, _, _, _, first_logits, _ = config3_oracle
+    plan = Plan(two_blocks, batch=1, capacity=len(p) + 2)
+    plan.prefill(p, mfma=True)
+    plan.generate(p, 1)
+    plan.collect()
+    e = logit_errors(plan.logits(0), first_logits, oracle)
+    print(f"MFMA prefill, 4096 ids, 2 blocks, first logits vs oracle: {e}")
+    assert e["north_star_frac"] == 1.0, e
+
+
+# At 36 blocks (measured on MI355X: max |d| 0.25 within peak / 16 = 0.377,
+# relative L2 0.040 above 0.03) the MFMA prefill also misses the reference's
+# own 36-block acceptance budget; expected failure, assertion unchanged.
+@pytest.mark.xfail(strict=True, reason="MFMA prefill: relative L2 0.040 against the exact pass at 36 blocks "
+                                       "exceeds the reference's 0.03 budget")
+@pytest.mark.timeout(900)
+def test_config3_mfma_prefill_full_depth_against_exact(full_model, oracle):
+    from dolittle_amd.qwen3 import Plan
+    p = prompt(4097, 4096)
+    exact = Plan(full_model, batch=1, capacity=len(p) + 2)
+    exact.prefill(p)
+    exact.generate(p, 1)
+    exact.collect()
+    mfma = Plan(full_model, batch=1, capacity=len(p) + 2)
+    mfma.prefill(p, mfma=True)
+    mfma.generate(p, 1)
+    mfma.collect()
+    e = logit_errors(mfma.logits(0), exact.logits(0), oracle)
+    print(f"MFMA prefill, 4096 ids, 36 blocks, first logits vs the exact pass: {e}")
+    assert e["max_abs"] <= max(1e-4, e["peak"] * 0.0625) and e["rel_l2"] <= 0.03, e
+
+
+@pytest.mark.timeout(900)
+def test_config3_decode_to_4608_keys_exact_prefill_equals_loop(full_model):
+    from dolittle_amd.qwen3 import Plan
+    p, new = prompt(4098, 4096), 512
+    loop = Plan(full_model, batch=1, capacity=len(p) + new)
+    loop.generate(p, new)
+    want, results = loop.collect()
+    assert results[0]["generated"] == new and results[0]["status"] == 0
+    assert results[0]["position"] == len(p) + new
+    pre = Plan(full_model, batch=1, capacity=len(p) + new)
+    pre.prefill(p)
+    pre.generate(p, new)
+    got, results = pre.collect()
+    assert results[0]["generated"] == new and results[0]["status"] == 0
+    assert got[0].tolist() == want[0].tolist()
+    assert np.array_equal(pre.logits(0), loop.logits(0))
+    for layer in (0, 24, 35):
+        k0, v0 = loop.read_cache(layer, 0, len(p) + new - 1)
+        k1, v1 = pre.read_cache(layer, 0, len(p) + new - 1)
+        assert np.array_equal(k0, k1) and np.array_equal(v0, v1), layer

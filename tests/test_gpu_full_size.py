@@ -85,7 +85,7 @@ def test_exact_prefill_equals_token_loop_full_size(full_model):
     loop.generate(p, new)
     want, _ = loop.collect()
     pre = Plan(full_model, batch=1, capacity=640)
-    pre.prefill(p, exact=True)
+    pre.prefill(p)
     pre.generate(p, new)
     got, results = pre.collect()
     assert results[0]["status"] == 0 and got[0].tolist() == want[0].tolist()

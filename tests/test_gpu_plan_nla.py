@@ -71,7 +71,7 @@ def test_intervention_matches_oracle(small_model, oracle, exact_prefill):
     plan.set_capture(layer)
     plan.set_intervention(1, layer, position, u, strength)
     if exact_prefill:
-        plan.prefill(prompt, exact=True)
+        plan.prefill(prompt)
         assert plan.read_intervention() == (0, 1)
     plan.generate(prompt, max_new)
     tokens, results = plan.collect()
@@ -128,10 +128,10 @@ def test_intervention_on_mfma_prefill(small_model, oracle):
     prompt = [int(t) for t in rng.integers(0, 151936, 24)]
     plan = Plan(small_model, batch=1, capacity=64)
     plan.set_capture(layer)
-    plan.prefill(prompt)
+    plan.prefill(prompt, mfma=True)
     before = plan.read_capture(0, 0, position + 1)
     plan.set_intervention(0, layer, position, u, strength)
-    plan.prefill(prompt)
+    plan.prefill(prompt, mfma=True)
     after = plan.read_capture(0, 0, position + 1)
     assert plan.read_intervention() == (0, 1)
     assert np.array_equal(after[:position], before[:position])
@@ -199,7 +199,7 @@ def test_injection_matches_oracle(small_model, oracle, device, queue, exact_pref
     plan = Plan(small_model, batch=2, capacity=64)
     plan.set_injection(inj, 3, seq_mask=0b10)
     if exact_prefill:
-        plan.prefill(prompt, exact=True)
+        plan.prefill(prompt)
     plan.generate(prompt, max_new)
     tokens, results = plan.collect()
     for seq in (0, 1):
@@ -259,9 +259,9 @@ def test_edge_positions(small_model, oracle, device, queue, prefill):
     plan.set_injection(inj, len(p) - 1, 1)
     plan.set_intervention(0, 1, 0, u, 0.25)
     if prefill == "exact":
-        plan.prefill(p, exact=True)
-    elif prefill == "mfma":
         plan.prefill(p)
+    elif prefill == "mfma":
+        plan.prefill(p, mfma=True)
     if prefill != "none":
         assert plan.read_intervention() == (0, 1)
     plan.generate(p, max_new)

@@ -100,7 +100,7 @@ def test_prefill_cache_and_first_logits_within_tolerance(prefill_model, oracle):
     n = 300
     prompt = [int(t) for t in np.random.default_rng(31).integers(0, cfg.vocab, n)]
     plan = Plan(prefill_model, batch=1, capacity=320)
-    plan.prefill(prompt)
+    plan.prefill(prompt, mfma=True)
     plan.generate(prompt, 1)
     tokens, results = plan.collect()
     assert results[0]["generated"] == 1 and results[0]["position"] == n + 1
@@ -162,7 +162,7 @@ def test_prefill_then_decode_continues(prefill_model):
     from dolittle_amd.qwen3 import Plan
     prompt = list(range(1000, 1000 + 130))
     plan = Plan(prefill_model, batch=2, capacity=160)
-    plan.prefill(prompt)
+    plan.prefill(prompt, mfma=True)
     plan.generate(prompt, 6)
     t1, res = plan.collect()
     assert all(r["generated"] == 6 and r["position"] == 136 for r in res)

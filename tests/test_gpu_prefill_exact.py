@@ -44,7 +44,7 @@ def run_pair(model, prompt, max_new, batch=1, capacity=64, setup=None, sampling=
         if setup:
             setup(plan)
         if exact:
-            plan.prefill(prompt, exact=True)
+            plan.prefill(prompt)
         plan.generate(prompt, max_new, sampling, seeds)
         tokens, results = plan.collect()
         out.append((tokens, results, plan))
@@ -110,3 +110,66 @@ def test_exact_prefill_with_embedding_override(model2):
     a, b = run_pair(model2, prompt, 4, batch=2, capacity=32,
                     setup=lambda plan: plan.set_embedding_override(6, bits, 0b10))
     assert_same(model2, a, b, 18, batch=2)
+
+
+@pytest.mark.parametrize("change", ["steering", "capture", "override"])
+def test_hooks_set_after_a_prefill_are_not_skipped(model2, change):
+    """A prefill followed by a hook change (steering of sequence 1, a capture
+    layer, an embedding override) and then generate() with the same prompt
+    must not resume over caches built without the hook: the result equals a
+    plan that never prefilled, captures included."""
+    from dolittle_amd.qwen3 import Plan
+    p = [int(t) for t in np.random.default_rng(61).integers(0, 151936, 20)]
+    new, layer = 4, 1
+    v = np.random.default_rng(62).standard_normal(4096).astype(np.float32)
+    row = np.random.default_rng(63).integers(0, 1 << 14, 4096).astype(np.uint16)
+
+    def hook(plan):
+        if change == "steering":
+            plan.set_steering(1, layer, v)
+        elif change == "capture":
+            plan.set_capture(layer)
+        else:
+            plan.set_embedding_override(7, row, 0b10)
+
+    out = []
+    for prefill in (True, False):
+        plan = Plan(model2, batch=2, capacity=32)
+        if prefill:
+            plan.prefill(p)
+        hook(plan)
+        plan.generate(p, new)
+        tokens, results = plan.collect()
+        out.append((tokens, results, plan))
+    (ta, ra, pa), (tb, rb, pb) = out
+    assert ta.tolist() == tb.tolist()
+    for s in range(2):
+        assert np.array_equal(pa.logits(s), pb.logits(s)), s
+        assert ra[s]["position"] == rb[s]["position"] == len(p) + new
+    if change == "capture":
+        for s in range(2):
+            assert np.array_equal(pa.read_capture(s, 0, len(p) + new), pb.read_capture(s, 0, len(p) + new))
+    else:
+        # The hook reached sequence 1 only.
+        assert ta[0].tolist() != ta[1].tolist() or not np.array_equal(pa.logits(0), pa.logits(1))
+
+
+def test_wrapped_ranges_are_length_errors(model2):
+    """A first position near 2^64 with a small count wraps first + count
+    around; the range checks reject it before any copy or launch."""
+    from dolittle_amd import _lib
+    from dolittle_amd.qwen3 import Plan
+    plan = Plan(model2, batch=1, capacity=32)
+    plan.set_capture(0)
+    huge = (1 << 64) - 2
+    buf = np.zeros(4 * 1024 * 4, np.uint16)
+    ptr = buf.ctypes.data_as(_lib.u16p)
+    with pytest.raises(_lib.LengthError):
+        _lib.call("dl_plan_read_cache", plan.handle, 0, 0, huge, 4, ptr, ptr)
+    with pytest.raises(_lib.LengthError):
+        _lib.call("dl_plan_write_cache", plan.handle, 0, 0, huge, 4, ptr, ptr)
+    with pytest.raises(_lib.LengthError):
+        _lib.call("dl_plan_read_capture", plan.handle, 0, huge, 4, ptr)
+    plan.prefill([1, 2, 3, 4, 5])
+    with pytest.raises(_lib.LengthError):
+        _lib.call("dl_plan_read_prefill_hidden", plan.handle, huge, 4, ptr)
