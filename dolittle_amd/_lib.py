@@ -178,6 +178,7 @@ SIGNATURES = {
     "dl_sampler_result": [vp, u32p, u32p],
     "dl_sampler_set_exact": [vp, cint],
     "dl_sampler_exact_replays": [vp, C.POINTER(u64)],
+    "dl_sample_noalloc": [vp, vp, u64, u64, C.POINTER(Sampling), u64, u32p],
     "dl_injection_bytes": [u64, cint, u64p],
     "dl_injection_submit": [vp, vp, cint, cint, u64, C.c_float, vp],
     "dl_direction_bytes": [u64, u64p],

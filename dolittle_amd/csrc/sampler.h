@@ -98,6 +98,7 @@ struct RowsArgs {
   int loop_rng;            // draw from each row's stream inside the selection
   int exact;               // always decide by the serial replay (diagnostic)
   LoopOutput loop;
+  Result* result_out;      // standalone: the caller's {token, status} instead of the row state's
 };
 
 struct Seeds {

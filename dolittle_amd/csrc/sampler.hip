@@ -24,6 +24,7 @@
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <vector>
 
 #include "dl_device.h"
@@ -527,6 +528,8 @@ __global__ __launch_bounds__(kSelectThreads) void k_sample_select(RowsArgs a) {
         c->row_generated[row] = emitted + 1;
         if (a.loop.stop_mask[r.token]) atomicOr(&c->finished_mask, 1u << row);
       }
+    } else if (a.result_out) {
+      *a.result_out = r;
     } else {
       state->result = r;
     }
@@ -592,7 +595,7 @@ __global__ void k_clear_state(RowState* state, int rows) {
   }
 }
 
-uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+constexpr uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 
 }  // namespace
 
@@ -688,9 +691,70 @@ void check_row(dl_sampler* s, const void* row, uint64_t row_bytes) {
   dl::require(row != nullptr && row_bytes == s->vocabulary * 2, "invalid device sampling row");
 }
 
+// ---------------------------------------------- allocation-free selection
+// Scratch of dl_sample_noalloc: the workspace of one selection row (the
+// 65,536-bin histogram, the FP64 weight of each distinct value, the argmax
+// partials and one row state), carved exactly as carve_workspace(base, 1, 0)
+// carves an allocated arena.  Each GPU holds its own copy until the process
+// ends.  Host code never passes the array's name to a kernel: its device
+// address comes from hipGetSymbolAddress, once per device.
+constexpr uint64_t kNoAllocScratchBytes =
+    align_up(uint64_t(kBins) * sizeof(uint32_t), 256) + align_up(uint64_t(kBins) * sizeof(double), 256) +
+    align_up(uint64_t(kCountBlocks) * sizeof(uint64_t), 256) + align_up(uint64_t(kCountBlocks) * sizeof(uint32_t), 256) +
+    align_up(sizeof(RowState), 256);
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+std::mutex scratch_mutex;
+std::vector<void*> scratch_address;  // per device ordinal, from hipGetSymbolAddress
+
+// The current device's address of `scratch` (the device is current: the
+// caller went through dl::enter).
+void* scratch_on(int ordinal) {
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_address.size() <= static_cast<size_t>(ordinal)) scratch_address.resize(ordinal + 1, nullptr);
+  if (!scratch_address[ordinal]) {
+    void* ptr = nullptr;
+    dl::check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "sampler scratch address");
+    dl::require(ptr != nullptr, "sampler scratch address", DL_RUNTIME_ERROR);
+    scratch_address[ordinal] = ptr;
+  }
+  return scratch_address[ordinal];
+}
+
 }  // namespace
 
 extern "C" {
+
+int dl_sample_noalloc(dl_queue* queue, const void* logits, uint64_t row_bytes, uint64_t vocabulary,
+                      const dl_sampling* settings, uint64_t draw_bits, uint32_t* result) {
+  return dl::guard([&] {
+    const Settings st = checked_settings(settings);
+    dl::require(vocabulary > 0, "unsupported sampling vocabulary");
+    dl::require(vocabulary <= kMaxVocabulary, "vocabulary above the allocation-free sampler's maximum of 2^28 ids",
+                DL_LENGTH_ERROR);
+    dl::require(logits != nullptr && row_bytes == vocabulary * 2, "invalid device sampling row");
+    dl::require(result != nullptr && reinterpret_cast<uintptr_t>(result) % alignof(uint32_t) == 0,
+                "invalid device result region");
+    dl::require(st.top_k <= vocabulary, "invalid device sampling row");
+    dl::enter(queue);
+    const Workspace ws = carve_workspace(scratch_on(queue->device->ordinal), 1, 0);
+    // The count kernel adds into the histogram, which must start at zero
+    // (a fill kernel, so the call can be recorded into a graph).
+    hipLaunchKernelGGL(k_clear_hist, dim3(64), dim3(256), 0, queue->stream, ws.hist, uint64_t(kBins));
+    RowsArgs a{};
+    a.logits = static_cast<const uint16_t*>(logits);
+    a.row_stride = vocabulary;
+    a.n = static_cast<uint32_t>(vocabulary);
+    a.rows = 1;
+    a.settings = st;
+    a.ws = ws;
+    a.draw_value = static_cast<double>(draw_bits >> 11) * 0x1p-53;
+    a.result_out = reinterpret_cast<Result*>(result);
+    launch_count(queue->stream, a);
+    launch_select(queue->stream, a);
+    dl::check_launch(queue, "allocation-free selection");
+  });
+}
 
 int dl_sampler_required_bytes(uint64_t vocabulary, uint64_t* bytes) {
   return dl::guard([&] {

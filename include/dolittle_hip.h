@@ -578,6 +578,19 @@ int dl_sampler_result(dl_sampler* sampler, uint32_t* token, uint32_t* status);
  * serial replay, and the number of selections the replay decided. */
 int dl_sampler_set_exact(dl_sampler* sampler, int exact);
 int dl_sampler_exact_replays(dl_sampler* sampler, uint64_t* count);
+/* No counterpart in the reference.  The selection of dl_sampler_submit with
+ * no sampler object and no allocation, for callers that cannot call
+ * hipMalloc (work recorded into a HIP graph, serving loops and harnesses that
+ * forbid allocation).  The workspace is a library-owned static device array
+ * of 789,760 bytes per GPU (one row's histogram, weights, partials and
+ * state), held until the process ends; the caller passes the BF16 logits row
+ * (row_bytes = vocabulary * 2, vocabulary at most 2^28, larger is a
+ * DL_LENGTH_ERROR) and `result`, device memory for {token, status} written
+ * when the queue reaches the call.  Every call on one GPU shares that array:
+ * calls that overlap on one GPU (two queues, two threads) race.  Results
+ * equal dl_sampler_submit's for the same row, settings and draw bits. */
+int dl_sample_noalloc(dl_queue* queue, const void* logits, uint64_t row_bytes, uint64_t vocabulary,
+                      const dl_sampling* settings, uint64_t draw_bits, uint32_t* result);
 
 #ifdef __cplusplus
 }
