@@ -26,6 +26,42 @@ def _mark_finalizing() -> None:
 atexit.register(_mark_finalizing)
 
 
+class Native:
+    """A native handle and the handles it was created from (its parents).
+
+    The C ABI requires dependents to go first: a device outlives its queues
+    and buffers, a queue and model outlive their plans (src/gpu/device.h:
+    "Device ... outlives every resource and queue it creates").  Python may
+    finalize the objects of one garbage cycle in any order, so destruction
+    is deferred: a handle is destroyed once its owner released it and every
+    handle created from it is destroyed, then its parents are reconsidered."""
+
+    __slots__ = ("destroy", "handle", "parents", "dependents", "released", "destroyed")
+
+    def __init__(self, destroy: str, handle, *parents: "Native"):
+        self.destroy, self.handle, self.parents = destroy, handle, tuple(p for p in parents if p is not None)
+        self.dependents, self.released, self.destroyed = 0, False, False
+        for parent in self.parents:
+            parent.dependents += 1
+
+    def release(self) -> None:
+        self.released = True
+        self._collect()
+
+    def _collect(self) -> None:
+        if not self.released or self.dependents or self.destroyed:
+            return
+        self.destroyed = True
+        if not _finalizing:
+            try:
+                call(self.destroy, self.handle)
+            except Exception:
+                pass
+        for parent in self.parents:
+            parent.dependents -= 1
+            parent._collect()
+
+
 def releasing() -> bool:
     """False once the interpreter is shutting down.  Objects still alive then
     (for example held by a stored traceback) are finalized in no particular
@@ -65,6 +101,11 @@ class Sampling(C.Structure):
 class GenerationResult(C.Structure):
     _fields_ = [("generated", C.c_uint32), ("reason", C.c_uint32), ("status", C.c_uint32),
                 ("reserved", C.c_uint32), ("position", C.c_uint64)]
+
+
+class SequenceEvent(C.Structure):
+    _fields_ = [("kind", C.c_uint8), ("reserved", C.c_uint8 * 3), ("status", C.c_uint32), ("position", C.c_uint64),
+                ("count", C.c_uint64), ("token", C.c_uint32), ("norm", C.c_float)]
 
 
 class ArchiveLimits(C.Structure):
@@ -159,6 +200,10 @@ SIGNATURES = {
     "dl_plan_launch_kernel": [vp, u32, u32, u32],
     "dl_plan_set_grid": [vp, u32, u32],
     "dl_plan_request_stop": [vp],
+    "dl_plan_collect_event": [vp, u32, u64, cint, vp, C.POINTER(cint)],
+    "dl_plan_event_count": [vp, u32, C.POINTER(u64)],
+    "dl_plan_set_step_window": [vp, u32],
+    "dl_plan_steps_enqueued": [vp, C.POINTER(u64)],
     "dl_plan_prefill": [vp, u32p, u32],
     "dl_plan_prefill_exact": [vp, u32p, u32],
     "dl_plan_read_prefill_hidden": [vp, u64, u64, u16p],

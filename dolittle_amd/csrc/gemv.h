@@ -59,12 +59,19 @@ __device__ __forceinline__ void stage_put(float* xs, int I, int b, int i, float 
 // before any is consumed.  Requires I % 8 == 0 and I <= 8 * 8 * blockDim.x.
 // `row_stride` (default I) is the distance between source rows, so a block
 // of columns of wider rows can be staged.
+//
+// `active`, when given, is the token loop's grid-uniform liveness word: it
+// is loaded first, and once the row's and the caller's loads are issued a
+// stopped loop returns false before any conversion or LDS store (a stopped
+// step then costs its launch and a few loads).  The word is only waited for
+// after the vector loads are in flight, so a live step waits no longer.
 template <int P, class Issue>
-__device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ x, int I, int rows, float* xs,
-                                           Issue&& issue, int row_stride = 0) {
+__device__ __forceinline__ bool stage_rows(const uint16_t* __restrict__ x, int I, int rows, float* xs,
+                                           Issue&& issue, int row_stride = 0, const uint32_t* active = nullptr) {
   constexpr int kMaxChunks = 8;
   const int chunks = I / 8;
   const uint64_t stride = row_stride ? row_stride : I;
+  const uint32_t live = active ? *active : 1u;
   for (int b = 0; b < rows; ++b) {
     const u32x4* src = reinterpret_cast<const u32x4*>(x + static_cast<uint64_t>(b) * stride);
     u32x4 v[kMaxChunks];
@@ -79,6 +86,7 @@ __device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ x, int I
       __builtin_amdgcn_sched_barrier(0);
       issue();
       __builtin_amdgcn_sched_barrier(0);
+      if (!live) return false;
     }
 #pragma unroll
     for (int j = 0; j < kMaxChunks; ++j) {
@@ -96,6 +104,7 @@ __device__ __forceinline__ void stage_rows(const uint16_t* __restrict__ x, int I
       }
     }
   }
+  return true;
 }
 
 // Stages the columns [0, I) of B BF16 rows (source rows `row_stride` apart)
@@ -335,10 +344,11 @@ constexpr int kNormK = 32;
 constexpr int kNormWidth = 128 * kNormK;
 
 template <int R, bool S16, bool S32, int G, class Issue>
-__device__ __forceinline__ void norm_stage_pass(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
+__device__ __forceinline__ bool norm_stage_pass(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
                                                 float eps, float* xs16, float* xs32, float* scratch, int b0, int B,
-                                                Issue&& issue) {
+                                                Issue&& issue, const uint32_t* active) {
   constexpr int D = kNormWidth;
+  const uint32_t live = active ? *active : 1u;
   const int tid = threadIdx.x, t = tid % 128, g = tid / 128;
   static_assert(R == 1 || R == 2, "a thread group owns one or two rows");
   const int r0 = b0 + R * g;
@@ -359,6 +369,7 @@ __device__ __forceinline__ void norm_stage_pass(const uint16_t* __restrict__ h, 
   __builtin_amdgcn_sched_barrier(0);
   issue();
   __builtin_amdgcn_sched_barrier(0);
+  if (!live) return false;
   if (has0) {
 #pragma unroll
     for (int b = 0; b < R; ++b) {
@@ -394,26 +405,30 @@ __device__ __forceinline__ void norm_stage_pass(const uint16_t* __restrict__ h, 
       }
     }
   }
+  return true;
 }
 
 // norm_stage_pass over B rows, R G at a time (R = 2 rows per group, 1 for
 // a single row) (scratch is reused between
 // passes behind a barrier); G = threads / 128 of the calling workgroup.
-// Rows have width kNormWidth.
+// Rows have width kNormWidth.  Returns false, before any math, when the
+// loop word `active` (read in the first pass, as in stage_rows) is zero.
 template <int B, bool S16, bool S32, int G, class Issue>
-__device__ __forceinline__ void norm_stage(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
-                                           float eps, float* xs16, float* xs32, float* scratch, Issue&& issue) {
+__device__ __forceinline__ bool norm_stage(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
+                                           float eps, float* xs16, float* xs32, float* scratch, Issue&& issue,
+                                           const uint32_t* active = nullptr) {
   constexpr int R = B == 1 ? 1 : 2;
   auto none = [] {};
 #pragma unroll
   for (int b0 = 0; b0 < B; b0 += R * G) {
     if (b0) {
       __syncthreads();
-      norm_stage_pass<R, S16, S32, G>(h, gain, eps, xs16, xs32, scratch, b0, B, none);
-    } else {
-      norm_stage_pass<R, S16, S32, G>(h, gain, eps, xs16, xs32, scratch, b0, B, issue);
+      norm_stage_pass<R, S16, S32, G>(h, gain, eps, xs16, xs32, scratch, b0, B, none, nullptr);
+    } else if (!norm_stage_pass<R, S16, S32, G>(h, gain, eps, xs16, xs32, scratch, b0, B, issue, active)) {
+      return false;
     }
   }
+  return true;
 }
 
 }  // namespace dl

@@ -23,6 +23,7 @@
 // inactive, replacing the reference's conditional CUDA graph nodes
 // (src/kernels/cuda/decode.cu:103-194, 339-353), which HIP lacks.
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -133,6 +134,54 @@ __global__ void k_rope_table(float* rope, uint64_t positions, int width, double 
 }
 
 // ----------------------------------------------------------- control kernels
+// ----------------------------------------------------------- event journal
+// DeviceSequence publication (decode.cu publish, :94-101): events are
+// written into host-mapped memory with vector stores, then one system-scope
+// release fence orders them before the per-sequence counters, which the
+// host reads with acquire loads.  One thread writes all of a step's events.
+__device__ void journal_write(const Journal& j, Control* c, int b, uint32_t kind, uint32_t status,
+                              uint64_t position, uint64_t count, uint32_t token, float norm) {
+  const uint32_t n = c->events[b];
+  if (!j.events || n >= j.capacity) return;  // capacity covers prompt + 2 * generated + 4 events
+  u32x4* dst = reinterpret_cast<u32x4*>(j.events + static_cast<uint64_t>(b) * j.capacity + n);
+  const u32x4 lo = {kind, status, static_cast<uint32_t>(position), static_cast<uint32_t>(position >> 32)};
+  const u32x4 hi = {static_cast<uint32_t>(count), static_cast<uint32_t>(count >> 32), token, __float_as_uint(norm)};
+  dst[0] = lo;
+  dst[1] = hi;
+  c->events[b] = n + 1;
+}
+
+// Publishes the event counts of sequences [0, batch) and the loop's
+// liveness and step count.
+__device__ void journal_publish(const Journal& j, const Control* c, int batch) {
+  if (!j.events) return;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+  for (int b = 0; b < batch; ++b)
+    __hip_atomic_store(&j.publication[b].completed, c->events[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store(&j.mirror->steps, c->steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store(&j.mirror->active, c->active, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Terminal events of the sequences not yet terminal when the loop ends at
+// `position` (decode.cu finish_sequence): failure on a latched status, eos
+// for a sequence that selected a stop id, limit when the whole budget was
+// produced and consumed, cancelled otherwise.
+__device__ void journal_finish(const Journal& j, Control* c, int batch, uint64_t position) {
+  for (int b = 0; b < batch; ++b) {
+    if ((c->terminal_mask >> b) & 1u) continue;
+    const uint32_t generated = c->row_generated[b];
+    const uint32_t reason =
+        c->status ? kFailure
+                  : (generated && ((c->finished_mask >> b) & 1u))
+                        ? kEos
+                        : (position == static_cast<uint64_t>(c->prompt_length) + generated && generated == c->max_new)
+                              ? kLimit
+                              : kCancelled;
+    journal_write(j, c, b, kTerminal, reason, position, generated, c->status, 0.0f);
+    c->terminal_mask |= 1u << b;
+  }
+}
+
 struct InitArgs {
   Control* ctl;
   uint64_t position;
@@ -140,6 +189,9 @@ struct InitArgs {
   int32_t capture_layer, steer_layer;
   uint32_t steer_mask, override_active, override_mask;
   uint64_t override_position;
+  Journal journal;
+  const uint32_t* injection_status;  // installed injection's status word, or null
+  const float* injection_norm;       // its norm word
 };
 
 __global__ void k_init_control(InitArgs a) {
@@ -162,7 +214,15 @@ __global__ void k_init_control(InitArgs a) {
   c.steer_layer = a.steer_layer;
   c.steer_mask = a.steer_mask;
   c.select_row = 0;
+  // The journal opens with the injection's status (decode.cu decide_stage,
+  // prefill) and, after a prompt pass, the positions it consumed.
+  for (uint32_t b = 0; b < a.batch; ++b) {
+    if (a.injection_status)
+      journal_write(a.journal, &c, b, kInjection, *a.injection_status, 0, 0, 0, *a.injection_norm);
+    if (a.position > 0) journal_write(a.journal, &c, b, kConsumed, 0, 0, a.position, 0, 0.0f);
+  }
   *a.ctl = c;
+  journal_publish(a.journal, &c, static_cast<int>(a.batch));
 }
 
 struct BeginArgs {
@@ -179,13 +239,19 @@ struct BeginArgs {
   int D;
   uint32_t V;
   int tied;
+  Journal journal;
+  int batch;
 };
 
 // Embedding (embedding.cu:60-80), the embedding override, and the step's
-// selection decision.  Grid: one block per sequence.  An invalid injection
-// (decode.cu decide_stage: the injection status gates the prompt) or a
+// decisions (decode.cu decide_stage / finish_consumption).  Grid: one block
+// per sequence.  An invalid injection (its status gates the prompt) or a
 // latched intervention failure ends the loop with reason failure before the
-// step consumes anything.
+// step consumes anything.  Cancellation is read once per step, here: while
+// the step would consume a prompt position nothing is pending and the loop
+// ends before it; when it would consume a selected token, that token is
+// still consumed ("a selection promises consumption") and no new one is
+// selected, so the loop ends after this step.
 __global__ __launch_bounds__(kBlock) void k_step_begin(BeginArgs a) {
   Control* c = a.ctl;
   if (!c->active) return;
@@ -195,13 +261,22 @@ __global__ __launch_bounds__(kBlock) void k_step_begin(BeginArgs a) {
     uint32_t failed = 0;
     if (a.injection_status && *a.injection_status) failed |= 8u;
     if (a.intervention_state && a.intervention_state[0]) failed |= 16u;
-    if (failed) {
+    const bool cancelled = __hip_atomic_load(a.cancel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != 0;
+    if (failed || (cancelled && pos < c->prompt_length)) {
       c->status |= failed;
       c->select_row = 0;
       c->active = 0;
-      c->reason = 3;
+      c->reason = failed ? 3u : 2u;
+      journal_finish(a.journal, c, a.batch, pos);
+      journal_publish(a.journal, c, a.batch);
     } else {
+      if (cancelled) {
+        c->cancel_pending = 1;
+        c->stop_pending = 1;
+      }
       c->select_row = (pos + 1 >= c->prompt_length && !c->stop_pending) ? 1u : 0u;
+      c->finished_before = c->finished_mask;
+      c->select_mask = c->select_row ? (c->all_mask & ~c->finished_mask) : 0u;
     }
   }
   const uint32_t token = pos < c->prompt_length ? a.tokens[pos] : a.selected[b];
@@ -270,13 +345,16 @@ __global__ __launch_bounds__(qkv_waves(B, Part) * 64) void k_qkv(QkvArgs a) {
   const int items = (tile_end - tile_begin) * Split;
   const int first = blockIdx.x * W + wave;
   FirstBatch fb{};
-  norm_stage<B, Part != kQkvKV, Part != kQkvQ, W / 2>(a.h, a.norm, a.eps, xs16, xs32, scratch, [&] {
-    if (first < items) issue_first(tile_src(tile_begin + first / Split), lane, fb);
-  });
+  // The prologue returns, after issuing its loads, when the loop is stopped
+  // (grid-uniform flag).
+  if (!norm_stage<B, Part != kQkvKV, Part != kQkvQ, W / 2>(
+          a.h, a.norm, a.eps, xs16, xs32, scratch,
+          [&] {
+            if (first < items) issue_first(tile_src(tile_begin + first / Split), lane, fb);
+          },
+          &a.ctl->active))
+    return;
   __syncthreads();
-  // The loop state is read after the prologue's loads are in flight (the
-  // prologue writes nothing outside LDS); the flag is grid-uniform.
-  if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
   for (int item = first; item < items; item += gridDim.x * W) {
     const int tile = tile_begin + item / Split, b0 = (item % Split) * BR;
@@ -903,13 +981,16 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual(ResidualArgs a)
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
   const int first = blockIdx.x * W + wave;
   FirstBatch fb{};
-  stage_rows<P>(a.x + static_cast<uint64_t>(a.row0) * a.I, a.I, B, xs, [&] {
-    if (first < items) issue_first(a.w + (first / Split) * chunks, lane, fb);
-  });
+  // The prologue returns, after issuing its loads, when the loop is stopped
+  // (grid-uniform flag).
+  if (!stage_rows<P>(
+          a.x + static_cast<uint64_t>(a.row0) * a.I, a.I, B, xs,
+          [&] {
+            if (first < items) issue_first(a.w + (first / Split) * chunks, lane, fb);
+          },
+          0, &a.ctl->active))
+    return;
   __syncthreads();
-  // Read after the prologue's loads are in flight (grid-uniform flag; the
-  // prologue writes only LDS).
-  if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
   const bool steer = a.steer != nullptr && a.layer == a.ctl->steer_layer;
   const bool capture = a.capture != nullptr && a.layer == a.ctl->capture_layer;
@@ -1008,13 +1089,16 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_gateup(GateUpArgs a) {
   const uint64_t chunks = static_cast<uint64_t>(S) * 64;
   const int first = blockIdx.x * W + wave;
   FirstBatch fb{};
-  norm_stage<B, true, false, W / 2>(a.h, a.norm, a.eps, xs, nullptr, scratch, [&] {
-    if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
-  });
+  // The prologue returns, after issuing its loads, when the loop is stopped
+  // (grid-uniform flag).
+  if (!norm_stage<B, true, false, W / 2>(
+          a.h, a.norm, a.eps, xs, nullptr, scratch,
+          [&] {
+            if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
+          },
+          &a.ctl->active))
+    return;
   __syncthreads();
-  // Read after the prologue's loads are in flight (grid-uniform flag; the
-  // prologue writes only LDS).
-  if (!a.ctl->active) return;
   (void)S;
   for (int tile = first; tile < tiles; tile += gridDim.x * W) {
     float acc[B];
@@ -1163,9 +1247,9 @@ struct EndArgs {
   uint32_t* out_tokens;     // [B][out_capacity]
   uint32_t out_capacity;
   const uint8_t* stop_mask; // [V]
-  const uint32_t* cancel;   // host-mapped cancel word
   const uint32_t* intervention_state;  // [status, count], or null
   int batch;
+  Journal journal;
 };
 
 // Greedy selection from the argmax partials (categorical rows were selected
@@ -1216,29 +1300,46 @@ __global__ __launch_bounds__(kBlock) void k_step_end(EndArgs a) {
     }
   }
   if (threadIdx.x != 0) return;
+  const uint64_t pos = c->position;
+  // Events of this step (decode.cu finish_prompt / finish_consumption /
+  // finish_selection): every running sequence consumed `pos`; the selecting
+  // ones chose the token of `pos + 1`; a sequence whose stop id was
+  // selected earlier has now consumed it and ends with reason eos.
+  for (int b = 0; b < a.batch; ++b)
+    if (!((c->terminal_mask >> b) & 1u)) journal_write(a.journal, c, b, kConsumed, 0, pos, 1, 0, 0.0f);
+  if (select && c->status == 0) {
+    for (int b = 0; b < a.batch; ++b)
+      if ((c->select_mask >> b) & 1u) journal_write(a.journal, c, b, kSelected, 0, pos + 1, 1, a.selected[b], 0.0f);
+  }
+  for (int b = 0; b < a.batch; ++b) {
+    if (((c->finished_before & ~c->terminal_mask) >> b) & 1u) {
+      journal_write(a.journal, c, b, kTerminal, kEos, pos + 1, c->row_generated[b], 0, 0.0f);
+      c->terminal_mask |= 1u << b;
+    }
+  }
   if (select) {
     c->generated += 1;
     if (c->generated >= c->max_new || (c->finished_mask & c->all_mask) == c->all_mask) c->stop_pending = 1;
-  } else if (c->stop_pending && c->position + 1 >= c->prompt_length) {
+  } else if (c->stop_pending && pos + 1 >= c->prompt_length) {
     // The final selection has now been consumed (decode.cu finish_consumption).
     c->active = 0;
-    c->reason = (c->max_new > 0 && (c->finished_mask & c->all_mask) == c->all_mask) ? 1u : 0u;
-  }
-  if (c->active && __hip_atomic_load(a.cancel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
-    c->active = 0;
-    c->reason = 2;
+    c->reason = c->cancel_pending ? 2u
+                                  : (c->max_new > 0 && (c->finished_mask & c->all_mask) == c->all_mask) ? 1u : 0u;
   }
   // decode.cu finish_consumption / finish_sequence: a latched intervention
   // failure ends the loop, and a loop that ends with its whole prompt
   // consumed must have applied the intervention exactly once.
   if (const uint32_t* iv = a.intervention_state) {
-    if (iv[0] || (!c->active && c->position + 1 >= c->prompt_length && iv[1] != 1)) c->status |= 16u;
+    if (iv[0] || (!c->active && pos + 1 >= c->prompt_length && iv[1] != 1)) c->status |= 16u;
   }
   if (c->status) {
     c->active = 0;
     c->reason = 3;
   }
-  c->position += 1;
+  c->position = pos + 1;
+  c->steps += 1;
+  if (!c->active) journal_finish(a.journal, c, a.batch, pos + 1);
+  journal_publish(a.journal, c, a.batch);
 }
 
 // Row-major seeded N(0, std) fill (untied embedding table).
@@ -1797,6 +1898,18 @@ struct dl_plan {
   uint8_t* stop_mask = nullptr;
   uint32_t* cancel_host = nullptr;
   uint32_t* cancel_device = nullptr;
+  // DeviceSequence event journal in pinned, host-mapped memory: per-sequence
+  // publication words, the loop mirror, then kMaxBatch x capacity events.
+  void* journal_host = nullptr;
+  dl::Journal journal{};  // device addresses of the same memory
+  dl::Publication* publication_host = nullptr;
+  dl::Mirror* mirror_host = nullptr;
+  dl::Event* events_host = nullptr;
+  // Bounded step window: 0 enqueues every step of a generation at once (the
+  // loop then completes without the host); n keeps at most 2n steps ahead of
+  // the device and enqueues no more once the loop has stopped.
+  uint32_t window = 0;
+  uint64_t steps_total = 0, steps_enqueued = 0;
   uint64_t cache_seq_stride = 0, cache_layer_stride = 0;
   hipGraph_t graphs[2] = {nullptr, nullptr};  // [0] long context, [1] short context
   hipGraphExec_t execs[2] = {nullptr, nullptr};
@@ -1833,6 +1946,7 @@ struct dl_plan {
   // storage belongs to the caller and must outlive its use.
   const uint16_t* injection_row = nullptr;
   const uint32_t* injection_status = nullptr;
+  const float* injection_norm = nullptr;
   // One-row residual intervention (steering.cu:107-159) on the output of
   // block `layer` for sequence `sequence` at `position`.
   struct Intervention {
@@ -1884,6 +1998,7 @@ struct dl_plan {
     }
     for (void* p : allocations) (void)hipFree(p);
     if (cancel_host) (void)hipHostFree(cancel_host);
+    if (journal_host) (void)hipHostFree(journal_host);
   }
 
   void record_step(hipStream_t s, bool short_context);
@@ -2123,7 +2238,7 @@ void record_step_all(dl_plan* p, hipStream_t s, bool short_context) {
   const auto& c = m->cfg;
   BeginArgs begin{p->ctl, p->tokens, p->selected, p->h, m->lm_head, m->embedding, p->override_source(),
                   p->cancel_device, p->injection_status, p->intervention_state(), static_cast<int>(c.hidden),
-                  c.vocab, c.tied_embeddings ? 1 : 0};
+                  c.vocab, c.tied_embeddings ? 1 : 0, p->journal, static_cast<int>(p->batch)};
   k_step_begin<<<p->batch, kBlock, 0, s>>>(begin);
   static const int kShort[] = {0, 8, 4, 5, 6};
   static const int kLong[] = {0, 1, 2, 3, 4, 5, 6};
@@ -2149,7 +2264,7 @@ void record_step_all(dl_plan* p, hipStream_t s, bool short_context) {
     sampling::launch_select(s, ra);
   }
   EndArgs ea{p->ctl, p->partial_keys, p->partial_flags, p->head_blocks, p->selected, p->out_tokens, p->cap,
-             p->stop_mask, p->cancel_device, p->intervention_state(), static_cast<int>(p->batch)};
+             p->stop_mask, p->intervention_state(), static_cast<int>(p->batch), p->journal};
   k_step_end<<<1, kBlock, 0, s>>>(ea);
 }
 
@@ -2201,6 +2316,7 @@ void reset_intervention(dl_plan* p) {
 }
 
 void launch_steps(dl_plan* p, uint32_t steps) {
+  p->steps_enqueued += steps;
   for (uint32_t i = 0; i < steps; ++i) {
     const bool short_context = p->host_position < static_cast<uint64_t>(dl::kFusedKeys);
     if (p->eager)
@@ -2212,15 +2328,42 @@ void launch_steps(dl_plan* p, uint32_t steps) {
   if (p->eager) dl::check_launch(p->queue, "decode step");
 }
 
+// Starts a loop at `position`.  The queue must be idle: the journal's host
+// words are reset here, before the device writes them again.
 void init_control(dl_plan* p, uint64_t position, uint32_t prompt_length, uint32_t max_new, uint32_t mode) {
   p->host_position = position;
+  p->steps_enqueued = 0;
+  p->steps_total = prompt_length > position ? prompt_length - position + uint64_t(max_new) : 0;
+  for (int b = 0; b < dl::kMaxBatch; ++b) __atomic_store_n(&p->publication_host[b].completed, 0u, __ATOMIC_RELAXED);
+  __atomic_store_n(&p->mirror_host->steps, 0u, __ATOMIC_RELAXED);
+  __atomic_store_n(&p->mirror_host->active, 1u, __ATOMIC_RELEASE);
   // An injection replaces a prompt row only (executor.cpp: the embedding
   // replacement is submitted with the prompt body).
   const bool override_on = p->override_active && !(p->injection_row && p->override_position >= prompt_length);
   dl::InitArgs a{p->ctl, position, prompt_length, max_new, p->batch, mode, p->capture_layer, p->steer_layer,
-                 p->steer_mask, override_on ? 1u : 0u, p->override_mask, p->override_position};
+                 p->steer_mask, override_on ? 1u : 0u, p->override_mask, p->override_position, p->journal,
+                 p->injection_status, p->injection_norm};
   dl::k_init_control<<<1, 1, 0, p->queue->stream>>>(a);
   dl::check_launch(p->queue, "init control");
+}
+
+// Window pacing: enqueues further steps of the running generation while
+// fewer than two windows are ahead of the device and the loop is live.
+void pump(dl_plan* p) {
+  if (!p->window || p->steps_enqueued >= p->steps_total) return;
+  if (!__atomic_load_n(&p->mirror_host->active, __ATOMIC_ACQUIRE)) return;
+  const uint64_t done = __atomic_load_n(&p->mirror_host->steps, __ATOMIC_ACQUIRE);
+  // A window is added only while at most one is ahead, so never more than
+  // two windows run past the last step the host saw.
+  while (p->steps_enqueued < p->steps_total && p->steps_enqueued - std::min(done, p->steps_enqueued) <= p->window) {
+    launch_steps(p, static_cast<uint32_t>(std::min<uint64_t>(p->window, p->steps_total - p->steps_enqueued)));
+  }
+}
+
+// True while a windowed generation still has steps to enqueue.
+bool pumping(const dl_plan* p) {
+  return p->window && p->steps_enqueued < p->steps_total &&
+         __atomic_load_n(&p->mirror_host->active, __ATOMIC_ACQUIRE) != 0;
 }
 }  // namespace
 
@@ -2288,6 +2431,26 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
     *p->cancel_host = 0;
     dl::check_hip(hipHostGetDevicePointer(reinterpret_cast<void**>(&p->cancel_device), p->cancel_host, 0),
                   "cancel word mapping");
+    {
+      // The journal: P + 2G + 3 events at most per sequence (an injection,
+      // the consumed positions, one selection and one consumption per
+      // token, the terminal) with P + G <= capacity.
+      const uint64_t per_sequence = 2ull * p->cap + 4;
+      const uint64_t head = sizeof(dl::Publication) * dl::kMaxBatch + sizeof(dl::Mirror);
+      const uint64_t bytes = head + uint64_t(B) * per_sequence * sizeof(dl::Event);
+      dl::check_hip(hipHostMalloc(&p->journal_host, bytes, hipHostMallocMapped | hipHostMallocCoherent), "journal");
+      std::memset(p->journal_host, 0, bytes);
+      void* device = nullptr;
+      dl::check_hip(hipHostGetDevicePointer(&device, p->journal_host, 0), "journal mapping");
+      auto* host = static_cast<uint8_t*>(p->journal_host);
+      auto* dev = static_cast<uint8_t*>(device);
+      p->publication_host = reinterpret_cast<dl::Publication*>(host);
+      p->mirror_host = reinterpret_cast<dl::Mirror*>(host + sizeof(dl::Publication) * dl::kMaxBatch);
+      p->events_host = reinterpret_cast<dl::Event*>(host + head);
+      p->journal = dl::Journal{reinterpret_cast<dl::Publication*>(dev),
+                               reinterpret_cast<dl::Mirror*>(dev + sizeof(dl::Publication) * dl::kMaxBatch),
+                               reinterpret_cast<dl::Event*>(dev + head), static_cast<uint32_t>(per_sequence)};
+    }
     dl::k_rope_table<<<fill_grid(cap * c.head_dim / 2), 256, 0, queue->stream>>>(p->rope, cap, c.head_dim,
                                                                                   c.rope_theta);
     dl::check_launch(queue, "rope table");
@@ -2481,6 +2644,7 @@ static void clear_injection(dl_plan* plan) {
   if (!plan->injection_row) return;
   plan->injection_row = nullptr;
   plan->injection_status = nullptr;
+  plan->injection_norm = nullptr;
   plan->override_active = false;
   dl::check_hip(hipStreamSynchronize(plan->queue->stream), "injection clear");
   plan->capture_step();
@@ -2522,6 +2686,7 @@ int dl_plan_set_injection(dl_plan* plan, uint64_t position, const void* storage,
     require(position < plan->capacity, "injection position outside the cache", DL_LENGTH_ERROR);
     const auto* base = static_cast<const uint8_t*>(storage);
     dl::check_hip(hipStreamSynchronize(plan->queue->stream), "injection setup");
+    plan->injection_norm = reinterpret_cast<const float*>(base);
     plan->injection_status = reinterpret_cast<const uint32_t*>(base + sizeof(float));
     plan->injection_row = reinterpret_cast<const uint16_t*>(base + sizeof(float) + sizeof(uint32_t));
     plan->override_active = true;
@@ -2663,7 +2828,13 @@ int dl_plan_generate(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_leng
   const int status =
       dl_plan_prepare_generation(plan, prompt, prompt_length, max_new, sampling, seeds, stop_ids, stop_count);
   if (status != DL_OK) return status;
-  return dl_plan_decode_steps(plan, static_cast<uint32_t>(prompt_length - plan->start_position) + max_new);
+  return guard([&] {
+    dl::enter(plan->queue);
+    if (plan->window)
+      pump(plan);
+    else
+      launch_steps(plan, static_cast<uint32_t>(plan->steps_total));
+  });
 }
 
 int dl_plan_prepare_generation(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length, uint32_t max_new,
@@ -2744,6 +2915,16 @@ int dl_plan_collect(dl_plan* plan, uint32_t* tokens, uint32_t max_new, dl_genera
     require(plan != nullptr, "null plan");
     dl::enter(plan->queue);
     hipStream_t s = plan->queue->stream;
+    // A windowed generation advances while it is collected.
+    while (pumping(plan)) {
+      pump(plan);
+      const hipError_t q = hipStreamQuery(s);
+      if (q != hipSuccess && q != hipErrorNotReady) {
+        plan->queue->device->poisoned = true;
+        dl::check_hip(q, "generation");
+      }
+      if (q == hipErrorNotReady) std::this_thread::sleep_for(std::chrono::microseconds(50));
+    }
     const hipError_t e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
       plan->queue->device->poisoned = true;
@@ -2764,8 +2945,74 @@ int dl_plan_collect(dl_plan* plan, uint32_t* tokens, uint32_t max_new, dl_genera
         results[b].status = c.status;
         results[b].reserved = c.active;
         results[b].position = c.position;
+        // A sequence's terminal event, when published, is its outcome
+        // (a sequence that stopped early ends at its own position).
+        const uint32_t count = __atomic_load_n(&plan->publication_host[b].completed, __ATOMIC_ACQUIRE);
+        if (count > 0) {
+          const dl::Event& last = plan->events_host[uint64_t(b) * plan->journal.capacity + count - 1];
+          if ((last.kind & 0xffu) == dl::kTerminal) {
+            results[b].reason = last.status;
+            results[b].generated = static_cast<uint32_t>(last.count);
+            results[b].position = last.position;
+          }
+        }
       }
     }
+  });
+}
+
+int dl_plan_collect_event(dl_plan* plan, uint32_t seq, uint64_t index, int wait, dl_sequence_event* event,
+                          int* ready) {
+  return guard([&] {
+    require(plan && event && ready, "null argument");
+    require(seq < plan->batch, "sequence out of range");
+    require(index < plan->journal.capacity, "event outside sequence", DL_LENGTH_ERROR);
+    dl::enter(plan->queue);
+    *ready = 0;
+    hipStream_t s = plan->queue->stream;
+    const dl::Event* slot = plan->events_host + uint64_t(seq) * plan->journal.capacity + index;
+    for (;;) {
+      pump(plan);
+      if (__atomic_load_n(&plan->publication_host[seq].completed, __ATOMIC_ACQUIRE) > index) {
+        std::memcpy(event, slot, sizeof *event);
+        *ready = 1;
+        return;
+      }
+      if (!wait) return;
+      const hipError_t q = hipStreamQuery(s);
+      if (q == hipSuccess) {
+        if (__atomic_load_n(&plan->publication_host[seq].completed, __ATOMIC_ACQUIRE) > index) continue;
+        if (pumping(plan)) continue;
+        dl::fail(DL_RUNTIME_ERROR, "sequence ended without event");
+      }
+      if (q != hipErrorNotReady) {
+        plan->queue->device->poisoned = true;
+        dl::check_hip(q, "generation");
+      }
+      std::this_thread::sleep_for(std::chrono::microseconds(50));
+    }
+  });
+}
+
+int dl_plan_event_count(dl_plan* plan, uint32_t seq, uint64_t* count) {
+  return guard([&] {
+    require(plan && count, "null argument");
+    require(seq < plan->batch, "sequence out of range");
+    *count = __atomic_load_n(&plan->publication_host[seq].completed, __ATOMIC_ACQUIRE);
+  });
+}
+
+int dl_plan_set_step_window(dl_plan* plan, uint32_t steps) {
+  return guard([&] {
+    require(plan != nullptr, "null plan");
+    plan->window = steps;
+  });
+}
+
+int dl_plan_steps_enqueued(dl_plan* plan, uint64_t* steps) {
+  return guard([&] {
+    require(plan && steps, "null argument");
+    *steps = plan->steps_enqueued;
   });
 }
 

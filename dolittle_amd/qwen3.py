@@ -21,6 +21,7 @@ ROLE = {
     "q_norm": 7, "k_norm": 8, "o": 9, "post_norm": 10, "gate": 11, "up": 12, "down": 13,
 }
 REASON = {0: "limit", 1: "eos", 2: "cancelled", 3: "failure"}
+EVENT_KIND = {0: "consumed", 1: "selected", 2: "terminal", 3: "injection"}
 
 
 @dataclass
@@ -78,6 +79,7 @@ class Qwen3Model:
         handle = C.c_void_p()
         _lib.call("dl_qwen3_create", device.handle, queue.handle, C.byref(cfg), C.byref(handle))
         self.handle = handle
+        self._native = _lib.Native("dl_qwen3_destroy", handle, device._native, queue._native)
 
     def fill_synthetic(self, seed: int, weight_std: float = 0.02) -> None:
         _lib.call("dl_qwen3_fill_synthetic", self.handle, self.queue.handle, seed, C.c_float(weight_std))
@@ -100,12 +102,9 @@ class Qwen3Model:
         return n.value
 
     def __del__(self):
-        if not _lib.releasing():
-            return
-        try:
-            _lib.call("dl_qwen3_destroy", self.handle)
-        except Exception:
-            pass
+        native = getattr(self, "_native", None)
+        if native is not None:
+            native.release()
 
 
 class Plan:
@@ -116,6 +115,7 @@ class Plan:
         handle = C.c_void_p()
         _lib.call("dl_plan_create", model.handle, model.queue.handle, batch, capacity, C.byref(handle))
         self.handle = handle
+        self._native = _lib.Native("dl_plan_destroy", handle, model._native)
         self.max_new = 0
 
     # -- diagnostic chunk path
@@ -273,10 +273,40 @@ class Plan:
     def request_stop(self) -> None:
         _lib.call("dl_plan_request_stop", self.handle)
 
+    # -- DeviceSequence event journal (src/inference/decoding/device.h:86-137)
+    def collect_event(self, seq: int, index: int, wait: bool = True) -> Optional[dict]:
+        """Event `index` of sequence `seq` as a dict, or None when `wait` is
+        False and it is not published yet."""
+        ev = _lib.SequenceEvent()
+        ready = C.c_int(0)
+        _lib.call("dl_plan_collect_event", self.handle, seq, index, 1 if wait else 0, C.byref(ev), C.byref(ready))
+        if not ready.value:
+            return None
+        return {"kind": EVENT_KIND.get(ev.kind, ev.kind), "status": ev.status, "position": ev.position,
+                "count": ev.count, "token": ev.token, "norm": ev.norm}
+
+    def event_count(self, seq: int = 0) -> int:
+        n = C.c_uint64()
+        _lib.call("dl_plan_event_count", self.handle, seq, C.byref(n))
+        return n.value
+
+    def events(self, seq: int = 0) -> list[dict]:
+        """Every event of sequence `seq` up to and including its terminal
+        event (waits for it)."""
+        out = []
+        while not out or out[-1]["kind"] != "terminal":
+            out.append(self.collect_event(seq, len(out)))
+        return out
+
+    def set_step_window(self, steps: int) -> None:
+        _lib.call("dl_plan_set_step_window", self.handle, steps)
+
+    def steps_enqueued(self) -> int:
+        n = C.c_uint64()
+        _lib.call("dl_plan_steps_enqueued", self.handle, C.byref(n))
+        return n.value
+
     def __del__(self):
-        if not _lib.releasing():
-            return
-        try:
-            _lib.call("dl_plan_destroy", self.handle)
-        except Exception:
-            pass
+        native = getattr(self, "_native", None)
+        if native is not None:
+            native.release()

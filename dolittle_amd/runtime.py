@@ -24,6 +24,7 @@ class DeviceBuffer:
             _lib.call("dl_buffer_alloc", device.handle, nbytes, alignment, C.byref(handle))
         self.device = device
         self.handle = handle
+        self._native = _lib.Native("dl_buffer_free", handle, device._native)
         self.nbytes = nbytes
         self.staging = staging
         address = C.c_void_p()
@@ -36,16 +37,13 @@ class DeviceBuffer:
 
     def free(self) -> None:
         if self.handle:
-            _lib.call("dl_buffer_free", self.handle)
             self.handle = None
+            self._native.release()
 
     def __del__(self):
-        if not _lib.releasing():
-            return
-        try:
-            self.free()
-        except Exception:
-            pass
+        native = getattr(self, "_native", None)
+        if native is not None:
+            native.release()
 
 
 class HostBuffer(DeviceBuffer):
@@ -64,6 +62,7 @@ class Event:
         handle = C.c_void_p()
         _lib.call("dl_event_create", device.handle, C.byref(handle))
         self.handle = handle
+        self._native = _lib.Native("dl_event_destroy", handle, device._native)
 
     def record(self, queue: "Queue") -> None:
         _lib.call("dl_event_record", self.handle, queue.handle)
@@ -74,12 +73,9 @@ class Event:
         return float(ms.value)
 
     def __del__(self):
-        if not _lib.releasing():
-            return
-        try:
-            _lib.call("dl_event_destroy", self.handle)
-        except Exception:
-            pass
+        native = getattr(self, "_native", None)
+        if native is not None:
+            native.release()
 
 
 class Queue:
@@ -90,6 +86,7 @@ class Queue:
         _lib.call("dl_queue_create", device.handle, C.byref(handle))
         self.device = device
         self.handle = handle
+        self._native = _lib.Native("dl_queue_destroy", handle, device._native)
 
     def upload(self, dst: DeviceBuffer, src: HostBuffer, nbytes: int, dst_offset=0, src_offset=0):
         _lib.call("dl_queue_upload", self.handle, dst.handle, dst_offset, src.handle, src_offset, nbytes)
@@ -121,12 +118,9 @@ class Queue:
         _lib.call("dl_queue_drain", self.handle)
 
     def __del__(self):
-        if not _lib.releasing():
-            return
-        try:
-            _lib.call("dl_queue_destroy", self.handle)
-        except Exception:
-            pass
+        native = getattr(self, "_native", None)
+        if native is not None:
+            native.release()
 
 
 class Device:
@@ -136,12 +130,18 @@ class Device:
         handle = C.c_void_p()
         _lib.call("dl_device_open", ordinal, C.byref(handle))
         self.handle = handle
+        self._native = _lib.Native("dl_device_close", handle)
         info = _lib.DeviceInfo()
         _lib.call("dl_device_info_get", handle, C.byref(info))
         self.name = info.name.decode()
         self.arch = info.arch.decode()
         self.compute_units = info.compute_units
         self.total_bytes = info.total_bytes
+
+    def __del__(self):
+        native = getattr(self, "_native", None)
+        if native is not None:
+            native.release()
 
     def allocate(self, nbytes: int, alignment: int = 256) -> DeviceBuffer:
         return DeviceBuffer(self, nbytes, alignment)

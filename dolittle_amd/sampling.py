@@ -43,6 +43,7 @@ class DeviceCategorical:
         _lib.call("dl_sampler_create", device.handle, queue.handle, vocabulary, code, budget,
                   C.byref(handle))
         self.handle = handle
+        self._native = _lib.Native("dl_sampler_destroy", handle, device._native, queue._native)
 
     @staticmethod
     def required_bytes(vocabulary: int) -> int:
@@ -100,13 +101,10 @@ class DeviceCategorical:
 
     def close(self) -> None:
         if getattr(self, "handle", None):
-            _lib.call("dl_sampler_destroy", self.handle)
             self.handle = None
+            self._native.release()
 
     def __del__(self):
-        if not _lib.releasing():
-            return
-        try:
-            self.close()
-        except Exception:
-            pass
+        native = getattr(self, "_native", None)
+        if native is not None:
+            native.release()

@@ -505,8 +505,53 @@ int dl_plan_set_grid(dl_plan* plan, uint32_t which, uint32_t blocks);
 int dl_plan_collect(dl_plan* plan, uint32_t* tokens, uint32_t max_new,
                     dl_generation_result* results);
 /* Requests cancellation of the running loop (may be called from another
- * thread; DeviceSequence::request_stop, decoding/device.h:126). */
+ * thread; DeviceSequence::request_stop, decoding/device.h:126).  The device
+ * reads it once per step: a prompt position not yet consumed stays
+ * unconsumed; a selected token is still consumed, and nothing further is
+ * selected (decode.cu: "a selection promises consumption"). */
 int dl_plan_request_stop(dl_plan* plan);
+
+/* DeviceSequence::Event (src/inference/decoding/device.h:86-102), 32 bytes:
+ * kind 0 consumed (positions [position, position + count) entered the
+ * caches), 1 selected (`token` chosen for absolute position `position`),
+ * 2 terminal (status = reason 0 limit / 1 eos / 2 cancelled / 3 failure,
+ * position = positions consumed, count = tokens generated, token = the
+ * failure status bits), 3 injection (status and norm of the installed
+ * DeviceInjection, first when one is installed).  Each sequence of a plan
+ * has its own journal, written by the device into pinned host-mapped memory
+ * (a system-scope release orders each event before its counter), so events
+ * can be read while the loop runs; a generation holds at most
+ * prompt + 2 * max_new + 3 events per sequence. */
+typedef struct dl_sequence_event {
+  uint8_t kind;
+  uint8_t reserved[3];
+  uint32_t status;
+  uint64_t position;
+  uint64_t count;
+  uint32_t token;
+  float norm;
+} dl_sequence_event;
+/* DeviceSequence::collect (decoding/device.h:136; decode.cu:579-610): event
+ * `index` of sequence `seq`.  With wait = 0 the call never blocks: *ready is
+ * 1 and *event filled when the event is published, else *ready is 0.  With
+ * wait != 0 it polls until the event is published, failing with
+ * DL_RUNTIME_ERROR if the queue drains without it.  An index beyond the
+ * journal's capacity is a DL_LENGTH_ERROR. */
+int dl_plan_collect_event(dl_plan* plan, uint32_t seq, uint64_t index, int wait,
+                          dl_sequence_event* event, int* ready);
+/* Events of sequence `seq` published so far (never blocks). */
+int dl_plan_event_count(dl_plan* plan, uint32_t seq, uint64_t* count);
+/* Bounded step window (no reference counterpart: HIP graphs have no
+ * conditional nodes, so each step is a host-enqueued graph replay).  0, the
+ * default, enqueues every step of a generation at once and the loop
+ * completes with no further host call, as the reference's conditional graph
+ * does; a stop leaves the remaining steps to replay as no-ops.  steps = n
+ * keeps at most 2n steps enqueued ahead of the device: dl_plan_collect and
+ * dl_plan_collect_event enqueue more while the loop is live and none after
+ * it stopped, so a stopped loop replays at most 2n idle steps. */
+int dl_plan_set_step_window(dl_plan* plan, uint32_t steps);
+/* Diagnostic: steps enqueued since the current generation started. */
+int dl_plan_steps_enqueued(dl_plan* plan, uint64_t* steps);
 
 /* ------------------------------------------ NLA injection and steering */
 /* DeviceInjection (src/inference/injection/device.h:29-47; kernel
