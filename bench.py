@@ -112,6 +112,26 @@ def other_configs(device, queue, model, cfg, seed, pplan, long_prompt):
                                  "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
         log(f"config 3: decode at {n + 1}..{n + max_new - 1} keys {ms * 1e3:.1f} us/token = {1000.0 / ms:.1f} tok/s "
             f"({gbs / HBM_PEAK_GBS:.1%} of HBM peak)")
+        # The long-context attention kernels, live, at the last decode
+        # position (4608 visible keys), cycling layers.
+        from dolittle_amd import _lib
+        _lib.call("dl_plan_bench_prepare", pplan.handle)
+        keys = n + max_new
+        kv = keys * 2 * cfg.kv_heads * cfg.head_dim * 2
+        attn = {}
+        for which, name in ((1, "k_attn_qk"), (2, "k_attn_softmax"), (3, "k_attn_pv")):
+            _lib.call("dl_plan_launch_kernel", pplan.handle, which, 0, 2)
+            ea, eb = Event(device), Event(device)
+            queue.drain()
+            ea.record(queue)
+            _lib.call("dl_plan_launch_kernel", pplan.handle, which, 0, 72)
+            eb.record(queue)
+            attn[name] = round(ea.elapsed_ms(eb) * 1e3 / 72, 2)
+        total = sum(attn.values())
+        attn.update({"keys": keys, "kv_bytes": kv, "total_us": round(total, 2),
+                     "hbm_frac": round(kv / (total * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        out["config3_attention"] = attn
+        log(f"config 3: attention at {keys} keys: {attn}")
 
     # Config 4: batch 2, 256-id prompt, 256 tokens; plain, then capture of
     # block 24 at every position for both sequences plus an FP32 steering

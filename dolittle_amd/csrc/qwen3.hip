@@ -29,6 +29,7 @@
 #include <cstring>
 #include <memory>
 #include <thread>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -414,30 +415,58 @@ struct AttnArgs {
 
 // Grid (kv head, 64-key tile, sequence); block 256 = 4 waves, one per query
 // head of the group.  Scores use 8 lanes per key, each an FMA chain over 16
-// contiguous features, merged at offsets 4,2,1 (attention.cu:231-300).
+// contiguous features, merged at offsets 4,2,1 (attention.cu:231-300).  The
+// tile's 64 cached key rows do not depend on this token: they are issued at
+// entry, with the head operands, so one memory latency covers both.
 __global__ __launch_bounds__(kBlock) void k_attn_qk(AttnArgs a) {
   __shared__ float qs[4][kHeadDim];
   __shared__ float ks[kHeadDim];
-  if (!a.ctl->active) return;
   const int g = blockIdx.x, key0 = blockIdx.y * 64, b = blockIdx.z;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int kl = lane / 8, l = lane % 8;
+  const int group = a.q_heads / a.kv_heads;
+  const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHeadDim, kw = static_cast<uint64_t>(a.kv_heads) * kHeadDim;
+  uint16_t* kc = a.k_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g) * a.cap * kHeadDim;
+  // Rows key0 .. key0 + 63 lie inside the cache (its capacity is a multiple
+  // of 64); rows at or past the position are loaded but never used.
+  u32x4 kpre[2][2];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const u32x4* src =
+        reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(key0 + wave * 16 + it * 8 + kl) * kHeadDim + 16 * l);
+    kpre[it][0] = src[0];
+    kpre[it][1] = src[1];
+  }
+  HeadOperands qh{}, kh{};
+  {
+    const uint16_t* x = a.q_raw + b * qw + static_cast<uint64_t>(g * group + wave) * kHeadDim;
+    qh.xa = dl_bf16_to_f32(x[lane]);
+    qh.xb = dl_bf16_to_f32(x[lane + 64]);
+    qh.ga = dl_bf16_to_f32(a.q_norm[lane]);
+    qh.gb = dl_bf16_to_f32(a.q_norm[lane + 64]);
+  }
+  if (wave == 0) {
+    const uint16_t* x = a.k_raw + b * kw + static_cast<uint64_t>(g) * kHeadDim;
+    kh.xa = dl_bf16_to_f32(x[lane]);
+    kh.xb = dl_bf16_to_f32(x[lane + 64]);
+    kh.ga = dl_bf16_to_f32(a.k_norm[lane]);
+    kh.gb = dl_bf16_to_f32(a.k_norm[lane + 64]);
+  }
+  if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position + static_cast<uint64_t>(b) * a.pos_step;
   const int count = static_cast<int>(pos) + 1;
   if (key0 >= count) return;
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int group = a.q_heads / a.kv_heads;
   const float* rope_pos = a.rope + pos * kHeadDim;
-  const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHeadDim, kw = static_cast<uint64_t>(a.kv_heads) * kHeadDim;
-  head_norm_rope(a.q_raw + b * qw + static_cast<uint64_t>(g * group + wave) * kHeadDim, a.q_norm, rope_pos, lane,
-                 a.eps, qs[wave]);
+  qh.cosine = kh.cosine = rope_pos[2 * lane];
+  qh.sine = kh.sine = rope_pos[2 * lane + 1];
+  head_norm_rope(qh, lane, a.eps, qs[wave]);
   const bool has_new = pos >= static_cast<uint64_t>(key0) && pos < static_cast<uint64_t>(key0) + 64;
-  uint16_t* kc = a.k_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g) * a.cap * kHeadDim;
   if (has_new && wave == 0) {
-    head_norm_rope(a.k_raw + b * kw + static_cast<uint64_t>(g) * kHeadDim, a.k_norm, rope_pos, lane, a.eps, ks);
+    head_norm_rope(kh, lane, a.eps, ks);
     kc[pos * kHeadDim + lane] = bf16_bits(ks[lane]);
     kc[pos * kHeadDim + lane + 64] = bf16_bits(ks[lane + 64]);
   }
   __syncthreads();
-  const int kl = lane / 8, l = lane % 8;
   float q[4][16];
 #pragma unroll
   for (int h = 0; h < 4; ++h)
@@ -453,8 +482,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_qk(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) kf[i] = ks[16 * l + i];
       } else {
-        const u32x4* src = reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(j) * kHeadDim + 16 * l);
-        const u32x4 w0 = src[0], w1 = src[1];
+        const u32x4 w0 = kpre[it][0], w1 = kpre[it][1];
         kf[0] = dl_bf16_lo(w0.x); kf[1] = dl_bf16_hi(w0.x); kf[2] = dl_bf16_lo(w0.y); kf[3] = dl_bf16_hi(w0.y);
         kf[4] = dl_bf16_lo(w0.z); kf[5] = dl_bf16_hi(w0.z); kf[6] = dl_bf16_lo(w0.w); kf[7] = dl_bf16_hi(w0.w);
         kf[8] = dl_bf16_lo(w1.x); kf[9] = dl_bf16_hi(w1.x); kf[10] = dl_bf16_lo(w1.y); kf[11] = dl_bf16_hi(w1.y);
@@ -477,31 +505,34 @@ __global__ __launch_bounds__(kBlock) void k_attn_qk(AttnArgs a) {
   }
 }
 
-// Grid (query head, sequence).  m = max, e = exp(s - m), denominator from 32
-// partials owning j mod 32 merged at offsets 16..1, p = e / l
-// (attention.cu:301-330).  Each thread issues its score loads 16 at a time
-// before using any (indices clamped to the last key, which leaves the max
-// unchanged), and each partial reads its keys from LDS 16 at a time.
+// Grid (query head, sequence), 1024 threads.  m = max, e = exp(s - m),
+// denominator from 32 partials owning j mod 32 merged at offsets 16..1,
+// p = e / l (attention.cu:301-330).  Every thread issues all of its score
+// loads before using any (indices clamped to the last key, which leaves the
+// max unchanged); each partial reads its terms from LDS 16 at a time and
+// adds them in ascending key order.
 constexpr int kSoftmaxChunk = 16;
+constexpr int kSoftmaxThreads = 1024;
+constexpr int kSoftmaxLoads = 8;  // scores per thread in flight: 8192 keys per pass
 
-__global__ __launch_bounds__(kBlock) void k_attn_softmax(AttnArgs a) {
+__global__ __launch_bounds__(kSoftmaxThreads) void k_attn_softmax(AttnArgs a) {
   extern __shared__ float es[];
-  __shared__ float wave_max[kBlock / 64];
+  __shared__ float wave_max[kSoftmaxThreads / 64];
   __shared__ float denominator_shared;
   if (!a.ctl->active) return;
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int count = static_cast<int>(a.ctl->position + static_cast<uint64_t>(b) * a.pos_step) + 1;
   const uint64_t row = (static_cast<uint64_t>(b) * a.q_heads + h) * a.cap;
   const float* sc = a.scores + row;
-  float m = sc[0];
-  for (int base = 0; base < count; base += kBlock * kSoftmaxChunk) {
-    float s[kSoftmaxChunk];
+  float m = -INFINITY;
+  for (int base = 0; base < count; base += kSoftmaxThreads * kSoftmaxLoads) {
+    float s[kSoftmaxLoads];
 #pragma unroll
-    for (int i = 0; i < kSoftmaxChunk; ++i) s[i] = sc[min(base + tid + i * kBlock, count - 1)];
+    for (int i = 0; i < kSoftmaxLoads; ++i) s[i] = sc[min(base + tid + i * kSoftmaxThreads, count - 1)];
 #pragma unroll
-    for (int i = 0; i < kSoftmaxChunk; ++i) {
+    for (int i = 0; i < kSoftmaxLoads; ++i) {
       m = fmaxf(m, s[i]);
-      const int j = base + tid + i * kBlock;
+      const int j = base + tid + i * kSoftmaxThreads;
       if (j < count) es[j] = s[i];
     }
   }
@@ -510,8 +541,8 @@ __global__ __launch_bounds__(kBlock) void k_attn_softmax(AttnArgs a) {
   if (tid % 64 == 0) wave_max[tid / 64] = m;
   __syncthreads();
 #pragma unroll
-  for (int w = 0; w < kBlock / 64; ++w) m = fmaxf(m, wave_max[w]);
-  for (int j = tid; j < count; j += kBlock) es[j] = dl_expf(es[j] - m);
+  for (int w = 0; w < kSoftmaxThreads / 64; ++w) m = fmaxf(m, wave_max[w]);
+  for (int j = tid; j < count; j += kSoftmaxThreads) es[j] = dl_expf(es[j] - m);
   __syncthreads();
   if (tid < 32) {
     float p = 0.0f;
@@ -530,160 +561,199 @@ __global__ __launch_bounds__(kBlock) void k_attn_softmax(AttnArgs a) {
   }
   __syncthreads();
   const float l = denominator_shared;
-  for (int j = tid; j < count; j += kBlock) a.probs[row + j] = es[j] / l;
+  for (int j = tid; j < count; j += kSoftmaxThreads) a.probs[row + j] = es[j] / l;
 }
 
-// One PV key of a 64-key block: acc = fma(p, v, acc) with v the BF16 value
-// of key K of this lane's feature and p the probability of key K of this
-// lane's head.  The 16 lanes of a head (one DPP row) hold the block's 64
-// probabilities, 4 per lane; row_newbcast reads lane K / 4 of the row as the
-// multiplicand, so the product needs no separate broadcast instruction.
-// v_fmac_f32 rounds once (fused), as fma_rn does.
-template <int C>
-__device__ inline float pick(const float4& x) {
-  if constexpr (C == 0) return x.x;
-  else if constexpr (C == 1) return x.y;
-  else if constexpr (C == 2) return x.z;
-  else return x.w;
-}
-template <int C>
-__device__ inline uint32_t pick(const u32x4& x) {
-  if constexpr (C == 0) return x.x;
-  else if constexpr (C == 1) return x.y;
-  else if constexpr (C == 2) return x.z;
-  else return x.w;
-}
-template <int K>
-__device__ inline float pv_key(float acc, const float4& pc, const u32x4* vc) {
-  const uint32_t word = pick<(K % 8) / 2>(vc[K / 8]);
-  const float v = (K % 2) ? dl_bf16_hi(word) : dl_bf16_lo(word);
-  asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
-               : "+v"(acc)
-               : "v"(pick<K % 4>(pc)), "v"(v), "n"(K / 4));
-  return acc;
-}
-// The keys lo <= K < hi of a block (all 64 unless kMasked: the first and
-// last block of a range).
-template <bool kMasked, int... K>
-__device__ inline float pv_block(float acc, const float4& pc, const u32x4* vc, int lo, int hi,
-                                 std::integer_sequence<int, K...>) {
-  // Two wait states between any VALU write of the probability registers and
-  // their first DPP read.
-  asm volatile("s_nop 1");
-  ((acc = (!kMasked || (K >= lo && K < hi)) ? pv_key<K>(acc, pc, vc) : acc), ...);
-  return acc;
-}
-
-// Grid (kv head * 8 feature blocks, sequence), 192 threads.  Waves 0 and 1
+// Grid (kv head * 8 feature blocks, sequence), 256 threads.  Waves 0 and 2
 // run the two PV key ranges (the first ceil(n/2) keys and the rest) for the
 // group's 4 query heads x 16 features, lane = (head, feature); each output
 // feature is round(A + B), A and B ascending FMA chains (attention.cu:331-375).
-// V is stored transposed, so a lane reads 8 consecutive keys of its feature
-// per 16-byte load; loads run 3 blocks of 64 keys ahead of the FMAs (the
-// range's unaligned ends are masked blocks of the same pipeline), and one
-// float4 per lane carries its head's 64 probabilities of a block.  Wave 2
-// first touches every V row and probability row the chains read, so the
-// chains' loads hit L2 instead of waiting on HBM.
+//
+// The keys go through LDS in chunks of kPvChunk.  Waves 1 and 3 only copy:
+// each chunk's 32 V rows (BF16, both ranges) and 8 probability rows (FP32)
+// go from global memory straight into a kPvSlots-slot LDS ring
+// (global_load_lds, no registers in flight), kPvSlots - 1 chunks ahead of
+// the chains, with explicit vmcnt waits and plain barriers (a fenced
+// barrier would wait for every copy in flight).  A copy instruction writes
+// 64 x 16 bytes contiguously; its lanes fetch the rows interleaved 16 bytes
+// at a time and its block is padded, so the 16 V rows (and the 4
+// probability rows) a chain wave reads at one key fall in distinct banks.
 constexpr int kPvFeatures = 16;
-constexpr int kPvThreads = 192;
-constexpr int kPvTouchBatch = 32;
-constexpr int kPvBuffers = 4;
+constexpr int kPvThreads = 256;
+constexpr int kPvChunk = 128;
+constexpr int kPvSlots = 6;             // chunks in the copy ring
+constexpr int kPvCopies = 6;            // global_load_lds per producer wave per chunk
+constexpr int kPvBlock = 1024 + 64;     // bytes per copy block in LDS (64 lanes x 16 bytes + pad)
+constexpr int kPvSlotBytes = 12 * kPvBlock;  // 8 V blocks (4 rows each) + 4 probability blocks (2 rows each)
 
-__global__ __launch_bounds__(kPvThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_attn_pv(AttnArgs a) {
+typedef __attribute__((address_space(3))) void pv_lds_void;
+typedef __attribute__((address_space(1))) void pv_global_void;
+
+// s_waitcnt immediate waiting until at most n vector-memory operations of
+// this wave are outstanding (vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt
+// left at their no-wait maxima).
+constexpr unsigned pv_vmcnt(unsigned n) { return 0x0f70u | (n & 0xfu) | ((n >> 4) << 14); }
+
+struct PvSlot {
+  uint8_t bytes[kPvSlotBytes];
+};
+
+__global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
+  __shared__ __align__(16) PvSlot s0, s1, s2, s3, s4, s5;
   __shared__ float second[64];
   if (!a.ctl->active) return;
   constexpr int kBlocksPerGroup = kHeadDim / kPvFeatures;
   const int g = blockIdx.x / kBlocksPerGroup, fb = blockIdx.x % kBlocksPerGroup, b = blockIdx.y;
   const int count = static_cast<int>(a.ctl->position + static_cast<uint64_t>(b) * a.pos_step) + 1;
   const int split = (count - 1) / 2 + 1;
-  // Wave-uniform wave index: the key ranges and loop bounds below stay in
-  // scalar registers, so the loops branch on scalars.
+  // Wave-uniform values in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
   const int group = a.q_heads / a.kv_heads;
   const uint16_t* vbase =
       a.v_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g * kHeadDim + fb * kPvFeatures) * a.cap;
   const float* pbase = a.probs + (static_cast<uint64_t>(b) * a.q_heads + g * group) * a.cap;
-  float acc = 0.0f;
-  if (wave == 2) {
-    // One dword per 128-byte line of the 16 V rows and 4 probability rows.
-    const int v_lines = (count * 2 + 127) / 128, p_lines = (count * 4 + 127) / 128;
-    const int v_total = kPvFeatures * v_lines, total = v_total + group * p_lines;
-    uint32_t x = 0;
-    for (int i = lane; i < total; i += 64 * kPvTouchBatch) {
-      uint32_t t[kPvTouchBatch];
+  // Range r covers keys [begin_r, end_r), staged from the 8-aligned key below
+  // begin_r; chunk c of range r holds keys jb0_r + kPvChunk c + [0, kPvChunk).
+  const int end0 = split, begin1 = split, end1 = count;
+  const int jb0_1 = begin1 & ~7;
+  const int chunks0 = (end0 + kPvChunk - 1) / kPvChunk;
+  const int chunks1 = end1 > begin1 ? (end1 - jb0_1 + kPvChunk - 1) / kPvChunk : 0;
+  const int chunks = max(chunks0, chunks1);
+  // Waves 0 and 2 run the chains (ranges 0 and 1), waves 1 and 3 copy, so
+  // that the two chains do not share a SIMD when a workgroup's consecutive
+  // waves are paired on SIMDs.
+  const bool producer = (wave & 1) != 0;
+
+  // Copy k (0..11) of a chunk fills block k of its slot.  k < 8: V rows
+  // 4k .. 4k + 3 (row = range * 16 + feature); lane L fetches row 4k + L % 4,
+  // keys 8 (L / 4) .. + 7.  k >= 8: probability rows 2(k - 8) + {0, 1}
+  // (row = range * 4 + head); lane L fetches row 2(k - 8) + L % 2, keys
+  // 4 (L / 2) .. + 3.  Sources past a range are clamped to its last 8 (4)
+  // keys, inside the cache rows; the chains never use those values.  The
+  // chunk index is clamped to the last chunk, so every step issues the same
+  // number of copies and waits with the same count.  Producer wave w takes
+  // the copies k = w / 2 + 2 n.
+  auto copy = [&](PvSlot& slot, int c) {
+    c = min(c, chunks - 1);
 #pragma unroll
-      for (int u = 0; u < kPvTouchBatch; ++u) {
-        const int k = min(i + u * 64, total - 1);
-        const uint32_t* src =
-            k < v_total ? reinterpret_cast<const uint32_t*>(vbase + static_cast<uint64_t>(k / v_lines) * a.cap) +
-                              (k % v_lines) * 32
-                        : reinterpret_cast<const uint32_t*>(pbase + static_cast<uint64_t>((k - v_total) / p_lines) *
-                                                                        a.cap) +
-                              ((k - v_total) % p_lines) * 32;
-        t[u] = *src;
+    for (int n = 0; n < kPvCopies; ++n) {
+      const int k = wave / 2 + 2 * n;
+      if (k < 8) {
+        const int row = 4 * k + lane % 4, r = row / kPvFeatures, f = row % kPvFeatures;
+        const int jb0 = r ? jb0_1 : 0, last8 = ((r ? end1 : end0) - 1) & ~7;
+        const int key = max(0, min(jb0 + kPvChunk * c + 8 * (lane / 4), last8));
+        __builtin_amdgcn_global_load_lds((const pv_global_void*)(vbase + static_cast<uint64_t>(f) * a.cap + key),
+                                         (pv_lds_void*)(slot.bytes + k * kPvBlock), 16, 0, 0);
+      } else {
+        const int row = 2 * (k - 8) + lane % 2, r = row / 4, hl = row % 4;
+        const int jb0 = r ? jb0_1 : 0, last4 = ((r ? end1 : end0) - 1) & ~3;
+        const int key = max(0, min(jb0 + kPvChunk * c + 4 * (lane / 2), last4));
+        __builtin_amdgcn_global_load_lds((const pv_global_void*)(pbase + static_cast<uint64_t>(hl) * a.cap + key),
+                                         (pv_lds_void*)(slot.bytes + k * kPvBlock), 16, 0, 0);
       }
-#pragma unroll
-      for (int u = 0; u < kPvTouchBatch; ++u) x ^= t[u];
     }
-    asm volatile("" ::"v"(x));
-  } else {
-    const int hl = lane / kPvFeatures, f = lane % kPvFeatures;
-    const uint16_t* v = vbase + static_cast<uint64_t>(f) * a.cap;
-    const float* p = pbase + static_cast<uint64_t>(hl) * a.cap;
-    const int begin = wave ? split : 0, end = wave ? count : split;
-    // Blocks of 64 keys from the 8-aligned key below `begin`; the first and
-    // last block mask the keys outside [begin, end).  Loads past the range
-    // are clamped to its last 8-key group (last 4 keys for probabilities),
-    // which stays inside the row because the capacity is a multiple of 64;
-    // their values are never used.
-    const int jb0 = begin & ~7;
-    const int blocks = end > begin ? (end - jb0 + 63) / 64 : 0;
-    if (blocks > 0) {
-      const int last8 = (end - 1) & ~7, last4 = (end - 1) & ~3;
-      u32x4 vbuf[kPvBuffers][8];
-      float4 pbuf[kPvBuffers];
-      auto load = [&](int buf, int x) {
-        const int jb = jb0 + 64 * min(x, blocks - 1);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) vbuf[buf][i] = *reinterpret_cast<const u32x4*>(v + min(jb + 8 * i, last8));
-        pbuf[buf] = *reinterpret_cast<const float4*>(p + min(jb + 4 * f, last4));
-      };
-      const auto keys = std::make_integer_sequence<int, 64>{};
-      auto run = [&](int buf, int x) {
-        const int jb = jb0 + 64 * x;
-        const int lo = max(begin - jb, 0), hi = min(end - jb, 64);
-        if (lo == 0 && hi == 64)
-          acc = pv_block<false>(acc, pbuf[buf], vbuf[buf], lo, hi, keys);
-        else
-          acc = pv_block<true>(acc, pbuf[buf], vbuf[buf], lo, hi, keys);
-      };
-#pragma unroll
-      for (int u = 0; u < kPvBuffers - 1; ++u) load(u, u);
-      // Uniform trip count and one exit: the loop head always has the same
-      // kPvBuffers - 1 blocks outstanding.
-      int k = 0;
-      for (; k + kPvBuffers <= blocks; k += kPvBuffers) {
-#pragma unroll
-        for (int u = 0; u < kPvBuffers; ++u) {
-          load((u + kPvBuffers - 1) % kPvBuffers, k + u + kPvBuffers - 1);
-          __builtin_amdgcn_sched_barrier(0);
-          run(u, k + u);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-      // Fewer than kPvBuffers blocks remain, already in buffers 0, 1, ...
-#pragma unroll
-      for (int u = 0; u < kPvBuffers - 1; ++u)
-        if (k + u < blocks) run(u, k + u);
-    }
-    if (wave == 1) second[lane] = acc;
+  };
+
+  if (producer && chunks > 0) {
+    copy(s0, 0);
+    copy(s1, 1);
+    copy(s2, 2);
+    copy(s3, 3);
+    copy(s4, 4);
+    __builtin_amdgcn_s_waitcnt(pv_vmcnt((kPvSlots - 2) * kPvCopies));  // chunk 0 is in s0
   }
+
+  // Chains: wave r runs range r; lane = (head hl, feature f).  V row
+  // r * 16 + f lives in block (r * 16 + f) / 4 at 16-byte piece
+  // 4 g + f % 4 for key group g (8 keys); probability row r * 4 + hl in
+  // block 8 + (r * 4 + hl) / 2 at piece 2 q + hl % 2 for key group q (4 keys).
+  const int hl = lane / kPvFeatures, f = lane % kPvFeatures;
+  const int r = wave / 2;
+  const int begin = r ? begin1 : 0, end = r ? end1 : end0, jb0 = r ? jb0_1 : 0;
+  const int mine = r ? chunks1 : chunks0;
+  const int vrow = r * kPvFeatures + f, prow = r * 4 + hl;
+  const int voff = (vrow / 4) * kPvBlock + (vrow % 4) * 16;
+  const int poff = (8 + prow / 2) * kPvBlock + (prow % 2) * 16;
+  float acc = 0.0f;
+  // Step c: after the barrier the chains run chunk c from slot c % kPvSlots
+  // while the producers copy chunk c + kPvSlots - 1 into chunk c - 1's slot
+  // and wait until chunk c + 1 has landed.  `chunks` is uniform, so every
+  // wave meets every barrier.
+  auto step = [&](int c, const PvSlot& cur, PvSlot& ahead) {
+    __builtin_amdgcn_s_barrier();  // chunk c is in `cur`; every chain is done with chunk c - 1
+    if (producer) {
+      copy(ahead, c + kPvSlots - 1);
+      __builtin_amdgcn_s_waitcnt(pv_vmcnt((kPvSlots - 2) * kPvCopies));
+      return;
+    }
+    if (c >= mine) return;
+    const uint8_t* vb = cur.bytes + voff;
+    const uint8_t* pb = cur.bytes + poff;
+    const int cs = jb0 + kPvChunk * c;
+    const int lo = max(begin - cs, 0), hi = min(end - cs, kPvChunk);
+    auto eight = [&](int q, bool masked) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(vb + 64 * q);
+      const float4 pa = *reinterpret_cast<const float4*>(pb + 32 * (2 * q));
+      const float4 pc = *reinterpret_cast<const float4*>(pb + 32 * (2 * q + 1));
+      const float vv[8] = {dl_bf16_lo(w.x), dl_bf16_hi(w.x), dl_bf16_lo(w.y), dl_bf16_hi(w.y),
+                           dl_bf16_lo(w.z), dl_bf16_hi(w.z), dl_bf16_lo(w.w), dl_bf16_hi(w.w)};
+      const float pp[8] = {pa.x, pa.y, pa.z, pa.w, pc.x, pc.y, pc.z, pc.w};
+      if (!masked) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fma_rn(pp[e], vv[e], acc);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (8 * q + e >= lo && 8 * q + e < hi) acc = fma_rn(pp[e], vv[e], acc);
+      }
+    };
+    if (lo == 0 && hi == kPvChunk) {
+      // The reads of group q + kAhead are issued before the FMAs of group
+      // q (the order is pinned with scheduling barriers), so the LDS
+      // latency hides behind the chain and the waits stay partial (at most
+      // 3 kAhead reads are outstanding; the wait counter has 4 bits).  The
+      // chain then runs at the rate of its two VALU instructions per key
+      // (widen, FMA).
+      constexpr int kGroups = kPvChunk / 8, kAhead = 3;
+      u32x4 w[kGroups];
+      float4 pa[kGroups], pc[kGroups];
+      auto read = [&](int q) {
+        w[q] = *reinterpret_cast<const u32x4*>(vb + 64 * q);
+        pa[q] = *reinterpret_cast<const float4*>(pb + 32 * (2 * q));
+        pc[q] = *reinterpret_cast<const float4*>(pb + 32 * (2 * q + 1));
+      };
+#pragma unroll
+      for (int q = 0; q < kAhead; ++q) read(q);
+#pragma unroll
+      for (int q = 0; q < kGroups; ++q) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (q + kAhead < kGroups) read(q + kAhead);
+        __builtin_amdgcn_sched_barrier(0);
+        const float vv[8] = {dl_bf16_lo(w[q].x), dl_bf16_hi(w[q].x), dl_bf16_lo(w[q].y), dl_bf16_hi(w[q].y),
+                             dl_bf16_lo(w[q].z), dl_bf16_hi(w[q].z), dl_bf16_lo(w[q].w), dl_bf16_hi(w[q].w)};
+        const float pp[8] = {pa[q].x, pa[q].y, pa[q].z, pa[q].w, pc[q].x, pc[q].y, pc[q].z, pc[q].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fma_rn(pp[e], vv[e], acc);
+      }
+    } else {
+      for (int q = lo / 8; q * 8 < hi; ++q) eight(q, true);
+    }
+  };
+  static_assert(kPvSlots == 6 && (kPvSlots - 2) * kPvCopies <= 63, "the ring below is unrolled for 6 slots");
+  for (int c0 = 0; c0 < chunks; c0 += kPvSlots) {
+    step(c0, s0, s5);
+    if (c0 + 1 < chunks) step(c0 + 1, s1, s0);
+    if (c0 + 2 < chunks) step(c0 + 2, s2, s1);
+    if (c0 + 3 < chunks) step(c0 + 3, s3, s2);
+    if (c0 + 4 < chunks) step(c0 + 4, s4, s3);
+    if (c0 + 5 < chunks) step(c0 + 5, s5, s4);
+  }
+  if (producer) __builtin_amdgcn_s_waitcnt(pv_vmcnt(0));  // no copy outstanding at exit
+  if (wave == 2) second[lane] = acc;
   __syncthreads();
-  if (wave == 0) {
-    const int hl = lane / kPvFeatures, f = lane % kPvFeatures;
+  if (wave == 0)
     a.att[static_cast<uint64_t>(b) * a.q_heads * kHeadDim + (g * group + hl) * kHeadDim + fb * kPvFeatures + f] =
         bf16_bits(acc + second[lane]);
-  }
 }
 
 // Short-context attention in one kernel (the reference's retained-score
@@ -2164,7 +2234,7 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       });
       break;
     case 1: k_attn_qk<<<dim3(c.kv_heads, p->cap / 64, B), kBlock, 0, s>>>(aa); break;
-    case 2: k_attn_softmax<<<dim3(c.q_heads, B), kBlock, size_t(p->cap) * sizeof(float), s>>>(aa); break;
+    case 2: k_attn_softmax<<<dim3(c.q_heads, B), kSoftmaxThreads, size_t(p->cap) * sizeof(float), s>>>(aa); break;
     case 3: k_attn_pv<<<dim3(c.kv_heads * (kHeadDim / kPvFeatures), B), kPvThreads, 0, s>>>(aa); break;
     case 8: k_attn_fused<<<dim3(c.q_heads, B), kAttnThreads, 0, s>>>(aa); break;
     case 9: k_append_keys<<<dim3(c.kv_heads, B), 64, 0, s>>>(aa); break;

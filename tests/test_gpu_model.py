@@ -125,7 +125,7 @@ def test_config1_single_block_decode(device, queue, oracle):
     assert np.array_equal(plan.logits(0), oracle.logits(w, run.h))
 
 
-@pytest.mark.parametrize("position", [77, 1023, 1024, 1089, 1500, 1543, 4607])
+@pytest.mark.parametrize("position", [1, 63, 64, 77, 383, 511, 512, 513, 777, 1023, 1024, 1089, 1500, 1543, 4607])
 def test_single_block_both_attention_paths(device, queue, oracle, position):
     """Positions below 1024 run the fused short-context attention kernel,
     positions from 1024 the three-kernel split; both equal the oracle, up to
