@@ -26,6 +26,7 @@ import time
 
 import numpy as np
 
+ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense BF16 MFMA, MI355X
 METRIC = "Qwen3-8B batch-1 decode tokens/s on 1 MI355X; % HBM roofline; prefill tok/s"
@@ -118,7 +119,7 @@ def other_configs(device, queue, model, cfg, seed, pplan, long_prompt):
         _lib.call("dl_plan_bench_prepare", pplan.handle)
         keys = n + max_new
         kv = keys * 2 * cfg.kv_heads * cfg.head_dim * 2
-        attn = {}
+        attn, total = {}, 0.0
         for which, name in ((1, "k_attn_qk"), (2, "k_attn_softmax"), (3, "k_attn_pv")):
             _lib.call("dl_plan_launch_kernel", pplan.handle, which, 0, 2)
             ea, eb = Event(device), Event(device)
@@ -126,8 +127,14 @@ def other_configs(device, queue, model, cfg, seed, pplan, long_prompt):
             ea.record(queue)
             _lib.call("dl_plan_launch_kernel", pplan.handle, which, 0, 72)
             eb.record(queue)
-            attn[name] = round(ea.elapsed_ms(eb) * 1e3 / 72, 2)
-        total = sum(attn.values())
+            us = ea.elapsed_ms(eb) * 1e3 / 72
+            alg = attention_bytes(cfg, which, keys)
+            gbs = alg / (us * 1e-6) / 1e9
+            attn[name] = {"us": round(us, 2), "algorithmic_bytes": alg, "GB/s": round(gbs, 1),
+                          "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            if keys == TRAFFIC_KEYS["long"]:
+                attn[name]["traffic"] = load_traffic(name)[0]
+            total += us
         attn.update({"keys": keys, "kv_bytes": kv, "total_us": round(total, 2),
                      "hbm_frac": round(kv / (total * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
         out["config3_attention"] = attn
@@ -173,14 +180,35 @@ def other_configs(device, queue, model, cfg, seed, pplan, long_prompt):
     return out
 
 
+def cpu_info():
+    """This host's logical CPU count, the CPUs this process may run on and
+    the CPU model."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "model": name}
+
+
+def cpu_threads():
+    """Every CPU this job is given: OMP_NUM_THREADS where the host sets it
+    (the GPU host gives each one-GPU job a share of its cores that way), else
+    the CPUs of this process's affinity mask."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else len(os.sched_getaffinity(0))
+
+
 def cpu_baseline(model, plan, context, threads, seconds=10.0):
     """Times the CPU contract restatement on a bounded sample of the decode
-    workload: whole tokens (36 block steps, then the final norm + LM head)
-    at `context` cached keys, repeated for at least `seconds`.  Layer 0's
-    weights and KV rows (copied from the device) stand in for every block,
-    which has the same shapes and arithmetic; each block step appends one
-    position to the CPU cache."""
-    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle"))
+    workload: whole tokens (the 36 block steps, each with its own block's
+    weights and KV rows copied from the device, then the final norm + LM
+    head) from `context` cached keys, repeated for at least `seconds`."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as o
     lib = o.lib()
     lib.or_set_threads(threads)
@@ -190,46 +218,201 @@ def cpu_baseline(model, plan, context, threads, seconds=10.0):
     roles = (("input_norm", "input_norm"), ("wq", "q"), ("wk", "k"), ("wv", "v"), ("q_norm", "q_norm"),
              ("k_norm", "k_norm"), ("wo", "o"), ("post_norm", "post_norm"), ("wg", "gate"), ("wu", "up"),
              ("wd", "down"))
-    block = {name: np.ascontiguousarray(model.read(role, 0).reshape(-1)) for name, role in roles}
+    blocks = [{name: np.ascontiguousarray(model.read(role, layer).reshape(-1)) for name, role in roles}
+              for layer in range(cfg.layers)]
     lm = np.ascontiguousarray(model.read("lm_head").reshape(-1))
-    weights = o.Qwen3Weights(dims, [block], np.ascontiguousarray(model.read("final_norm")), lm, lm)
+    weights = o.Qwen3Weights(dims, blocks, np.ascontiguousarray(model.read("final_norm")), lm, lm)
     kw = cfg.kv_heads * cfg.head_dim
-    max_tokens = 64
-    capacity = context + max_tokens * cfg.layers + 1
-    k = np.zeros(capacity * kw, np.uint16)
-    v = np.zeros(capacity * kw, np.uint16)
-    keys, values = plan.read_cache(0, 0, context)
-    k[: context * kw] = keys
-    v[: context * kw] = values
+    max_tokens = 512
+    capacity = context + max_tokens + 1
+    caches = []
+    for layer in range(cfg.layers):
+        k = np.zeros(capacity * kw, np.uint16)
+        v = np.zeros(capacity * kw, np.uint16)
+        keys, values = plan.read_cache(layer, 0, context)
+        k[: context * kw] = keys
+        v[: context * kw] = values
+        caches.append((k, v))
     h0 = np.ascontiguousarray(plan.hidden(0))
     tokens, position = 0, context
     t0 = time.perf_counter()
     while tokens < max_tokens and (tokens == 0 or time.perf_counter() - t0 < seconds):
         h = h0.copy()
-        for _ in range(cfg.layers):
-            o.block_forward(weights, 0, h, 1, position, k, v)
-            position += 1
+        for layer in range(cfg.layers):
+            o.block_forward(weights, layer, h, 1, position, *caches[layer])
         o.logits(weights, h)
+        position += 1
         tokens += 1
     elapsed = time.perf_counter() - t0
+    info = cpu_info()
     return {
         "value": round(tokens / elapsed, 4),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"CPU contract restatement (oracle/, C, -O3, {threads} OpenMP threads): {tokens} whole decode "
-                   f"tokens ({cfg.layers} block steps + final norm + LM head each) from {context} cached keys, "
-                   f"{elapsed:.1f} s; layer 0's weights stand in for every block"),
+        "nproc": info["nproc"],
+        "affinity_cpus": info["affinity"],
+        "cpu_model": info["model"],
+        "sample": (f"CPU contract restatement (oracle/, C, -O3, {threads} OpenMP threads = every CPU this job is "
+                   f"given; host nproc {info['nproc']}, {info['model']}): {tokens} whole decode tokens "
+                   f"({cfg.layers} block steps with each block's own weights and KV rows + final norm + LM head) "
+                   f"from {context} cached keys, {elapsed:.1f} s"),
     }
 
 
-def load_traffic():
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_gateup.json")
-    if not os.path.exists(path):
-        return None
-    with open(path) as f:
+# The decode kernels the HBM-traffic counter runs measure, in launch order:
+# (hook index of dl_plan_launch_kernel, kernel name as rocprofv3 reports it
+# with the namespace stripped (a prefix), launches, plan).  The "short" plan
+# sits at 384 visible keys (the bench's last decode position), the "long" one
+# at 4608 (config 3's last).
+TRAFFIC_KERNELS = (
+    (0, "k_qkv<1, 0, 1>", 8, "short"),
+    (4, "k_residual<16, 1, 1>", 8, "short"),
+    (5, "k_gateup<1>", 8, "short"),
+    (6, "k_residual<32, 1, 1>", 8, "short"),
+    (7, "k_lm_head<1>", 4, "short"),
+    (8, "k_attn_fused", 8, "short"),
+    (1, "k_attn_qk", 8, "long"),
+    (2, "k_attn_softmax", 8, "long"),
+    (3, "k_attn_pv", 8, "long"),
+)
+TRAFFIC_KEYS = {"short": 384, "long": 4608}
+TRAFFIC_COPY_BYTES = 256 << 20
+TRAFFIC_LAYERS = 4
+TRAFFIC_PATH = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def attention_bytes(cfg, which, keys):
+    """Algorithmic bytes of one attention launch at batch 1 over `keys`
+    visible keys: BF16 K and V rows of one layer, FP32 scores and
+    probabilities of the 32 query heads, the BF16 query / key / output rows."""
+    KW, QW = cfg.kv_heads * cfg.head_dim, cfg.q_heads * cfg.head_dim
+    rows, scores = keys * KW * 2, cfg.q_heads * keys * 4
+    return {
+        1: rows + scores + QW * 2 + 2 * KW * 2,      # K rows, scores out, q / k in, k append
+        2: 2 * scores,                               # scores in, probabilities out
+        3: rows + scores + QW * 2,                   # V rows, probabilities in, att out
+        8: 2 * rows + QW * 2 + 2 * KW * 2 + QW * 2,  # K and V rows, q / k in, k append, att out
+    }[which]
+
+
+def launch_bytes(cfg, which, keys):
+    return attention_bytes(cfg, which, keys) if which in (1, 2, 3, 8) else kernel_bytes(cfg, which)
+
+
+def sources_digest():
+    """SHA-256 over the backend's sources and build script: counter results
+    are valid only for the kernels they were measured on."""
+    import hashlib
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "dolittle_amd", "csrc")
+    paths = sorted(os.path.join(csrc, n) for n in os.listdir(csrc) if n.endswith((".hip", ".h", ".cpp")))
+    for path in paths + [os.path.join(ROOT, "dolittle_amd", "build.py")]:
+        h.update(os.path.basename(path).encode() + b"\0")
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def traffic_driver(device, queue, seed):
+    """The program the two counter runs profile (rocprofv3 --pmc FETCH_SIZE,
+    then WRITE_SIZE): Qwen3-8B blocks (4 of them; every block has the same
+    shapes) with the full 151,936-row LM head, two plans brought to 384 and
+    4608 visible keys, then TRAFFIC_KERNELS' launches, then three copies of
+    256 MiB device to device, the calibration of known size."""
+    from dolittle_amd import _lib
+    from dolittle_amd.qwen3 import Plan, Qwen3Config, Qwen3Model
+    cfg = Qwen3Config(layers=TRAFFIC_LAYERS)
+    model = Qwen3Model(device, queue, cfg)
+    model.fill_synthetic(seed, 0.02)
+    rng = np.random.default_rng(seed)
+    plans = {}
+    for name, keys in TRAFFIC_KEYS.items():
+        prompt = rng.integers(0, cfg.vocab, keys - 2).astype(np.uint32)
+        plan = Plan(model, batch=1, capacity=keys + 1)
+        plan.prefill(prompt, mfma=True)
+        plan.generate(prompt, 2)
+        _, results = plan.collect()
+        assert results[0]["position"] == keys, results
+        _lib.call("dl_plan_bench_prepare", plan.handle)
+        plans[name] = plan
+    queue.drain()
+    log("traffic driver: measured launches")
+    for which, _, count, plan in TRAFFIC_KERNELS:
+        _lib.call("dl_plan_launch_kernel", plans[plan].handle, which, 0, count)
+    a, b = device.allocate(TRAFFIC_COPY_BYTES), device.allocate(TRAFFIC_COPY_BYTES)
+    for _ in range(3):
+        queue.copy(b, a, TRAFFIC_COPY_BYTES)
+    queue.drain()
+    log("traffic driver done")
+
+
+def traffic_summary(fetch_csv, write_csv):
+    """Reads the counter CSVs of the two runs of traffic_driver and writes
+    profiles/traffic.json: per kernel the mean FETCH_SIZE / WRITE_SIZE (KiB
+    per dispatch) of its measured launches (the last dispatches of that
+    name), each scaled by what the counter reads for the 256 MiB copy."""
+    import csv
+    from dolittle_amd.qwen3 import Qwen3Config
+    cfg = Qwen3Config()
+    per = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        got = []
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == counter:
+                    name = r["Kernel_Name"].replace("void ", "").replace("dl::(anonymous namespace)::", "")
+                    got.append((int(r["Dispatch_Id"]), name, float(r["Counter_Value"])))
+        got.sort()
+        per[counter] = got
+
+    def last(counter, match, count):
+        vals = [v for _, n, v in per[counter] if match(n)][-count:]
+        if len(vals) != count:
+            raise SystemExit(f"{counter}: found {len(vals)} of {count} dispatches")
+        return sum(vals) / count
+
+    copy = lambda n: "copyBuffer" in n  # noqa: E731
+    kib = TRAFFIC_COPY_BYTES / 1024
+    fetch_copy, write_copy = last("FETCH_SIZE", copy, 3), last("WRITE_SIZE", copy, 3)
+    ff, wf = kib / fetch_copy, kib / write_copy
+    kernels = {}
+    for which, prefix, count, plan in TRAFFIC_KERNELS:
+        match = lambda n, p=prefix: n.startswith(p)  # noqa: E731
+        fetch, write = last("FETCH_SIZE", match, count), last("WRITE_SIZE", match, count)
+        hbm = round((fetch * ff + write * wf) * 1024)
+        alg = launch_bytes(cfg, which, TRAFFIC_KEYS[plan])
+        kernels[prefix] = {"hook": which, "keys": TRAFFIC_KEYS[plan], "dispatches": count,
+                           "fetch_size_kib": round(fetch, 2), "write_size_kib": round(write, 2),
+                           "hbm_bytes_per_launch": hbm, "algorithmic_bytes_per_launch": alg,
+                           "traffic_over_algorithmic": round(hbm / alg, 4)}
+        log(f"{prefix:<24} fetch {fetch:12.2f} KiB  write {write:10.2f} KiB  -> {hbm:>12,} B  "
+            f"({hbm / alg:.3f} x algorithmic)")
+    out = {"sources_sha256": sources_digest(),
+           "copy_calibration": {"bytes": TRAFFIC_COPY_BYTES, "fetch_size_kib": round(fetch_copy, 2),
+                                "write_size_kib": round(write_copy, 2), "fetch_factor": round(ff, 5),
+                                "write_factor": round(wf, 5)},
+           "kernels": kernels,
+           "command": "rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) -- python3 bench.py --traffic-driver; "
+                      "python3 bench.py --traffic-summary FETCH.csv WRITE.csv"}
+    with open(TRAFFIC_PATH, "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    log(f"wrote {TRAFFIC_PATH}")
+
+
+def load_traffic(prefix):
+    """HBM bytes per launch of one kernel from profiles/traffic.json, or
+    (None, reason) when absent or measured on other sources."""
+    if not os.path.exists(TRAFFIC_PATH):
+        return None, "no counter measurement"
+    with open(TRAFFIC_PATH) as f:
         data = json.load(f)
-    return data.get("hbm_bytes_per_launch")
+    if data.get("sources_sha256") != sources_digest():
+        return None, "stale: counters were measured on other kernel sources"
+    entry = data["kernels"].get(prefix)
+    return (entry["hbm_bytes_per_launch"], "rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated") if entry \
+        else (None, "kernel not measured")
 
 
 def main() -> int:
@@ -242,8 +425,10 @@ def main() -> int:
     ap.add_argument("--kernel-iters", type=int, default=72)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-driver", action="store_true",
-                    help="only launch k_gateup 20 times and copy 256 MiB three times "
+                    help="only launch the decode kernels a few times each and copy 256 MiB three times "
                          "(the program run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/traffic.json from the two counter runs' CSVs (no GPU)")
     ap.add_argument("--mfma-prompt", type=int, default=4096,
                     help="prompt length of the MFMA prefill measurement (0 skips it)")
     ap.add_argument("--no-other-configs", action="store_true",
@@ -251,6 +436,9 @@ def main() -> int:
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (PMC scaling reference)")
     args = ap.parse_args()
+    if args.traffic_summary:
+        traffic_summary(*args.traffic_summary)
+        return 0
     if args.gpus != 1:
         print("bench.py measures one MI355X: this backend has no multi-GPU path; run with --gpus 1",
               file=sys.stderr)
@@ -262,21 +450,7 @@ def main() -> int:
     device = Device(0)
     queue = device.create_queue()
     if args.traffic_driver:
-        # The gate/up kernel is identical in every block; two blocks and a
-        # short vocabulary keep the counter runs short.
-        small = Qwen3Model(device, queue, Qwen3Config(layers=2, vocab=2048))
-        small.fill_synthetic(args.seed, 0.02)
-        tplan = Plan(small, batch=1, capacity=256)
-        tplan.generate(list(range(10, 40)), 2)
-        tplan.collect()
-        _lib.call("dl_plan_bench_prepare", tplan.handle)
-        _lib.call("dl_plan_launch_kernel", tplan.handle, 5, 0, 20)
-        n = 256 << 20
-        a, b = device.allocate(n), device.allocate(n)
-        for _ in range(3):
-            queue.copy(b, a, n)
-        queue.drain()
-        log("traffic driver done")
+        traffic_driver(device, queue, args.seed)
         return 0
     cfg = Qwen3Config()
     t0 = time.perf_counter()
@@ -322,9 +496,12 @@ def main() -> int:
     # launch streams distinct weights.
     _lib.call("dl_plan_bench_prepare", plan.handle)
     kernels = {}
+    prefixes = {which: prefix for which, prefix, _, _ in TRAFFIC_KERNELS}
     names = {0: "k_qkv", 4: "k_residual<16> (O)", 5: "k_gateup", 6: "k_residual<32> (down)", 7: "k_lm_head",
              8: "k_attn_fused"}
-    attn_keys = args.prompt + args.warmup + args.steps
+    # The bench control sits at the last consumed position: every position
+    # so far is a visible key.
+    attn_keys = args.prompt + max_new
     for which in (5, 7, 0, 6, 4, 8):
         iters = args.kernel_iters if which != 7 else max(8, args.kernel_iters // 8)
         _lib.call("dl_plan_launch_kernel", plan.handle, which, 0, 2)  # warm
@@ -334,15 +511,17 @@ def main() -> int:
         _lib.call("dl_plan_launch_kernel", plan.handle, which, 0, iters)
         eb.record(queue)
         us = ea.elapsed_ms(eb) * 1e3 / iters
+        alg = launch_bytes(cfg, which, attn_keys)
+        gbs = alg / (us * 1e-6) / 1e9
+        entry = {"us": round(us, 2), "algorithmic_bytes": alg, "GB/s": round(gbs, 1),
+                 "frac": round(gbs / HBM_PEAK_GBS, 4)}
         if which == 8:
-            # K and V rows of one layer at the bench position (the four query
-            # heads of a group share them through L2).
-            kv = attn_keys * 2 * cfg.kv_heads * cfg.head_dim * 2
-            kernels[names[which]] = {"us": round(us, 2), "keys": attn_keys, "kv_bytes": kv}
-            log(f"  {names[which]:<24} {us:8.2f} us  ({attn_keys} keys)")
-            continue
-        gbs = kernel_bytes(cfg, which) / (us * 1e-6) / 1e9
-        kernels[names[which]] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            # The four query heads of a group share their K and V rows
+            # through L2: the bytes count each row once.
+            entry["keys"] = attn_keys
+        if which != 8 or attn_keys == TRAFFIC_KEYS["short"]:
+            entry["traffic"] = load_traffic(prefixes[which])[0]
+        kernels[names[which]] = entry
         log(f"  {names[which]:<24} {us:8.2f} us  {gbs:7.0f} GB/s  {gbs / HBM_PEAK_GBS:.1%}")
     dominant = kernels["k_gateup"]
 
@@ -399,12 +578,13 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        threads = cpu_threads()
         t0 = time.perf_counter()
         cpu = cpu_baseline(model, plan, int(mean_context), threads)
         log(f"cpu baseline: {cpu['value']} tok/s ({time.perf_counter() - t0:.1f}s)")
 
     gateup_bytes = kernel_bytes(cfg, 5)
+    gateup_traffic, gateup_traffic_source = load_traffic(prefixes[5])
     line = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -438,7 +618,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": dominant["frac"],
-            "traffic": load_traffic(),
+            "traffic": gateup_traffic,
+            "traffic_source": gateup_traffic_source,
             "algorithmic_bytes_per_launch": gateup_bytes,
             "avg_launch_us": dominant["us"],
         },

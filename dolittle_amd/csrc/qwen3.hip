@@ -602,8 +602,10 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
   __shared__ __align__(16) PvSlot s0, s1, s2, s3, s4, s5;
   __shared__ float second[64];
   if (!a.ctl->active) return;
-  constexpr int kBlocksPerGroup = kHeadDim / kPvFeatures;
-  const int g = blockIdx.x / kBlocksPerGroup, fb = blockIdx.x % kBlocksPerGroup, b = blockIdx.y;
+  // Group-minor numbering keeps the feature blocks of one K/V group on one
+  // XCD (workgroups are dealt to the XCDs round-robin): its L2 serves the
+  // group's probability rows once for all of them.
+  const int g = blockIdx.x % a.kv_heads, fb = blockIdx.x / a.kv_heads, b = blockIdx.y;
   const int count = static_cast<int>(a.ctl->position + static_cast<uint64_t>(b) * a.pos_step) + 1;
   const int split = (count - 1) / 2 + 1;
   // Wave-uniform values in scalar registers.
@@ -776,10 +778,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
   __shared__ float red[kAttnThreads];
   __shared__ float wave_max[kAttnThreads / 64];
   __shared__ float denominator_shared;
-  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int wave = tid / 64, lane = tid % 64;
+  // Workgroups are dealt to the XCDs round-robin by linear id: numbering the
+  // query heads group-minor puts the heads of one K/V group on one XCD, whose
+  // L2 then serves the group's key and value rows once for all of them.
   const int group = a.q_heads / a.kv_heads;
-  const int g = h / group;
+  const int g = blockIdx.x % a.kv_heads, h = g * group + blockIdx.x / a.kv_heads;
+  const int b = blockIdx.y, tid = threadIdx.x;
+  const int wave = tid / 64, lane = tid % 64;
   const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHeadDim, kw = static_cast<uint64_t>(a.kv_heads) * kHeadDim;
   // This token's q/k rows and their norm gains do not depend on the loop
   // state: they are issued before the control block is read, and the rope
