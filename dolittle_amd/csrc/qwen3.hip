@@ -564,27 +564,32 @@ __global__ __launch_bounds__(kSoftmaxThreads) void k_attn_softmax(AttnArgs a) {
   for (int j = tid; j < count; j += kSoftmaxThreads) a.probs[row + j] = es[j] / l;
 }
 
-// Grid (kv head * 8 feature blocks, sequence), 256 threads.  Waves 0 and 2
-// run the two PV key ranges (the first ceil(n/2) keys and the rest) for the
-// group's 4 query heads x 16 features, lane = (head, feature); each output
-// feature is round(A + B), A and B ascending FMA chains (attention.cu:331-375).
+// Grid (kv head * 32 feature blocks, sequence), 128 threads.  Wave 0 runs
+// both PV key ranges (the first ceil(n/2) keys and the rest) for the group's
+// 4 query heads x 4 features: lane = (range, head, feature) in lanes 0-31;
+// each output feature is round(A + B), A and B ascending FMA chains
+// (attention.cu:331-375).  One wave holds both ranges, so the kernel's VALU
+// time is one wave's chain however the waves are placed on SIMDs.
 //
-// The keys go through LDS in chunks of kPvChunk.  Waves 1 and 3 only copy:
-// each chunk's 32 V rows (BF16, both ranges) and 8 probability rows (FP32)
-// go from global memory straight into a kPvSlots-slot LDS ring
-// (global_load_lds, no registers in flight), kPvSlots - 1 chunks ahead of
-// the chains, with explicit vmcnt waits and plain barriers (a fenced
-// barrier would wait for every copy in flight).  A copy instruction writes
-// 64 x 16 bytes contiguously; its lanes fetch the rows interleaved 16 bytes
-// at a time and its block is padded, so the 16 V rows (and the 4
-// probability rows) a chain wave reads at one key fall in distinct banks.
-constexpr int kPvFeatures = 16;
-constexpr int kPvThreads = 256;
+// The keys go through LDS in chunks of kPvChunk.  Wave 1 only copies: each
+// chunk's 8 V rows (BF16, both ranges) and 8 probability rows (FP32) go from
+// global memory straight into a kPvSlots-slot LDS ring (global_load_lds, no
+// registers in flight), kPvSlots - 1 chunks ahead of the chains, with
+// explicit vmcnt waits and plain barriers (a fenced barrier would wait for
+// every copy in flight).  The copy rate of a workgroup is bounded by the
+// bytes it keeps in flight, so the work is spread over 256 workgroups, one
+// per CU.  A copy instruction writes 64 x 16 bytes contiguously; its lanes
+// fetch the rows interleaved 16 bytes at a time and its block is padded, so
+// the rows the chain wave reads at one key fall in distinct banks.
+constexpr int kPvFeatures = 4;
+constexpr int kPvThreads = 128;
 constexpr int kPvChunk = 128;
-constexpr int kPvSlots = 6;             // chunks in the copy ring
-constexpr int kPvCopies = 6;            // global_load_lds per producer wave per chunk
+constexpr int kPvSlots = 9;             // chunks in the copy ring (static LDS stays under 64 KiB)
+constexpr int kPvVBlocks = 2;           // V blocks per chunk (4 rows each)
+constexpr int kPvCopies = 6;            // global_load_lds per chunk: 2 V blocks + 4 probability blocks
 constexpr int kPvBlock = 1024 + 64;     // bytes per copy block in LDS (64 lanes x 16 bytes + pad)
-constexpr int kPvSlotBytes = 12 * kPvBlock;  // 8 V blocks (4 rows each) + 4 probability blocks (2 rows each)
+constexpr int kPvSlotBytes = kPvCopies * kPvBlock;
+constexpr int kPvInFlight = (kPvSlots - 2) * kPvCopies;  // copies a step leaves outstanding
 
 typedef __attribute__((address_space(3))) void pv_lds_void;
 typedef __attribute__((address_space(1))) void pv_global_void;
@@ -594,13 +599,8 @@ typedef __attribute__((address_space(1))) void pv_global_void;
 // left at their no-wait maxima).
 constexpr unsigned pv_vmcnt(unsigned n) { return 0x0f70u | (n & 0xfu) | ((n >> 4) << 14); }
 
-struct PvSlot {
-  uint8_t bytes[kPvSlotBytes];
-};
-
 __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
-  __shared__ __align__(16) PvSlot s0, s1, s2, s3, s4, s5;
-  __shared__ float second[64];
+  __shared__ __align__(16) uint8_t ring[kPvSlots * kPvSlotBytes];
   if (!a.ctl->active) return;
   // Group-minor numbering keeps the feature blocks of one K/V group on one
   // XCD (workgroups are dealt to the XCDs round-robin): its L2 serves the
@@ -621,6 +621,183 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
   const int chunks0 = (end0 + kPvChunk - 1) / kPvChunk;
   const int chunks1 = end1 > begin1 ? (end1 - jb0_1 + kPvChunk - 1) / kPvChunk : 0;
   const int chunks = max(chunks0, chunks1);
+  const bool producer = wave == 1;
+
+  // Copy k (0..5) of a chunk fills block k of its slot.  k < 2: V rows
+  // 4k .. 4k + 3 (row = range * 4 + feature); lane L fetches row 4k + L % 4,
+  // keys 8 (L / 4) .. + 7.  k >= 2: probability rows 2(k - 2) + {0, 1}
+  // (row = range * 4 + head); lane L fetches row 2(k - 2) + L % 2, keys
+  // 4 (L / 2) .. + 3.  Sources past a range are clamped to its last 8 (4)
+  // keys, inside the cache rows; the chains never use those values.  The
+  // chunk index is clamped to the last chunk, so every step issues the same
+  // number of copies and waits with the same count.
+  auto copy = [&](uint8_t* slot, int c) {
+    c = min(c, chunks - 1);
+#pragma unroll
+    for (int k = 0; k < kPvCopies; ++k) {
+      if (k < kPvVBlocks) {
+        const int row = 4 * k + lane % 4, r = row / kPvFeatures, f = row % kPvFeatures;
+        const int jb0 = r ? jb0_1 : 0, last8 = ((r ? end1 : end0) - 1) & ~7;
+        const int key = max(0, min(jb0 + kPvChunk * c + 8 * (lane / 4), last8));
+        __builtin_amdgcn_global_load_lds((const pv_global_void*)(vbase + static_cast<uint64_t>(f) * a.cap + key),
+                                         (pv_lds_void*)(slot + k * kPvBlock), 16, 0, 0);
+      } else {
+        const int row = 2 * (k - kPvVBlocks) + lane % 2, r = row / 4, hl = row % 4;
+        const int jb0 = r ? jb0_1 : 0, last4 = ((r ? end1 : end0) - 1) & ~3;
+        const int key = max(0, min(jb0 + kPvChunk * c + 4 * (lane / 2), last4));
+        __builtin_amdgcn_global_load_lds((const pv_global_void*)(pbase + static_cast<uint64_t>(hl) * a.cap + key),
+                                         (pv_lds_void*)(slot + k * kPvBlock), 16, 0, 0);
+      }
+    }
+  };
+
+  if (producer && chunks > 0) {
+#pragma unroll
+    for (int c = 0; c < kPvSlots - 1; ++c) copy(ring + c * kPvSlotBytes, c);
+    __builtin_amdgcn_s_waitcnt(pv_vmcnt(kPvInFlight));  // chunk 0 has landed
+  }
+
+  // Chain lane L (lanes 32-63 repeat lanes 0-31 and write nothing): range
+  // r = L / 16 % 2, head hl, feature f.  V row r * 4 + f lives in block r at
+  // 16-byte piece 4 q + f for key group q (8 keys); probability row
+  // r * 4 + hl in block 2 + (r * 4 + hl) / 2 at piece 2 q + hl % 2 for key
+  // group q (4 keys).
+  const int r = (lane / 16) & 1, hl = (lane % 16) / kPvFeatures, f = lane % kPvFeatures;
+  const int begin = r ? begin1 : 0, end = r ? end1 : end0, jb0 = r ? jb0_1 : 0;
+  const int prow = r * 4 + hl;
+  const int voff = r * kPvBlock + f * 16;
+  const int poff = (kPvVBlocks + prow / 2) * kPvBlock + (prow % 2) * 16;
+  float acc = 0.0f;
+  // Step c: after the barrier the chains run chunk c from slot c % kPvSlots
+  // while the producer copies chunk c + kPvSlots - 1 into chunk c - 1's slot
+  // and waits until chunk c + 1 has landed.  `chunks` is uniform, so both
+  // waves meet every barrier.
+  int slot = 0;
+  for (int c = 0; c < chunks; ++c) {
+    __builtin_amdgcn_s_barrier();  // chunk c is in its slot; the chains are done with chunk c - 1
+    uint8_t* cur = ring + slot * kPvSlotBytes;
+    if (producer) {
+      const int ahead = slot == 0 ? kPvSlots - 1 : slot - 1;
+      copy(ring + ahead * kPvSlotBytes, c + kPvSlots - 1);
+      __builtin_amdgcn_s_waitcnt(pv_vmcnt(kPvInFlight));
+    } else {
+      const uint8_t* vb = cur + voff;
+      const uint8_t* pb = cur + poff;
+      // Both ranges' chunk c full: the unmasked path (wave-uniform).
+      const int cs0 = kPvChunk * c, cs1 = jb0_1 + kPvChunk * c;
+      const bool full = cs0 + kPvChunk <= end0 && begin1 <= cs1 && cs1 + kPvChunk <= end1;
+      if (full) {
+        // The reads of group q + kAhead are issued before the FMAs of group
+        // q (the order is pinned with scheduling barriers), so the LDS
+        // latency hides behind the chain and the waits stay partial (at most
+        // 3 kAhead reads are outstanding; the wait counter has 4 bits).
+        constexpr int kGroups = kPvChunk / 8, kAhead = 3;
+        u32x4 w[kGroups];
+        float4 pa[kGroups], pc[kGroups];
+        auto read = [&](int q) {
+          w[q] = *reinterpret_cast<const u32x4*>(vb + 64 * q);
+          pa[q] = *reinterpret_cast<const float4*>(pb + 32 * (2 * q));
+          pc[q] = *reinterpret_cast<const float4*>(pb + 32 * (2 * q + 1));
+        };
+#pragma unroll
+        for (int q = 0; q < kAhead; ++q) read(q);
+#pragma unroll
+        for (int q = 0; q < kGroups; ++q) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (q + kAhead < kGroups) read(q + kAhead);
+          __builtin_amdgcn_sched_barrier(0);
+          const float vv[8] = {dl_bf16_lo(w[q].x), dl_bf16_hi(w[q].x), dl_bf16_lo(w[q].y), dl_bf16_hi(w[q].y),
+                               dl_bf16_lo(w[q].z), dl_bf16_hi(w[q].z), dl_bf16_lo(w[q].w), dl_bf16_hi(w[q].w)};
+          const float pp[8] = {pa[q].x, pa[q].y, pa[q].z, pa[q].w, pc[q].x, pc[q].y, pc[q].z, pc[q].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc = fma_rn(pp[e], vv[e], acc);
+        }
+      } else {
+        // Keys [lo, hi) of this lane's range in the chunk (empty once the
+        // range is done); the group loop bounds are the union over ranges.
+        const int cs = jb0 + kPvChunk * c;
+        const int lo = max(begin - cs, 0), hi = min(end - cs, kPvChunk);
+        const int q_end = (min(max(end0 - cs0, end1 - cs1), kPvChunk) + 7) / 8;
+        for (int q = 0; q < q_end; ++q) {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(vb + 64 * q);
+          const float4 pa = *reinterpret_cast<const float4*>(pb + 32 * (2 * q));
+          const float4 pc = *reinterpret_cast<const float4*>(pb + 32 * (2 * q + 1));
+          const float vv[8] = {dl_bf16_lo(w.x), dl_bf16_hi(w.x), dl_bf16_lo(w.y), dl_bf16_hi(w.y),
+                               dl_bf16_lo(w.z), dl_bf16_hi(w.z), dl_bf16_lo(w.w), dl_bf16_hi(w.w)};
+          const float pp[8] = {pa.x, pa.y, pa.z, pa.w, pc.x, pc.y, pc.z, pc.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (8 * q + e >= lo && 8 * q + e < hi) acc = fma_rn(pp[e], vv[e], acc);
+        }
+      }
+    }
+    slot = slot == kPvSlots - 1 ? 0 : slot + 1;
+  }
+  static_assert(kPvInFlight <= 63, "the wait counter holds at most 63 outstanding copies");
+  static_assert(kPvVBlocks * 4 == 2 * kPvFeatures && (kPvCopies - kPvVBlocks) * 2 == 2 * 4,
+                "blocks of 4 V rows for two ranges of kPvFeatures, of 2 probability rows for two ranges of 4 heads");
+  if (producer) {
+    __builtin_amdgcn_s_waitcnt(pv_vmcnt(0));  // no copy outstanding at exit
+    return;
+  }
+  const float second = __shfl_down(acc, 16);
+  if (lane < 16)
+    a.att[static_cast<uint64_t>(b) * a.q_heads * kHeadDim + (g * group + hl) * kHeadDim + fb * kPvFeatures + f] =
+        bf16_bits(acc + second);
+}
+
+// Several rows per launch (the chunked prompt pass): k_attn_pv's work in 64
+// workgroups per row, so that 8 rows still fit the GPU in one round.  Grid
+// (kv head * 8 feature blocks, row), 256 threads.  Waves 0 and 2 run the two
+// PV key ranges (the first ceil(n/2) keys and the rest) for the
+// group's 4 query heads x 16 features, lane = (head, feature); each output
+// feature is round(A + B), A and B ascending FMA chains (attention.cu:331-375).
+//
+// The keys go through LDS in chunks of kPwChunk.  Waves 1 and 3 only copy:
+// each chunk's 32 V rows (BF16, both ranges) and 8 probability rows (FP32)
+// go from global memory straight into a kPwSlots-slot LDS ring
+// (global_load_lds, no registers in flight), kPwSlots - 1 chunks ahead of
+// the chains, with explicit vmcnt waits and plain barriers (a fenced
+// barrier would wait for every copy in flight).  A copy instruction writes
+// 64 x 16 bytes contiguously; its lanes fetch the rows interleaved 16 bytes
+// at a time and its block is padded, so the 16 V rows (and the 4
+// probability rows) a chain wave reads at one key fall in distinct banks.
+constexpr int kPwFeatures = 16;
+constexpr int kPwThreads = 256;
+constexpr int kPwChunk = 128;
+constexpr int kPwSlots = 6;             // chunks in the copy ring
+constexpr int kPwCopies = 6;            // global_load_lds per producer wave per chunk
+constexpr int kPwBlock = 1024 + 64;     // bytes per copy block in LDS (64 lanes x 16 bytes + pad)
+constexpr int kPwSlotBytes = 12 * kPwBlock;  // 8 V blocks (4 rows each) + 4 probability blocks (2 rows each)
+
+
+struct PwSlot {
+  uint8_t bytes[kPwSlotBytes];
+};
+
+__global__ __launch_bounds__(kPwThreads) void k_attn_pv_rows(AttnArgs a) {
+  __shared__ __align__(16) PwSlot s0, s1, s2, s3, s4, s5;
+  __shared__ float second[64];
+  if (!a.ctl->active) return;
+  // Group-minor numbering keeps the feature blocks of one K/V group on one
+  // XCD (workgroups are dealt to the XCDs round-robin): its L2 serves the
+  // group's probability rows once for all of them.
+  const int g = blockIdx.x % a.kv_heads, fb = blockIdx.x / a.kv_heads, b = blockIdx.y;
+  const int count = static_cast<int>(a.ctl->position + static_cast<uint64_t>(b) * a.pos_step) + 1;
+  const int split = (count - 1) / 2 + 1;
+  // Wave-uniform values in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+  const int group = a.q_heads / a.kv_heads;
+  const uint16_t* vbase =
+      a.v_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g * kHeadDim + fb * kPwFeatures) * a.cap;
+  const float* pbase = a.probs + (static_cast<uint64_t>(b) * a.q_heads + g * group) * a.cap;
+  // Range r covers keys [begin_r, end_r), staged from the 8-aligned key below
+  // begin_r; chunk c of range r holds keys jb0_r + kPwChunk c + [0, kPwChunk).
+  const int end0 = split, begin1 = split, end1 = count;
+  const int jb0_1 = begin1 & ~7;
+  const int chunks0 = (end0 + kPwChunk - 1) / kPwChunk;
+  const int chunks1 = end1 > begin1 ? (end1 - jb0_1 + kPwChunk - 1) / kPwChunk : 0;
+  const int chunks = max(chunks0, chunks1);
   // Waves 0 and 2 run the chains (ranges 0 and 1), waves 1 and 3 copy, so
   // that the two chains do not share a SIMD when a workgroup's consecutive
   // waves are paired on SIMDs.
@@ -635,23 +812,23 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
   // chunk index is clamped to the last chunk, so every step issues the same
   // number of copies and waits with the same count.  Producer wave w takes
   // the copies k = w / 2 + 2 n.
-  auto copy = [&](PvSlot& slot, int c) {
+  auto copy = [&](PwSlot& slot, int c) {
     c = min(c, chunks - 1);
 #pragma unroll
-    for (int n = 0; n < kPvCopies; ++n) {
+    for (int n = 0; n < kPwCopies; ++n) {
       const int k = wave / 2 + 2 * n;
       if (k < 8) {
-        const int row = 4 * k + lane % 4, r = row / kPvFeatures, f = row % kPvFeatures;
+        const int row = 4 * k + lane % 4, r = row / kPwFeatures, f = row % kPwFeatures;
         const int jb0 = r ? jb0_1 : 0, last8 = ((r ? end1 : end0) - 1) & ~7;
-        const int key = max(0, min(jb0 + kPvChunk * c + 8 * (lane / 4), last8));
+        const int key = max(0, min(jb0 + kPwChunk * c + 8 * (lane / 4), last8));
         __builtin_amdgcn_global_load_lds((const pv_global_void*)(vbase + static_cast<uint64_t>(f) * a.cap + key),
-                                         (pv_lds_void*)(slot.bytes + k * kPvBlock), 16, 0, 0);
+                                         (pv_lds_void*)(slot.bytes + k * kPwBlock), 16, 0, 0);
       } else {
         const int row = 2 * (k - 8) + lane % 2, r = row / 4, hl = row % 4;
         const int jb0 = r ? jb0_1 : 0, last4 = ((r ? end1 : end0) - 1) & ~3;
-        const int key = max(0, min(jb0 + kPvChunk * c + 4 * (lane / 2), last4));
+        const int key = max(0, min(jb0 + kPwChunk * c + 4 * (lane / 2), last4));
         __builtin_amdgcn_global_load_lds((const pv_global_void*)(pbase + static_cast<uint64_t>(hl) * a.cap + key),
-                                         (pv_lds_void*)(slot.bytes + k * kPvBlock), 16, 0, 0);
+                                         (pv_lds_void*)(slot.bytes + k * kPwBlock), 16, 0, 0);
       }
     }
   };
@@ -662,37 +839,37 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
     copy(s2, 2);
     copy(s3, 3);
     copy(s4, 4);
-    __builtin_amdgcn_s_waitcnt(pv_vmcnt((kPvSlots - 2) * kPvCopies));  // chunk 0 is in s0
+    __builtin_amdgcn_s_waitcnt(pv_vmcnt((kPwSlots - 2) * kPwCopies));  // chunk 0 is in s0
   }
 
   // Chains: wave r runs range r; lane = (head hl, feature f).  V row
   // r * 16 + f lives in block (r * 16 + f) / 4 at 16-byte piece
   // 4 g + f % 4 for key group g (8 keys); probability row r * 4 + hl in
   // block 8 + (r * 4 + hl) / 2 at piece 2 q + hl % 2 for key group q (4 keys).
-  const int hl = lane / kPvFeatures, f = lane % kPvFeatures;
+  const int hl = lane / kPwFeatures, f = lane % kPwFeatures;
   const int r = wave / 2;
   const int begin = r ? begin1 : 0, end = r ? end1 : end0, jb0 = r ? jb0_1 : 0;
   const int mine = r ? chunks1 : chunks0;
-  const int vrow = r * kPvFeatures + f, prow = r * 4 + hl;
-  const int voff = (vrow / 4) * kPvBlock + (vrow % 4) * 16;
-  const int poff = (8 + prow / 2) * kPvBlock + (prow % 2) * 16;
+  const int vrow = r * kPwFeatures + f, prow = r * 4 + hl;
+  const int voff = (vrow / 4) * kPwBlock + (vrow % 4) * 16;
+  const int poff = (8 + prow / 2) * kPwBlock + (prow % 2) * 16;
   float acc = 0.0f;
-  // Step c: after the barrier the chains run chunk c from slot c % kPvSlots
-  // while the producers copy chunk c + kPvSlots - 1 into chunk c - 1's slot
+  // Step c: after the barrier the chains run chunk c from slot c % kPwSlots
+  // while the producers copy chunk c + kPwSlots - 1 into chunk c - 1's slot
   // and wait until chunk c + 1 has landed.  `chunks` is uniform, so every
   // wave meets every barrier.
-  auto step = [&](int c, const PvSlot& cur, PvSlot& ahead) {
+  auto step = [&](int c, const PwSlot& cur, PwSlot& ahead) {
     __builtin_amdgcn_s_barrier();  // chunk c is in `cur`; every chain is done with chunk c - 1
     if (producer) {
-      copy(ahead, c + kPvSlots - 1);
-      __builtin_amdgcn_s_waitcnt(pv_vmcnt((kPvSlots - 2) * kPvCopies));
+      copy(ahead, c + kPwSlots - 1);
+      __builtin_amdgcn_s_waitcnt(pv_vmcnt((kPwSlots - 2) * kPwCopies));
       return;
     }
     if (c >= mine) return;
     const uint8_t* vb = cur.bytes + voff;
     const uint8_t* pb = cur.bytes + poff;
-    const int cs = jb0 + kPvChunk * c;
-    const int lo = max(begin - cs, 0), hi = min(end - cs, kPvChunk);
+    const int cs = jb0 + kPwChunk * c;
+    const int lo = max(begin - cs, 0), hi = min(end - cs, kPwChunk);
     auto eight = [&](int q, bool masked) {
       const u32x4 w = *reinterpret_cast<const u32x4*>(vb + 64 * q);
       const float4 pa = *reinterpret_cast<const float4*>(pb + 32 * (2 * q));
@@ -709,14 +886,14 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
           if (8 * q + e >= lo && 8 * q + e < hi) acc = fma_rn(pp[e], vv[e], acc);
       }
     };
-    if (lo == 0 && hi == kPvChunk) {
+    if (lo == 0 && hi == kPwChunk) {
       // The reads of group q + kAhead are issued before the FMAs of group
       // q (the order is pinned with scheduling barriers), so the LDS
       // latency hides behind the chain and the waits stay partial (at most
       // 3 kAhead reads are outstanding; the wait counter has 4 bits).  The
       // chain then runs at the rate of its two VALU instructions per key
       // (widen, FMA).
-      constexpr int kGroups = kPvChunk / 8, kAhead = 3;
+      constexpr int kGroups = kPwChunk / 8, kAhead = 3;
       u32x4 w[kGroups];
       float4 pa[kGroups], pc[kGroups];
       auto read = [&](int q) {
@@ -741,8 +918,8 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
       for (int q = lo / 8; q * 8 < hi; ++q) eight(q, true);
     }
   };
-  static_assert(kPvSlots == 6 && (kPvSlots - 2) * kPvCopies <= 63, "the ring below is unrolled for 6 slots");
-  for (int c0 = 0; c0 < chunks; c0 += kPvSlots) {
+  static_assert(kPwSlots == 6 && (kPwSlots - 2) * kPwCopies <= 63, "the ring below is unrolled for 6 slots");
+  for (int c0 = 0; c0 < chunks; c0 += kPwSlots) {
     step(c0, s0, s5);
     if (c0 + 1 < chunks) step(c0 + 1, s1, s0);
     if (c0 + 2 < chunks) step(c0 + 2, s2, s1);
@@ -754,7 +931,7 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
   if (wave == 2) second[lane] = acc;
   __syncthreads();
   if (wave == 0)
-    a.att[static_cast<uint64_t>(b) * a.q_heads * kHeadDim + (g * group + hl) * kHeadDim + fb * kPvFeatures + f] =
+    a.att[static_cast<uint64_t>(b) * a.q_heads * kHeadDim + (g * group + hl) * kHeadDim + fb * kPwFeatures + f] =
         bf16_bits(acc + second[lane]);
 }
 
@@ -771,7 +948,12 @@ constexpr int kAttnKeysPerPass = kAttnThreads / 8;
 constexpr int kAttnKeyPasses = 8;     // key rows issued at kernel entry: 512 keys
 constexpr int kAttnValueBlocks = 8;  // 8-key V blocks per PV chain issued at entry (one 64-key block)
 
-__global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
+// The attention of query head slot `slot` (group-minor numbering) of row
+// `b`; false when the loop is stopped (nothing is written).  kHandoff writes
+// the output with device-coherent stores and waits for them, for a reader
+// in the same launch (no cache writeback needed).
+template <bool kHandoff = false>
+__device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int b) {
   __shared__ float qs[kHeadDim];
   __shared__ float ks[kHeadDim];
   __shared__ __align__(16) float sc[kFusedKeys];
@@ -782,8 +964,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
   // query heads group-minor puts the heads of one K/V group on one XCD, whose
   // L2 then serves the group's key and value rows once for all of them.
   const int group = a.q_heads / a.kv_heads;
-  const int g = blockIdx.x % a.kv_heads, h = g * group + blockIdx.x / a.kv_heads;
-  const int b = blockIdx.y, tid = threadIdx.x;
+  const int g = slot % a.kv_heads, h = g * group + slot / a.kv_heads;
+  const int tid = threadIdx.x;
   const int wave = tid / 64, lane = tid % 64;
   const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHeadDim, kw = static_cast<uint64_t>(a.kv_heads) * kHeadDim;
   // This token's q/k rows and their norm gains do not depend on the loop
@@ -800,7 +982,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
     head.ga = dl_bf16_to_f32(gain[lane]);
     head.gb = dl_bf16_to_f32(gain[lane + 64]);
   }
-  if (!a.ctl->active) return;
+  if (!a.ctl->active) return false;
   const uint64_t pos = a.ctl->position + static_cast<uint64_t>(b) * a.pos_step;
   const int count = static_cast<int>(pos) + 1;
   const float* rope_pos = a.rope + pos * kHeadDim;
@@ -975,8 +1157,21 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
     red[tid] = acc;
   }
   __syncthreads();
-  if (tid < kHeadDim) a.att[static_cast<uint64_t>(b) * qw + h * kHeadDim + tid] = bf16_bits(red[tid] + red[tid + kHeadDim]);
+  if constexpr (kHandoff) {
+    if (tid < kHeadDim / 2) {
+      const uint32_t lo = bf16_bits(red[2 * tid] + red[2 * tid + kHeadDim]);
+      const uint32_t hi = bf16_bits(red[2 * tid + 1] + red[2 * tid + 1 + kHeadDim]);
+      uint32_t* out = reinterpret_cast<uint32_t*>(a.att + static_cast<uint64_t>(b) * qw + h * kHeadDim) + tid;
+      __hip_atomic_store(out, lo | (hi << 16), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(pv_vmcnt(0));
+    }
+  } else {
+    if (tid < kHeadDim) a.att[static_cast<uint64_t>(b) * qw + h * kHeadDim + tid] = bf16_bits(red[tid] + red[tid + kHeadDim]);
+  }
+  return true;
 }
+
+__global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) { attn_fused_body(a, blockIdx.x, blockIdx.y); }
 
 // ------------------------------------------------- residual GEMV (O, down)
 struct ResidualArgs {
@@ -1139,6 +1334,115 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual_chunked(Residua
     chain_merge<P, B>(acc);
     if (active) residual_outputs<P, B>(a, acc, tile, lane, epi + wave * RW * B, pos, steer, capture, steer_mask);
   }
+}
+
+// --------------------------------------- attention + O projection, batch 1
+// One launch for a short-context step's attention and O projection of a
+// single row.  Workgroups [0, q_heads) run the fused attention of one query
+// head each; the others each own 8 O tiles (one per wavefront).  An O
+// wavefront issues its whole weight tile (kOChunks 16-byte chunks per lane)
+// at entry, so the O weights stream from HBM while the attention runs, then
+// waits for the attention output, stages it and runs the tile's chains from
+// registers: the same chain steps, in the same order, as k_residual.
+//
+// Hand-off: the attention output goes through device-coherent stores (each
+// wavefront waits until its stores are done), each attention workgroup then
+// counts itself in sync[0]; the last one sets a go flag on each of 8 cache
+// lines (sync[32 (1 + x)]), every O workgroup polls the line of its XCD and
+// reads the output with device-coherent loads.  All hand-off traffic meets
+// at the device's coherence point, so no cache writeback or invalidation
+// (which scans a whole XCD's L2) is needed.  The attention workgroups come first in the grid and the whole grid
+// fits the GPU at once, so the wait always ends; a bounded poll that expires
+// anyway records the failure in sync[2] and goes on.  The last O workgroup
+// to finish (sync[1]) clears the words for the next launch.
+constexpr int kOChunks = 32;           // 16-byte weight chunks per lane: I / (8 P) with I = 4096, P = 16
+constexpr int kOWaves = kAttnThreads / 64;
+constexpr int kSyncWords = 32 * 10;    // counter, exit count, failure word; 8 go lines; padding
+constexpr uint32_t kHandoffPolls = 1u << 22;
+
+struct AttnOArgs {
+  AttnArgs attn;
+  ResidualArgs o;
+  uint32_t* sync;
+};
+
+__device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int o_workgroups, uint32_t* sync) {
+  constexpr int P = 16, RW = 64 / P;
+  // 16-byte aligned: the attention's static arrays come first, and the chain
+  // reads the staged inputs 16 bytes at a time.
+  extern __shared__ __align__(16) float xs[];
+  __shared__ float epi[kOWaves * RW];
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int tile = wg * kOWaves + wave;
+  const u32x4* src = a.w + static_cast<uint64_t>(tile) * (kOChunks * 64) + lane;
+  u32x4 w[kOChunks];
+#pragma unroll
+  for (int s = 0; s < kOChunks; ++s) w[s] = load_stream(src + s * 64);
+  if (!a.ctl->active) return;
+  const uint64_t pos = a.ctl->position;
+  uint32_t* go = sync + 32 * (1 + blockIdx.x % 8);
+  if (threadIdx.x == 0) {
+    uint32_t polls = 0;
+    while (__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+      __builtin_amdgcn_s_sleep(4);
+      if (++polls == kHandoffPolls) {
+        __hip_atomic_store(sync + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  // The attention output, read device-coherently (it was written in this
+  // launch), staged as stage_rows does.
+  // All of a thread's loads are issued before any is used.
+  constexpr int kWords = kOChunks * 8 * P / 2 / kAttnThreads;
+  static_assert(kWords * 2 * kAttnThreads == kOChunks * 8 * P, "the O input row splits evenly over the threads");
+  const uint32_t* x32 = reinterpret_cast<const uint32_t*>(a.x);
+  uint32_t v[kWords];
+#pragma unroll
+  for (int k = 0; k < kWords; ++k)
+    v[k] = __hip_atomic_load(x32 + threadIdx.x + k * kAttnThreads, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int k = 0; k < kWords; ++k) {
+    const int wi = threadIdx.x + k * kAttnThreads;
+    stage_put<P>(xs, a.I, 0, 2 * wi, dl_bf16_lo(v[k]));
+    stage_put<P>(xs, a.I, 0, 2 * wi + 1, dl_bf16_hi(v[k]));
+  }
+  __syncthreads();
+  const int L = a.I / P, stride = L + kXsPad, bstride = P * stride;
+  const float* xt = xs + (lane % P) * stride;
+  float acc[1] = {0.0f};
+#pragma unroll
+  for (int s = 0; s < kOChunks; ++s) chain_step<1>(w[s], xt, bstride, s, acc);
+  chain_merge<P, 1>(acc);
+  residual_outputs<P, 1>(a, acc, tile, lane, epi + wave * RW, pos, false, false, 0u);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t done = __hip_atomic_fetch_add(sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == static_cast<uint32_t>(o_workgroups) - 1u) {
+      // Every workgroup of this launch is past its wait: clear for the next.
+      __hip_atomic_store(sync, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int x = 0; x < 8; ++x) __hip_atomic_store(sync + 32 * (1 + x), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(sync + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kAttnThreads) void k_attn_o(AttnOArgs a) {
+  const uint32_t heads = static_cast<uint32_t>(a.attn.q_heads);
+  if (blockIdx.x < heads) {
+    if (!attn_fused_body<true>(a.attn, blockIdx.x, 0)) return;
+    __syncthreads();  // every output word of this workgroup has been written
+    if (threadIdx.x == 0) {
+      const uint32_t n = __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (n == heads - 1u) {
+        for (int x = 0; x < 8; ++x)
+          __hip_atomic_store(a.sync + 32 * (1 + x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    return;
+  }
+  o_prefetched(a.o, blockIdx.x - heads, gridDim.x - heads, a.sync);
 }
 
 // ------------------------------------------------------------ gate/up GEMV
@@ -1968,6 +2272,9 @@ struct dl_plan {
   uint16_t *h = nullptr, *q_raw = nullptr, *k_raw = nullptr, *att = nullptr, *act = nullptr, *logits = nullptr;
   uint16_t *k_cache = nullptr, *v_cache = nullptr, *capture = nullptr, *override_row = nullptr;
   float *scores = nullptr, *probs = nullptr, *rope = nullptr, *steer = nullptr;
+  // Hand-off words of the fused attention + O launch (zero between launches;
+  // word 2 records an expired hand-off wait).
+  uint32_t* attn_sync = nullptr;
   uint64_t* partial_keys = nullptr;
   uint32_t *partial_flags = nullptr, *tokens = nullptr, *selected = nullptr, *out_tokens = nullptr;
   uint8_t* stop_mask = nullptr;
@@ -2240,8 +2547,21 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       break;
     case 1: k_attn_qk<<<dim3(c.kv_heads, p->cap / 64, B), kBlock, 0, s>>>(aa); break;
     case 2: k_attn_softmax<<<dim3(c.q_heads, B), kSoftmaxThreads, size_t(p->cap) * sizeof(float), s>>>(aa); break;
-    case 3: k_attn_pv<<<dim3(c.kv_heads * (kHeadDim / kPvFeatures), B), kPvThreads, 0, s>>>(aa); break;
+    case 3:
+      if (B == 1)
+        k_attn_pv<<<dim3(c.kv_heads * (kHeadDim / kPvFeatures), 1), kPvThreads, 0, s>>>(aa);
+      else
+        k_attn_pv_rows<<<dim3(c.kv_heads * (kHeadDim / kPwFeatures), B), kPwThreads, 0, s>>>(aa);
+      break;
     case 8: k_attn_fused<<<dim3(c.q_heads, B), kAttnThreads, 0, s>>>(aa); break;
+    case 10: {
+      // Attention + O of one row (fused_attention_o decides when it applies).
+      ResidualArgs oa{ctl, r.att, reinterpret_cast<const u32x4*>(m->o[l]), r.h, nullptr, nullptr, QW, D,
+                      static_cast<int>(p->cap), static_cast<int>(l), 0, r.same_sequence, r.sequence};
+      const int o_workgroups = D / (64 / 16) / kOWaves;
+      k_attn_o<<<c.q_heads + o_workgroups, kAttnThreads, p16_lds(1, QW), s>>>(AttnOArgs{aa, oa, p->attn_sync});
+      break;
+    }
     case 9: k_append_keys<<<dim3(c.kv_heads, B), 64, 0, s>>>(aa); break;
     case 4:
       for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
@@ -2304,6 +2624,16 @@ void launch_intervention(dl_plan* p, hipStream_t s, uint32_t l, dl::Control* ctl
   dl::k_plan_intervene<<<1, dl::nla::kThreads, 0, s>>>(a);
 }
 
+// Whether a short-context step of this plan runs attention and the O
+// projection as one launch (k_attn_o): one row, and the O tile shape the
+// kernel holds in registers (I = 4096 inputs at P = 16, whole workgroups of
+// O tiles).
+bool fused_attention_o(const dl_plan* p) {
+  const auto& c = p->model->cfg;
+  const int QW = c.q_heads * c.head_dim, tiles = c.hidden / (64 / 16);
+  return p->batch == 1 && QW / (8 * 16) == dl::kOChunks && tiles % dl::kOWaves == 0;
+}
+
 // Records one decode step.  `short_context` selects the fused attention
 // kernel (positions below kFusedKeys) instead of the three-kernel split;
 // categorical generation adds the device sampler after the LM head.
@@ -2316,9 +2646,13 @@ void record_step_all(dl_plan* p, hipStream_t s, bool short_context) {
                   c.vocab, c.tied_embeddings ? 1 : 0, p->journal, static_cast<int>(p->batch)};
   k_step_begin<<<p->batch, kBlock, 0, s>>>(begin);
   static const int kShort[] = {0, 8, 4, 5, 6};
+  static const int kShortFused[] = {0, 10, 5, 6};
   static const int kLong[] = {0, 1, 2, 3, 4, 5, 6};
+  const bool fused = fused_attention_o(p);
   for (uint32_t l = 0; l < c.layers; ++l) {
-    if (short_context)
+    if (short_context && fused)
+      for (int which : kShortFused) launch_step_kernel(p, s, which, l, p->ctl, plan_rows(p));
+    else if (short_context)
       for (int which : kShort) launch_step_kernel(p, s, which, l, p->ctl, plan_rows(p));
     else
       for (int which : kLong) launch_step_kernel(p, s, which, l, p->ctl, plan_rows(p));
@@ -2484,6 +2818,8 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
     p->probs = p->alloc<float>(B * c.q_heads * cap);
     dl::check_hip(hipMemsetAsync(p->probs, 0, B * c.q_heads * cap * 4, queue->stream), "probs clear");
     p->rope = p->alloc<float>(cap * c.head_dim);
+    p->attn_sync = p->alloc<uint32_t>(dl::kSyncWords);
+    dl::check_hip(hipMemsetAsync(p->attn_sync, 0, dl::kSyncWords * 4, queue->stream), "hand-off clear");
     p->partial_keys = p->alloc<uint64_t>(B * 1024);
     p->partial_flags = p->alloc<uint32_t>(B * 1024);
     p->tokens = p->alloc<uint32_t>(cap);
@@ -2551,7 +2887,7 @@ int dl_plan_launch_kernel(dl_plan* plan, uint32_t which, uint32_t first_layer, u
   return guard([&] {
     require(plan != nullptr, "null plan");
     dl::enter(plan->queue);
-    require(which <= 8, "unknown step kernel");
+    require(which <= 8 || (which == 10 && fused_attention_o(plan)), "unknown step kernel");
     const uint32_t L = plan->model->cfg.layers;
     require(first_layer < L, "layer out of range");
     for (uint32_t i = 0; i < count; ++i) {
@@ -3004,6 +3340,12 @@ int dl_plan_collect(dl_plan* plan, uint32_t* tokens, uint32_t max_new, dl_genera
     if (e != hipSuccess) {
       plan->queue->device->poisoned = true;
       dl::check_hip(e, "generation");
+    }
+    uint32_t handoff = 0;
+    dl::check_hip(hipMemcpy(&handoff, plan->attn_sync + 2, 4, hipMemcpyDeviceToHost), "read hand-off word");
+    if (handoff != 0) {
+      plan->queue->device->poisoned = true;
+      dl::fail(DL_RUNTIME_ERROR, "attention to O hand-off wait expired; the results are invalid");
     }
     dl::Control c;
     dl::check_hip(hipMemcpy(&c, plan->ctl, sizeof c, hipMemcpyDeviceToHost), "read control");
