@@ -314,6 +314,9 @@ struct QkvArgs {
 // not fit in LDS together, so kQkvQ (Q rows, P = 16 layout) and kQkvKV (K
 // and V rows, P = 32 layout) run as two launches.
 enum QkvPart : int { kQkvAll = 0, kQkvQ = 1, kQkvKV = 2 };
+// Input width of the batch-1 GEMV paths that hold a wavefront's whole weight
+// tile in registers (Qwen3-8B's hidden width).
+constexpr int kWholeTileInputs = 4096;
 constexpr int qkv_waves(int rows, int part) { return part == kQkvAll ? kWaves : gemv_waves(rows); }
 
 // Split > 1 divides each tile's B rows into Split work items of B / Split
@@ -321,7 +324,9 @@ constexpr int qkv_waves(int rows, int part) { return part == kQkvAll ? kWaves : 
 // per wavefront the chain length per wavefront, not the CU count, bounds
 // these launches at eight rows.
 template <int B, int Part = kQkvAll, int Split = 1>
-__global__ __launch_bounds__(qkv_waves(B, Part) * 64) void k_qkv(QkvArgs a) {
+// Two wavefronts per SIMD at least: the batch-1 whole-tile path holds 128
+// weight VGPRs, and a grid of one tile per wavefront must be resident at once.
+__global__ __launch_bounds__(qkv_waves(B, Part) * 64) __attribute__((amdgpu_waves_per_eu(2))) void k_qkv(QkvArgs a) {
   constexpr int W = qkv_waves(B, Part);
   constexpr int BR = B / Split;
   static_assert(B % Split == 0, "rows split evenly");
@@ -345,6 +350,63 @@ __global__ __launch_bounds__(qkv_waves(B, Part) * 64) void k_qkv(QkvArgs a) {
   const int tile_begin = Part == kQkvKV ? q_tiles : 0, tile_end = Part == kQkvQ ? q_tiles : total;
   const int items = (tile_end - tile_begin) * Split;
   const int first = blockIdx.x * W + wave;
+  if constexpr (B == 1 && Part == kQkvAll && Split == 1) {
+    if (gridDim.x * W >= static_cast<unsigned>(items) && a.D == kWholeTileInputs) {
+      // One tile per wavefront, held in registers (32 chunks per lane for a
+      // Q tile, 16 for K or V): the first 16 chunks are issued before the
+      // prologue, the rest right after it, and the chains run from
+      // registers; the same chain steps as chain_tile.
+      const bool has = first < items;
+      const int tile = tile_begin + first;
+      const bool is_q = tile < q_tiles;
+      constexpr int SQ = kWholeTileInputs / 128, SK = kWholeTileInputs / 256;
+      u32x4 w[SQ];
+      if (!norm_stage<1, true, true, W / 2>(
+              a.h, a.norm, a.eps, xs16, xs32, scratch,
+              [&] {
+                if (has) {
+                  const u32x4* src = tile_src(tile) + lane;
+#pragma unroll
+                  for (int s = 0; s < SK; ++s) w[s] = load_stream(src + s * 64);
+                }
+              },
+              &a.ctl->active))
+        return;
+      if (has && is_q) {
+        const u32x4* src = tile_src(tile) + lane;
+#pragma unroll
+        for (int s = SK; s < SQ; ++s) w[s] = load_stream(src + s * 64);
+      }
+      __syncthreads();
+      if (!has) return;
+      float acc[1] = {0.0f};
+      if (is_q) {
+        constexpr int P = 16, stride = kWholeTileInputs / P + kXsPad;
+        const float* xt = xs16 + (lane % P) * stride;
+#pragma unroll
+        for (int s = 0; s < SQ; ++s) chain_step<1>(w[s], xt, P * stride, s, acc);
+        chain_merge<P, 1>(acc);
+        if (lane % P == 0) a.q_out[tile * 4 + lane / P] = bf16_bits(acc[0]);
+      } else {
+        constexpr int P = 32, stride = kWholeTileInputs / P + kXsPad;
+        const float* xt = xs32 + (lane % P) * stride;
+#pragma unroll
+        for (int s = 0; s < SK; ++s) chain_step<1>(w[s], xt, P * stride, s, acc);
+        chain_merge<P, 1>(acc);
+        if (lane % P == 0) {
+          int kt = tile - q_tiles;
+          const bool is_v = kt >= k_tiles;
+          if (is_v) kt -= k_tiles;
+          const int row = kt * 2 + lane / P;
+          if (is_v)
+            a.v_cache[static_cast<uint64_t>(row) * a.cap + a.ctl->position] = bf16_bits(acc[0]);
+          else
+            a.k_out[row] = bf16_bits(acc[0]);
+        }
+      }
+      return;
+    }
+  }
   FirstBatch fb{};
   // The prologue returns, after issuing its loads, when the loop is stopped
   // (grid-uniform flag).
@@ -1393,8 +1455,8 @@ __device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int 
   }
   __syncthreads();
   // The attention output, read device-coherently (it was written in this
-  // launch), staged as stage_rows does.
-  // All of a thread's loads are issued before any is used.
+  // launch), staged as stage_rows does; all of a thread's loads are issued
+  // before any is used.
   constexpr int kWords = kOChunks * 8 * P / 2 / kAttnThreads;
   static_assert(kWords * 2 * kAttnThreads == kOChunks * 8 * P, "the O input row splits evenly over the threads");
   const uint32_t* x32 = reinterpret_cast<const uint32_t*>(a.x);
@@ -2645,17 +2707,20 @@ void record_step_all(dl_plan* p, hipStream_t s, bool short_context) {
                   p->cancel_device, p->injection_status, p->intervention_state(), static_cast<int>(c.hidden),
                   c.vocab, c.tied_embeddings ? 1 : 0, p->journal, static_cast<int>(p->batch)};
   k_step_begin<<<p->batch, kBlock, 0, s>>>(begin);
-  static const int kShort[] = {0, 8, 4, 5, 6};
-  static const int kShortFused[] = {0, 10, 5, 6};
-  static const int kLong[] = {0, 1, 2, 3, 4, 5, 6};
-  const bool fused = fused_attention_o(p);
+  const bool fused_attn = fused_attention_o(p);
   for (uint32_t l = 0; l < c.layers; ++l) {
-    if (short_context && fused)
-      for (int which : kShortFused) launch_step_kernel(p, s, which, l, p->ctl, plan_rows(p));
-    else if (short_context)
-      for (int which : kShort) launch_step_kernel(p, s, which, l, p->ctl, plan_rows(p));
-    else
-      for (int which : kLong) launch_step_kernel(p, s, which, l, p->ctl, plan_rows(p));
+    launch_step_kernel(p, s, 0, l, p->ctl, plan_rows(p));
+    if (short_context && fused_attn) {
+      launch_step_kernel(p, s, 10, l, p->ctl, plan_rows(p));
+    } else {
+      if (short_context)
+        launch_step_kernel(p, s, 8, l, p->ctl, plan_rows(p));
+      else
+        for (int which : {1, 2, 3}) launch_step_kernel(p, s, which, l, p->ctl, plan_rows(p));
+      launch_step_kernel(p, s, 4, l, p->ctl, plan_rows(p));
+    }
+    launch_step_kernel(p, s, 5, l, p->ctl, plan_rows(p));
+    launch_step_kernel(p, s, 6, l, p->ctl, plan_rows(p));
     launch_intervention(p, s, l, p->ctl, plan_rows(p));
   }
   launch_step_kernel(p, s, 7, 0, p->ctl, plan_rows(p));
