@@ -273,6 +273,7 @@ TRAFFIC_KERNELS = (
     (7, "k_lm_head<1>", 4, "short"),
     (8, "k_attn_fused", 8, "short"),
     (10, "k_attn_o", 8, "short"),
+    (12, "k_qkv_attn_o", 8, "short"),
     (1, "k_attn_qk", 8, "long"),
     (2, "k_attn_softmax", 8, "long"),
     (3, "k_attn_pv", 8, "long"),
@@ -300,6 +301,8 @@ def attention_bytes(cfg, which, keys):
 def launch_bytes(cfg, which, keys):
     if which == 10:  # fused attention + O projection
         return attention_bytes(cfg, 8, keys) + kernel_bytes(cfg, 4)
+    if which == 12:  # fused QKV + attention + O projection
+        return kernel_bytes(cfg, 0) + attention_bytes(cfg, 8, keys) + kernel_bytes(cfg, 4)
     return attention_bytes(cfg, which, keys) if which in (1, 2, 3, 8) else kernel_bytes(cfg, which)
 
 
@@ -501,11 +504,12 @@ def main() -> int:
     kernels = {}
     prefixes = {which: prefix for which, prefix, _, _ in TRAFFIC_KERNELS}
     names = {0: "k_qkv", 4: "k_residual<16> (O)", 5: "k_gateup", 6: "k_residual<32> (down)", 7: "k_lm_head",
-             8: "k_attn_fused", 10: "k_attn_o (attention + O)"}
+             8: "k_attn_fused", 10: "k_attn_o (attention + O)",
+             12: "k_qkv_attn_o (QKV + attention + O)"}
     # The bench control sits at the last consumed position: every position
     # so far is a visible key.
     attn_keys = args.prompt + max_new
-    for which in (5, 7, 0, 6, 4, 8, 10):
+    for which in (5, 7, 0, 6, 4, 8, 10, 12):
         iters = args.kernel_iters if which != 7 else max(8, args.kernel_iters // 8)
         _lib.call("dl_plan_launch_kernel", plan.handle, which, 0, 2)  # warm
         ea, eb = Event(device), Event(device)
@@ -518,7 +522,7 @@ def main() -> int:
         gbs = alg / (us * 1e-6) / 1e9
         entry = {"us": round(us, 2), "algorithmic_bytes": alg, "GB/s": round(gbs, 1),
                  "frac": round(gbs / HBM_PEAK_GBS, 4)}
-        if which in (8, 10):
+        if which in (8, 10, 12):
             # The four query heads of a group share their K and V rows
             # through L2: the bytes count each row once.
             entry["keys"] = attn_keys

@@ -1014,8 +1014,51 @@ constexpr int kAttnValueBlocks = 8;  // 8-key V blocks per PV chain issued at en
 // `b`; false when the loop is stopped (nothing is written).  kHandoff writes
 // the output with device-coherent stores and waits for them, for a reader
 // in the same launch (no cache writeback needed).
-template <bool kHandoff = false>
-__device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int b) {
+// Hand-off words between the workgroup roles of one launch: uint32 words,
+// one 128-byte line (32 words) each, zero between launches.  `go` is the
+// first of 8 go-flag lines (a waiting workgroup polls the line of its XCD,
+// so the polling spreads over 8 lines), `exit` counts the last role's
+// finished workgroups (the last one zeroes lines [0, exit]), `failure`
+// records an expired wait.
+struct Handoff {
+  uint32_t* words;
+  int go, exit, failure;
+};
+constexpr uint32_t kHandoffPolls = 1u << 22;
+
+__device__ __forceinline__ uint32_t* handoff_line(const Handoff& hs, int line) { return hs.words + 32 * line; }
+
+// Thread 0 polls its XCD's go line (relaxed device-coherent loads, no cache
+// invalidation); a wait that expires records the failure and goes on.
+__device__ __forceinline__ void handoff_wait(const Handoff& hs) {
+  if (threadIdx.x == 0) {
+    const uint32_t* go = handoff_line(hs, hs.go + blockIdx.x % 8);
+    uint32_t polls = 0;
+    while (__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+      __builtin_amdgcn_s_sleep(4);
+      if (++polls == kHandoffPolls) {
+        __hip_atomic_store(handoff_line(hs, hs.failure), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// Raises the 8 go lines starting at `go`.
+__device__ __forceinline__ void handoff_raise(const Handoff& hs, int go) {
+  for (int x = 0; x < 8; ++x)
+    __hip_atomic_store(handoff_line(hs, go + x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// kFromQkv: q, k and the new v row are written in this launch (by the QKV
+// workgroups before the attention ones in the grid): the head rows are read
+// device-coherently after the go flag `qkv_go` (a Handoff whose `go` names
+// those lines), and the chain holding the current position takes its value
+// from `v_new` (the V cache column is written in this launch too).
+template <bool kHandoff = false, bool kFromQkv = false>
+__device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int b, const Handoff* qkv_go = nullptr,
+                                                const uint16_t* v_new = nullptr) {
   __shared__ float qs[kHeadDim];
   __shared__ float ks[kHeadDim];
   __shared__ __align__(16) float sc[kFusedKeys];
@@ -1035,12 +1078,14 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
   // row of the position right after it.  Loads retire in order, so anything
   // issued before them would delay the head norms.
   HeadOperands head{};
+  const uint16_t* head_row = wave == 0 ? a.q_raw + b * qw + static_cast<uint64_t>(h) * kHeadDim
+                                       : a.k_raw + b * kw + static_cast<uint64_t>(g) * kHeadDim;
   if (wave < 2) {
-    const uint16_t* x = wave == 0 ? a.q_raw + b * qw + static_cast<uint64_t>(h) * kHeadDim
-                                  : a.k_raw + b * kw + static_cast<uint64_t>(g) * kHeadDim;
     const uint16_t* gain = wave == 0 ? a.q_norm : a.k_norm;
-    head.xa = dl_bf16_to_f32(x[lane]);
-    head.xb = dl_bf16_to_f32(x[lane + 64]);
+    if constexpr (!kFromQkv) {
+      head.xa = dl_bf16_to_f32(head_row[lane]);
+      head.xb = dl_bf16_to_f32(head_row[lane + 64]);
+    }
     head.ga = dl_bf16_to_f32(gain[lane]);
     head.gb = dl_bf16_to_f32(gain[lane + 64]);
   }
@@ -1084,6 +1129,24 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
     for (int i = 0; i < kAttnValueBlocks; ++i) {
       const int jb = min(first_block + 8 * i, a.cap - 8);
       vpre[i] = *reinterpret_cast<const u32x4*>(v + jb);
+    }
+  }
+  float v_pos = 0.0f;  // the new value at `pos` of this lane's feature (kFromQkv)
+  if constexpr (kFromQkv) {
+    __builtin_amdgcn_sched_barrier(0);
+    handoff_wait(*qkv_go);
+    if (wave < 2) {
+      const uint32_t* x32 = reinterpret_cast<const uint32_t*>(head_row);
+      const uint32_t wa = __hip_atomic_load(x32 + lane / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t wb = __hip_atomic_load(x32 + 32 + lane / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      head.xa = (lane & 1) ? dl_bf16_hi(wa) : dl_bf16_lo(wa);
+      head.xb = (lane & 1) ? dl_bf16_hi(wb) : dl_bf16_lo(wb);
+    }
+    if (chain) {
+      const int c = g * kHeadDim + f;
+      const uint32_t wv =
+          __hip_atomic_load(reinterpret_cast<const uint32_t*>(v_new) + c / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v_pos = (c & 1) ? dl_bf16_hi(wv) : dl_bf16_lo(wv);
     }
   }
 
@@ -1181,10 +1244,18 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
 #pragma unroll
       for (int i = 0; i < 16; ++i) pc[i] = *reinterpret_cast<const float4*>(sc + min(jb + 4 * i, last4));
       const int lo = max(begin - jb, 0), hi = min(end - jb, 64);
+      // kFromQkv: the block holding `pos` takes the new value there
+      // (wave-uniform: pos, jb and the chain's range are).
+      const int pi = static_cast<int>(pos) - jb;
+      const bool patch = kFromQkv && pi >= lo && pi < hi;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float vf[8] = {dl_bf16_lo(vb[i].x), dl_bf16_hi(vb[i].x), dl_bf16_lo(vb[i].y), dl_bf16_hi(vb[i].y),
-                             dl_bf16_lo(vb[i].z), dl_bf16_hi(vb[i].z), dl_bf16_lo(vb[i].w), dl_bf16_hi(vb[i].w)};
+        float vf[8] = {dl_bf16_lo(vb[i].x), dl_bf16_hi(vb[i].x), dl_bf16_lo(vb[i].y), dl_bf16_hi(vb[i].y),
+                       dl_bf16_lo(vb[i].z), dl_bf16_hi(vb[i].z), dl_bf16_lo(vb[i].w), dl_bf16_hi(vb[i].w)};
+        if (patch) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vf[e] = 8 * i + e == pi ? v_pos : vf[e];
+        }
         const float pf[8] = {pc[2 * i].x, pc[2 * i].y, pc[2 * i].z, pc[2 * i].w,
                              pc[2 * i + 1].x, pc[2 * i + 1].y, pc[2 * i + 1].z, pc[2 * i + 1].w};
         if (lo == 0 && hi == 64) {
@@ -1409,18 +1480,18 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual_chunked(Residua
 //
 // Hand-off: the attention output goes through device-coherent stores (each
 // wavefront waits until its stores are done), each attention workgroup then
-// counts itself in sync[0]; the last one sets a go flag on each of 8 cache
-// lines (sync[32 (1 + x)]), every O workgroup polls the line of its XCD and
-// reads the output with device-coherent loads.  All hand-off traffic meets
-// at the device's coherence point, so no cache writeback or invalidation
-// (which scans a whole XCD's L2) is needed.  The attention workgroups come first in the grid and the whole grid
-// fits the GPU at once, so the wait always ends; a bounded poll that expires
-// anyway records the failure in sync[2] and goes on.  The last O workgroup
-// to finish (sync[1]) clears the words for the next launch.
+// counts itself; the last one raises the go lines, every O workgroup polls
+// the line of its XCD and reads the output with device-coherent loads.  All
+// hand-off traffic meets at the device's coherence point, so no cache
+// writeback or invalidation (which scans a whole XCD's L2) is needed.  The
+// waiting workgroups come after the ones they wait for in the grid, which
+// are dispatched first, and the waits are bounded (handoff_wait).
 constexpr int kOChunks = 32;           // 16-byte weight chunks per lane: I / (8 P) with I = 4096, P = 16
 constexpr int kOWaves = kAttnThreads / 64;
-constexpr int kSyncWords = 32 * 10;    // counter, exit count, failure word; 8 go lines; padding
-constexpr uint32_t kHandoffPolls = 1u << 22;
+// k_attn_o's lines: attention count 0, go 1-8, O exit 9, failure 10.
+constexpr Handoff kAttnOLayout{nullptr, 1, 9, 10};
+constexpr int kAttnOCount = 0;
+constexpr int kSyncWords = 32 * 11;
 
 struct AttnOArgs {
   AttnArgs attn;
@@ -1428,7 +1499,9 @@ struct AttnOArgs {
   uint32_t* sync;
 };
 
-__device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int o_workgroups, uint32_t* sync) {
+// The O workgroup `wg` of `o_workgroups`: waits on hs's go lines; the last
+// to finish zeroes lines [0, hs.exit].
+__device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int o_workgroups, const Handoff& hs) {
   constexpr int P = 16, RW = 64 / P;
   // 16-byte aligned: the attention's static arrays come first, and the chain
   // reads the staged inputs 16 bytes at a time.
@@ -1442,18 +1515,7 @@ __device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int 
   for (int s = 0; s < kOChunks; ++s) w[s] = load_stream(src + s * 64);
   if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
-  uint32_t* go = sync + 32 * (1 + blockIdx.x % 8);
-  if (threadIdx.x == 0) {
-    uint32_t polls = 0;
-    while (__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
-      __builtin_amdgcn_s_sleep(4);
-      if (++polls == kHandoffPolls) {
-        __hip_atomic_store(sync + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-    }
-  }
-  __syncthreads();
+  handoff_wait(hs);
   // The attention output, read device-coherently (it was written in this
   // launch), staged as stage_rows does; all of a thread's loads are issued
   // before any is used.
@@ -1480,31 +1542,159 @@ __device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int 
   residual_outputs<P, 1>(a, acc, tile, lane, epi + wave * RW, pos, false, false, 0u);
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t done = __hip_atomic_fetch_add(sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t done = __hip_atomic_fetch_add(handoff_line(hs, hs.exit), 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
     if (done == static_cast<uint32_t>(o_workgroups) - 1u) {
       // Every workgroup of this launch is past its wait: clear for the next.
-      __hip_atomic_store(sync, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (int x = 0; x < 8; ++x) __hip_atomic_store(sync + 32 * (1 + x), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(sync + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int line = 0; line <= hs.exit; ++line)
+        __hip_atomic_store(handoff_line(hs, line), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+  }
+}
+
+// Counts one finished workgroup on `count`; the last of `total` raises the
+// go lines `go`.
+__device__ __forceinline__ void handoff_signal(const Handoff& hs, int count, uint32_t total, int go) {
+  if (threadIdx.x == 0) {
+    const uint32_t n = __hip_atomic_fetch_add(handoff_line(hs, count), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (n == total - 1u) handoff_raise(hs, go);
   }
 }
 
 __global__ __launch_bounds__(kAttnThreads) void k_attn_o(AttnOArgs a) {
   const uint32_t heads = static_cast<uint32_t>(a.attn.q_heads);
+  Handoff hs = kAttnOLayout;
+  hs.words = a.sync;
   if (blockIdx.x < heads) {
     if (!attn_fused_body<true>(a.attn, blockIdx.x, 0)) return;
     __syncthreads();  // every output word of this workgroup has been written
-    if (threadIdx.x == 0) {
-      const uint32_t n = __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (n == heads - 1u) {
-        for (int x = 0; x < 8; ++x)
-          __hip_atomic_store(a.sync + 32 * (1 + x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+    handoff_signal(hs, kAttnOCount, heads, hs.go);
     return;
   }
-  o_prefetched(a.o, blockIdx.x - heads, gridDim.x - heads, a.sync);
+  o_prefetched(a.o, blockIdx.x - heads, gridDim.x - heads, hs);
+}
+
+// ------------------------------------ QKV + attention + O projection, batch 1
+// One launch for a short-context step's QKV projection, attention and O
+// projection of a single row: workgroups [0, kQkvWorkgroups) own one QKV
+// tile per wavefront (held in registers, as k_qkv's batch-1 path), then the
+// attention workgroups, then the O workgroups (as in k_attn_o).  The QKV
+// workgroups write q and k with device-coherent stores, the new V values
+// both into the cache column (for later steps) and, device-coherently, into
+// `v_new` (for this launch's attention, which substitutes them at the
+// current position); each counts itself on the counter of its XCD (lines
+// 0-7), the last of each counter counts the counter done (line 8), and the
+// last counter done raises the QKV go lines (9-16).  The attention
+// workgroups issue their key and value prefetch, wait for those lines, then
+// run; they count themselves on line 17 and the last raises the attention go
+// lines (18-25) that the O workgroups wait on.
+constexpr int kQkvoQkvCount = 0, kQkvoQkvDone = 8, kQkvoQkvGo = 9, kQkvoAttnCount = 17;
+constexpr Handoff kQkvoLayout{nullptr, 18, 26, 27};
+constexpr int kQkvoSyncWords = 32 * 28;
+constexpr int kQkvWaves = kAttnThreads / 64;
+
+struct QkvAttnOArgs {
+  QkvArgs qkv;
+  AttnArgs attn;
+  ResidualArgs o;
+  uint16_t* v_new;
+  uint32_t* sync;
+  int qkv_workgroups;
+};
+
+__device__ __forceinline__ void qkv_phase(const QkvArgs& a, uint16_t* v_new, const Handoff& hs, int qkv_workgroups) {
+  constexpr int W = kQkvWaves;
+  extern __shared__ __align__(16) float lds[];
+  float* xs16 = lds;
+  float* xs32 = lds + staged_floats(16, kWholeTileInputs);
+  __shared__ float scratch[W * 40];
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int q_tiles = a.QW / 4, k_tiles = a.KW / 2;
+  const uint64_t q_chunks = static_cast<uint64_t>(a.D / 128) * 64, k_chunks = static_cast<uint64_t>(a.D / 256) * 64;
+  const int tile = blockIdx.x * W + wave;
+  const bool is_q = tile < q_tiles;
+  int kt = tile - q_tiles;
+  const bool is_v = !is_q && kt >= k_tiles;
+  if (is_v) kt -= k_tiles;
+  const u32x4* src = (is_q ? a.w + tile * q_chunks
+                           : a.w + q_tiles * q_chunks + (is_v ? k_tiles : 0) * k_chunks + kt * k_chunks) + lane;
+  constexpr int SQ = kWholeTileInputs / 128, SK = kWholeTileInputs / 256;
+  u32x4 w[SQ];
+  if (!norm_stage<1, true, true, W / 2>(
+          a.h, a.norm, a.eps, xs16, xs32, scratch,
+          [&] {
+#pragma unroll
+            for (int s = 0; s < SK; ++s) w[s] = load_stream(src + s * 64);
+          },
+          &a.ctl->active))
+    return;
+  if (is_q) {
+#pragma unroll
+    for (int s = SK; s < SQ; ++s) w[s] = load_stream(src + s * 64);
+  }
+  __syncthreads();
+  float acc[1] = {0.0f};
+  if (is_q) {
+    constexpr int P = 16, stride = kWholeTileInputs / P + kXsPad;
+    const float* xt = xs16 + (lane % P) * stride;
+#pragma unroll
+    for (int s = 0; s < SQ; ++s) chain_step<1>(w[s], xt, P * stride, s, acc);
+    chain_merge<P, 1>(acc);
+    // Lanes 0, 16, 32, 48 hold rows 4 t .. 4 t + 3: two words.
+    const uint32_t y = bf16_bits(acc[0]);
+    const uint32_t y1 = __shfl_down(y, 16, 64);
+    if (lane == 0 || lane == 32)
+      __hip_atomic_store(reinterpret_cast<uint32_t*>(a.q_out) + tile * 2 + lane / 32, y | (y1 << 16),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    constexpr int P = 32, stride = kWholeTileInputs / P + kXsPad;
+    const float* xt = xs32 + (lane % P) * stride;
+#pragma unroll
+    for (int s = 0; s < SK; ++s) chain_step<1>(w[s], xt, P * stride, s, acc);
+    chain_merge<P, 1>(acc);
+    // Lanes 0 and 32 hold rows 2 kt and 2 kt + 1: one word.
+    const uint32_t y = bf16_bits(acc[0]);
+    const uint32_t y1 = __shfl_down(y, 32, 64);
+    if (is_v && lane % P == 0)
+      a.v_cache[static_cast<uint64_t>(kt * 2 + lane / P) * a.cap + a.ctl->position] = static_cast<uint16_t>(y);
+    if (lane == 0)
+      __hip_atomic_store(reinterpret_cast<uint32_t*>(is_v ? v_new : a.k_out) + kt, y | (y1 << 16), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(pv_vmcnt(0));  // this wavefront's outputs are written
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    // The last workgroup of a counter's share counts the counter done; the
+    // last counter done raises the QKV go lines.
+    const int x = blockIdx.x % 8;
+    const uint32_t share = static_cast<uint32_t>((qkv_workgroups - x + 7) / 8);
+    const uint32_t n = __hip_atomic_fetch_add(handoff_line(hs, kQkvoQkvCount + x), 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    if (n == share - 1u) {
+      const uint32_t c = __hip_atomic_fetch_add(handoff_line(hs, kQkvoQkvDone), 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+      if (c == 7u) handoff_raise(hs, kQkvoQkvGo);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_qkv_attn_o(QkvAttnOArgs a) {
+  const uint32_t heads = static_cast<uint32_t>(a.attn.q_heads), nq = static_cast<uint32_t>(a.qkv_workgroups);
+  Handoff hs = kQkvoLayout;
+  hs.words = a.sync;
+  if (blockIdx.x < nq) {
+    qkv_phase(a.qkv, a.v_new, hs, a.qkv_workgroups);
+    return;
+  }
+  if (blockIdx.x < nq + heads) {
+    Handoff qkv_go = hs;
+    qkv_go.go = kQkvoQkvGo;
+    if (!attn_fused_body<true, true>(a.attn, blockIdx.x - nq, 0, &qkv_go, a.v_new)) return;
+    __syncthreads();  // every output word of this workgroup has been written
+    handoff_signal(hs, kQkvoAttnCount, heads, hs.go);
+    return;
+  }
+  o_prefetched(a.o, blockIdx.x - nq - heads, gridDim.x - nq - heads, hs);
 }
 
 // ------------------------------------------------------------ gate/up GEMV
@@ -2337,6 +2527,9 @@ struct dl_plan {
   // Hand-off words of the fused attention + O launch (zero between launches;
   // word 2 records an expired hand-off wait).
   uint32_t* attn_sync = nullptr;
+  // Hand-off words of the fused QKV + attention + O launch, and its new V row.
+  uint32_t* qkvo_sync = nullptr;
+  uint16_t* v_new = nullptr;
   uint64_t* partial_keys = nullptr;
   uint32_t *partial_flags = nullptr, *tokens = nullptr, *selected = nullptr, *out_tokens = nullptr;
   uint8_t* stop_mask = nullptr;
@@ -2616,6 +2809,20 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
         k_attn_pv_rows<<<dim3(c.kv_heads * (kHeadDim / kPwFeatures), B), kPwThreads, 0, s>>>(aa);
       break;
     case 8: k_attn_fused<<<dim3(c.q_heads, B), kAttnThreads, 0, s>>>(aa); break;
+    case 12: {
+      // QKV + attention + O of one row (fused_qkv_attention_o decides when it
+      // applies).
+      QkvArgs qa{ctl, r.h, m->input_norm[l], reinterpret_cast<const u32x4*>(m->qkv[l]), r.q_raw, r.k_raw, vc,
+                 r.v_append_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps};
+      ResidualArgs oa{ctl, r.att, reinterpret_cast<const u32x4*>(m->o[l]), r.h, nullptr, nullptr, QW, D,
+                      static_cast<int>(p->cap), static_cast<int>(l), 0, r.same_sequence, r.sequence};
+      const int qkv_workgroups = (QW / 4 + KW) / kQkvWaves;
+      const int o_workgroups = D / (64 / 16) / kOWaves;
+      const size_t lds = (staged_floats(16, D) + staged_floats(32, D)) * sizeof(float);
+      k_qkv_attn_o<<<qkv_workgroups + c.q_heads + o_workgroups, kAttnThreads, lds, s>>>(
+          QkvAttnOArgs{qa, aa, oa, p->v_new, p->qkvo_sync, qkv_workgroups});
+      break;
+    }
     case 10: {
       // Attention + O of one row (fused_attention_o decides when it applies).
       ResidualArgs oa{ctl, r.att, reinterpret_cast<const u32x4*>(m->o[l]), r.h, nullptr, nullptr, QW, D,
@@ -2696,6 +2903,15 @@ bool fused_attention_o(const dl_plan* p) {
   return p->batch == 1 && QW / (8 * 16) == dl::kOChunks && tiles % dl::kOWaves == 0;
 }
 
+// Whether a short-context step also folds the QKV projection into that
+// launch (k_qkv_attn_o): the QKV tile shapes of the batch-1 whole-tile path
+// (hidden width kWholeTileInputs) in whole workgroups.
+bool fused_qkv_attention_o(const dl_plan* p) {
+  const auto& c = p->model->cfg;
+  const int QW = c.q_heads * c.head_dim, KW = c.kv_heads * c.head_dim;
+  return fused_attention_o(p) && c.hidden == dl::kWholeTileInputs && (QW / 4 + KW) % dl::kQkvWaves == 0;
+}
+
 // Records one decode step.  `short_context` selects the fused attention
 // kernel (positions below kFusedKeys) instead of the three-kernel split;
 // categorical generation adds the device sampler after the LM head.
@@ -2707,12 +2923,15 @@ void record_step_all(dl_plan* p, hipStream_t s, bool short_context) {
                   p->cancel_device, p->injection_status, p->intervention_state(), static_cast<int>(c.hidden),
                   c.vocab, c.tied_embeddings ? 1 : 0, p->journal, static_cast<int>(p->batch)};
   k_step_begin<<<p->batch, kBlock, 0, s>>>(begin);
-  const bool fused_attn = fused_attention_o(p);
+  const bool fused_attn = fused_attention_o(p), fused_qkv = fused_qkv_attention_o(p);
   for (uint32_t l = 0; l < c.layers; ++l) {
-    launch_step_kernel(p, s, 0, l, p->ctl, plan_rows(p));
-    if (short_context && fused_attn) {
+    if (short_context && fused_qkv) {
+      launch_step_kernel(p, s, 12, l, p->ctl, plan_rows(p));
+    } else if (short_context && fused_attn) {
+      launch_step_kernel(p, s, 0, l, p->ctl, plan_rows(p));
       launch_step_kernel(p, s, 10, l, p->ctl, plan_rows(p));
     } else {
+      launch_step_kernel(p, s, 0, l, p->ctl, plan_rows(p));
       if (short_context)
         launch_step_kernel(p, s, 8, l, p->ctl, plan_rows(p));
       else
@@ -2885,6 +3104,9 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
     p->rope = p->alloc<float>(cap * c.head_dim);
     p->attn_sync = p->alloc<uint32_t>(dl::kSyncWords);
     dl::check_hip(hipMemsetAsync(p->attn_sync, 0, dl::kSyncWords * 4, queue->stream), "hand-off clear");
+    p->qkvo_sync = p->alloc<uint32_t>(dl::kQkvoSyncWords);
+    dl::check_hip(hipMemsetAsync(p->qkvo_sync, 0, dl::kQkvoSyncWords * 4, queue->stream), "hand-off clear");
+    p->v_new = p->alloc<uint16_t>(KW);
     p->partial_keys = p->alloc<uint64_t>(B * 1024);
     p->partial_flags = p->alloc<uint32_t>(B * 1024);
     p->tokens = p->alloc<uint32_t>(cap);
@@ -2952,7 +3174,8 @@ int dl_plan_launch_kernel(dl_plan* plan, uint32_t which, uint32_t first_layer, u
   return guard([&] {
     require(plan != nullptr, "null plan");
     dl::enter(plan->queue);
-    require(which <= 8 || (which == 10 && fused_attention_o(plan)), "unknown step kernel");
+    require(which <= 8 || (which == 10 && fused_attention_o(plan)) || (which == 12 && fused_qkv_attention_o(plan)),
+            "unknown step kernel");
     const uint32_t L = plan->model->cfg.layers;
     require(first_layer < L, "layer out of range");
     for (uint32_t i = 0; i < count; ++i) {
@@ -3406,9 +3629,12 @@ int dl_plan_collect(dl_plan* plan, uint32_t* tokens, uint32_t max_new, dl_genera
       plan->queue->device->poisoned = true;
       dl::check_hip(e, "generation");
     }
-    uint32_t handoff = 0;
-    dl::check_hip(hipMemcpy(&handoff, plan->attn_sync + 2, 4, hipMemcpyDeviceToHost), "read hand-off word");
-    if (handoff != 0) {
+    uint32_t handoff = 0, qkvo_handoff = 0;
+    dl::check_hip(hipMemcpy(&handoff, plan->attn_sync + 32 * dl::kAttnOLayout.failure, 4, hipMemcpyDeviceToHost),
+                  "read hand-off word");
+    dl::check_hip(hipMemcpy(&qkvo_handoff, plan->qkvo_sync + 32 * dl::kQkvoLayout.failure, 4, hipMemcpyDeviceToHost),
+                  "read hand-off word");
+    if (handoff != 0 || qkvo_handoff != 0) {
       plan->queue->device->poisoned = true;
       dl::fail(DL_RUNTIME_ERROR, "attention to O hand-off wait expired; the results are invalid");
     }
