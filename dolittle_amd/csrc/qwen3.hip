@@ -1186,13 +1186,25 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
       for (int off = 4; off; off >>= 1) acc = acc + __shfl_down(acc, off, 8);
       if (l == 0 && j < count) sc[j] = acc * a.scale;
     };
+    // A ring of kAttnKeyPasses passes: consuming pass p issues pass
+    // p + kAttnKeyPasses into the same registers, so that many key rows stay
+    // in flight over the whole row.
+    constexpr int kRing = kAttnKeyPasses * kAttnKeysPerPass;
+    for (int base0 = 0; base0 < count; base0 += kRing) {
 #pragma unroll
-    for (int p = 0; p < kAttnKeyPasses; ++p)
-      if (p * kAttnKeysPerPass < count) score(p * kAttnKeysPerPass + kg, kpre[p][0], kpre[p][1]);
-    for (int base = kAttnKeyPasses * kAttnKeysPerPass; base < count; base += kAttnKeysPerPass) {
-      const int j = min(base + kg, count - 1);
-      const u32x4* src = reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(j) * kHeadDim + 16 * l);
-      score(base + kg, src[0], src[1]);
+      for (int p = 0; p < kAttnKeyPasses; ++p) {
+        const int base = base0 + p * kAttnKeysPerPass;
+        if (base < count) {
+          const u32x4 w0 = kpre[p][0], w1 = kpre[p][1];
+          if (base + kRing < count) {
+            const int j = min(base + kRing + kg, count - 1);
+            const u32x4* src = reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(j) * kHeadDim + 16 * l);
+            kpre[p][0] = src[0];
+            kpre[p][1] = src[1];
+          }
+          score(base + kg, w0, w1);
+        }
+      }
     }
   }
   __syncthreads();
@@ -1211,8 +1223,18 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
   for (int j = tid; j < count; j += kAttnThreads) sc[j] = dl_expf(sc[j] - m);
   __syncthreads();
   if (tid < 32) {
+    // The partial's additions in ascending key order, its LDS reads issued
+    // eight at a time.
     float partial = 0.0f;
-    for (int j = tid; j < count; j += 32) partial = partial + sc[j];
+    int j = tid;
+    for (; j + 7 * 32 < count; j += 8 * 32) {
+      float e[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) e[k] = sc[j + 32 * k];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) partial = partial + e[k];
+    }
+    for (; j < count; j += 32) partial = partial + sc[j];
 #pragma unroll
     for (int off = 16; off; off >>= 1) partial = partial + __shfl_down(partial, off, 32);
     if (tid == 0) denominator_shared = partial;
@@ -1248,25 +1270,44 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
       // (wave-uniform: pos, jb and the chain's range are).
       const int pi = static_cast<int>(pos) - jb;
       const bool patch = kFromQkv && pi >= lo && pi < hi;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      // Wave-uniform branches: a block wholly inside the chain runs its 64
+      // steps straight; in the chain's first and last blocks (and the one
+      // holding `pos`) each 8-key group is skipped, run straight or run
+      // masked; a block past the chain does nothing.
+      if (hi <= lo) return;
+      auto group = [&](int i, bool full) {
         float vf[8] = {dl_bf16_lo(vb[i].x), dl_bf16_hi(vb[i].x), dl_bf16_lo(vb[i].y), dl_bf16_hi(vb[i].y),
                        dl_bf16_lo(vb[i].z), dl_bf16_hi(vb[i].z), dl_bf16_lo(vb[i].w), dl_bf16_hi(vb[i].w)};
-        if (patch) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) vf[e] = 8 * i + e == pi ? v_pos : vf[e];
-        }
         const float pf[8] = {pc[2 * i].x, pc[2 * i].y, pc[2 * i].z, pc[2 * i].w,
                              pc[2 * i + 1].x, pc[2 * i + 1].y, pc[2 * i + 1].z, pc[2 * i + 1].w};
-        if (lo == 0 && hi == 64) {
+        if (full) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) acc = fma_rn(pf[e], vf[e], acc);
         } else {
+          if (patch) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vf[e] = 8 * i + e == pi ? v_pos : vf[e];
+          }
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const float t = fma_rn(pf[e], vf[e], acc);
             acc = (8 * i + e >= lo && 8 * i + e < hi) ? t : acc;
           }
+        }
+      };
+      if (lo == 0 && hi == 64 && !patch) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) group(i, true);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int g0 = 8 * i;
+          if (g0 >= hi || g0 + 8 <= lo) continue;
+          const bool holds_pos = patch && pi >= g0 && pi < g0 + 8;
+          if (g0 >= lo && g0 + 8 <= hi && !holds_pos)
+            group(i, true);
+          else
+            group(i, false);
         }
       }
     };
@@ -3011,7 +3052,10 @@ void reset_intervention(dl_plan* p) {
 void launch_steps(dl_plan* p, uint32_t steps) {
   p->steps_enqueued += steps;
   for (uint32_t i = 0; i < steps; ++i) {
-    const bool short_context = p->host_position < static_cast<uint64_t>(dl::kFusedKeys);
+    // A plan whose cache ends at or below kFusedKeys has only the short
+    // graph (capture_step); its steps past the capacity find the loop
+    // stopped and replay that one.
+    const bool short_context = p->host_position < static_cast<uint64_t>(dl::kFusedKeys) || p->execs[0] == nullptr;
     if (p->eager)
       p->record_step(p->queue->stream, short_context);
     else

@@ -23,6 +23,8 @@ event.
   terminal event is cancelled with position = prompt + generated.
 - bounded window: an eos at token k of 100 leaves at most 2 windows of
   steps enqueued past the stop.
+- idle steps past a capacity below the one-kernel attention limit replay
+  the short-context graph and change nothing.
 - batch 2 where one sequence stops early: per-sequence terminal events.
 - a resumed prompt pass opens the journal with one consumed event
   covering the prefilled positions.
@@ -183,6 +185,20 @@ def test_window_bounds_the_steps_after_a_stop(small_model):
     plan.generate(p, new, stop_ids=[stream[k]])
     plan.collect()
     assert plan.steps_enqueued() == len(p) + new
+
+
+def test_idle_steps_past_a_short_capacity(small_model):
+    """A plan whose cache ends below the one-kernel attention limit has
+    only the short-context step graph; replaying steps past its capacity
+    (beyond that limit) finds the loop stopped and changes nothing."""
+    from dolittle_amd.qwen3 import Plan
+    p = [9, 8, 7]
+    plan = Plan(small_model, batch=1, capacity=64)
+    plan.generate(p, 8)
+    tokens, results = plan.collect()
+    plan.decode_steps(1100)
+    again, results_again = plan.collect()
+    assert again.tolist() == tokens.tolist() and results_again == results
 
 
 def test_batch_two_sequence_stops_early(small_model):
