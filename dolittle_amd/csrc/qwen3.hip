@@ -1056,9 +1056,17 @@ __device__ __forceinline__ void handoff_raise(const Handoff& hs, int go) {
 // device-coherently after the go flag `qkv_go` (a Handoff whose `go` names
 // those lines), and the chain holding the current position takes its value
 // from `v_new` (the V cache column is written in this launch too).
-template <bool kHandoff = false, bool kFromQkv = false>
+//
+// kSplit > 1 spreads one head's PV over kSplit workgroups: `slot` then runs
+// over q_heads x kSplit, and part slot / q_heads owns features
+// [part F, part F + F), F = 128 / kSplit, as one wavefront per chain half.
+// Every part computes the head's scores and softmax itself (identical
+// values), so no part waits for another; the parts' PV chains run on
+// different compute units.
+template <bool kHandoff = false, bool kFromQkv = false, int kSplit = 1>
 __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int b, const Handoff* qkv_go = nullptr,
                                                 const uint16_t* v_new = nullptr) {
+  static_assert(kSplit == 1 || kSplit == 2 || kSplit == 4, "a head splits into 1, 2 or 4 feature parts");
   __shared__ float qs[kHeadDim];
   __shared__ float ks[kHeadDim];
   __shared__ __align__(16) float sc[kFusedKeys];
@@ -1069,7 +1077,8 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
   // query heads group-minor puts the heads of one K/V group on one XCD, whose
   // L2 then serves the group's key and value rows once for all of them.
   const int group = a.q_heads / a.kv_heads;
-  const int g = slot % a.kv_heads, h = g * group + slot / a.kv_heads;
+  const int part = slot / a.q_heads, head_slot = slot % a.q_heads;
+  const int g = head_slot % a.kv_heads, h = g * group + head_slot / a.kv_heads;
   const int tid = threadIdx.x;
   const int wave = tid / 64, lane = tid % 64;
   const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHeadDim, kw = static_cast<uint64_t>(a.kv_heads) * kHeadDim;
@@ -1112,14 +1121,17 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
     kpre[p][0] = src[0];
     kpre[p][1] = src[1];
   }
-  // PV chains: thread f + 128 * half (half 0: keys [0, split), half 1:
-  // [split, count)), one chain per lane; waves 0-1 and 2-3 hold the halves.
+  // PV chains: one chain per lane of feature f and half (half 0: keys
+  // [0, split), half 1: [split, count)).  Whole heads: waves 0-1 and 2-3
+  // hold the halves (64 features each); parts: wave 0 and wave 1.
   const int split = (count - 1) / 2 + 1;
-  // Wave-uniform chain half (waves 0-1: keys [0, split), waves 2-3: the
-  // rest), so the PV loop bounds stay in scalar registers.
-  const int half = __builtin_amdgcn_readfirstlane(wave) / 2;
-  const int f = tid % kHeadDim;
-  const bool chain = wave < 4;
+  // Wave-uniform chain half, so the PV loop bounds stay in scalar registers.
+  constexpr int kPartFeatures = kHeadDim / kSplit;
+  constexpr int kHalfWaves = kSplit == 1 ? 2 : 1;
+  const int half = __builtin_amdgcn_readfirstlane(wave) / kHalfWaves;
+  const int fl = (wave % kHalfWaves) * 64 + lane;  // feature within the part
+  const int f = part * kPartFeatures + fl % kPartFeatures;
+  const bool chain = wave < 2 * kHalfWaves && fl < kPartFeatures;
   const int begin = half ? split : 0, end = half ? count : split;
   const int first_block = begin & ~7;
   const uint16_t* v = a.v_cache + b * a.cache_seq_stride + static_cast<uint64_t>(g * kHeadDim + f) * a.cap;
@@ -1154,7 +1166,7 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
   if (wave == 0) head_norm_rope(head, lane, a.eps, qs);
   if (wave == 1) {
     head_norm_rope(head, lane, a.eps, ks);
-    if (h % group == 0) {
+    if (h % group == 0 && part == 0) {
       kc[pos * kHeadDim + lane] = bf16_bits(ks[lane]);
       kc[pos * kHeadDim + lane + 64] = bf16_bits(ks[lane + 64]);
     }
@@ -1328,19 +1340,20 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
       }
       if (x < blocks) run(va, x);
     }
-    red[tid] = acc;
+    red[half * kHeadDim + fl] = acc;
   }
   __syncthreads();
+  uint16_t* att = a.att + static_cast<uint64_t>(b) * qw + h * kHeadDim + part * kPartFeatures;
   if constexpr (kHandoff) {
-    if (tid < kHeadDim / 2) {
+    if (tid < kPartFeatures / 2) {
       const uint32_t lo = bf16_bits(red[2 * tid] + red[2 * tid + kHeadDim]);
       const uint32_t hi = bf16_bits(red[2 * tid + 1] + red[2 * tid + 1 + kHeadDim]);
-      uint32_t* out = reinterpret_cast<uint32_t*>(a.att + static_cast<uint64_t>(b) * qw + h * kHeadDim) + tid;
-      __hip_atomic_store(out, lo | (hi << 16), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(reinterpret_cast<uint32_t*>(att) + tid, lo | (hi << 16), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
       __builtin_amdgcn_s_waitcnt(pv_vmcnt(0));
     }
   } else {
-    if (tid < kHeadDim) a.att[static_cast<uint64_t>(b) * qw + h * kHeadDim + tid] = bf16_bits(red[tid] + red[tid + kHeadDim]);
+    if (tid < kPartFeatures) att[tid] = bf16_bits(red[tid] + red[tid + kHeadDim]);
   }
   return true;
 }
@@ -1512,8 +1525,9 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual_chunked(Residua
 
 // --------------------------------------- attention + O projection, batch 1
 // One launch for a short-context step's attention and O projection of a
-// single row.  Workgroups [0, q_heads) run the fused attention of one query
-// head each; the others each own 8 O tiles (one per wavefront).  An O
+// single row.  Workgroups [0, q_heads kAttnSplit) run the fused attention,
+// kAttnSplit per query head (each the PV chains of its part of the head's
+// features); the others each own 8 O tiles (one per wavefront).  An O
 // wavefront issues its whole weight tile (kOChunks 16-byte chunks per lane)
 // at entry, so the O weights stream from HBM while the attention runs, then
 // waits for the attention output, stages it and runs the tile's chains from
@@ -1528,6 +1542,9 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual_chunked(Residua
 // waiting workgroups come after the ones they wait for in the grid, which
 // are dispatched first, and the waits are bounded (handoff_wait).
 constexpr int kOChunks = 32;           // 16-byte weight chunks per lane: I / (8 P) with I = 4096, P = 16
+// Workgroups per query head (feature parts of its PV): 2 measured better
+// than 1 and 4 in both fused launches.
+constexpr int kAttnSplit = 2;
 constexpr int kOWaves = kAttnThreads / 64;
 // k_attn_o's lines: attention count 0, go 1-8, O exit 9, failure 10.
 constexpr Handoff kAttnOLayout{nullptr, 1, 9, 10};
@@ -1603,11 +1620,11 @@ __device__ __forceinline__ void handoff_signal(const Handoff& hs, int count, uin
 }
 
 __global__ __launch_bounds__(kAttnThreads) void k_attn_o(AttnOArgs a) {
-  const uint32_t heads = static_cast<uint32_t>(a.attn.q_heads);
+  const uint32_t heads = static_cast<uint32_t>(a.attn.q_heads) * kAttnSplit;
   Handoff hs = kAttnOLayout;
   hs.words = a.sync;
   if (blockIdx.x < heads) {
-    if (!attn_fused_body<true>(a.attn, blockIdx.x, 0)) return;
+    if (!attn_fused_body<true, false, kAttnSplit>(a.attn, blockIdx.x, 0)) return;
     __syncthreads();  // every output word of this workgroup has been written
     handoff_signal(hs, kAttnOCount, heads, hs.go);
     return;
@@ -1617,9 +1634,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_o(AttnOArgs a) {
 
 // ------------------------------------ QKV + attention + O projection, batch 1
 // One launch for a short-context step's QKV projection, attention and O
-// projection of a single row: workgroups [0, kQkvWorkgroups) own one QKV
+// projection of a single row: workgroups [0, qkv_workgroups) own one QKV
 // tile per wavefront (held in registers, as k_qkv's batch-1 path), then the
-// attention workgroups, then the O workgroups (as in k_attn_o).  The QKV
+// attention workgroups (kAttnSplit per query head), then the O workgroups
+// (as in k_attn_o).  The QKV
 // workgroups write q and k with device-coherent stores, the new V values
 // both into the cache column (for later steps) and, device-coherently, into
 // `v_new` (for this launch's attention, which substitutes them at the
@@ -1720,7 +1738,7 @@ __device__ __forceinline__ void qkv_phase(const QkvArgs& a, uint16_t* v_new, con
 }
 
 __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_qkv_attn_o(QkvAttnOArgs a) {
-  const uint32_t heads = static_cast<uint32_t>(a.attn.q_heads), nq = static_cast<uint32_t>(a.qkv_workgroups);
+  const uint32_t heads = static_cast<uint32_t>(a.attn.q_heads) * kAttnSplit, nq = static_cast<uint32_t>(a.qkv_workgroups);
   Handoff hs = kQkvoLayout;
   hs.words = a.sync;
   if (blockIdx.x < nq) {
@@ -1730,7 +1748,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2)
   if (blockIdx.x < nq + heads) {
     Handoff qkv_go = hs;
     qkv_go.go = kQkvoQkvGo;
-    if (!attn_fused_body<true, true>(a.attn, blockIdx.x - nq, 0, &qkv_go, a.v_new)) return;
+    if (!attn_fused_body<true, true, kAttnSplit>(a.attn, blockIdx.x - nq, 0, &qkv_go, a.v_new)) return;
     __syncthreads();  // every output word of this workgroup has been written
     handoff_signal(hs, kQkvoAttnCount, heads, hs.go);
     return;
@@ -2860,7 +2878,7 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       const int qkv_workgroups = (QW / 4 + KW) / kQkvWaves;
       const int o_workgroups = D / (64 / 16) / kOWaves;
       const size_t lds = (staged_floats(16, D) + staged_floats(32, D)) * sizeof(float);
-      k_qkv_attn_o<<<qkv_workgroups + c.q_heads + o_workgroups, kAttnThreads, lds, s>>>(
+      k_qkv_attn_o<<<qkv_workgroups + c.q_heads * kAttnSplit + o_workgroups, kAttnThreads, lds, s>>>(
           QkvAttnOArgs{qa, aa, oa, p->v_new, p->qkvo_sync, qkv_workgroups});
       break;
     }
@@ -2869,7 +2887,8 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       ResidualArgs oa{ctl, r.att, reinterpret_cast<const u32x4*>(m->o[l]), r.h, nullptr, nullptr, QW, D,
                       static_cast<int>(p->cap), static_cast<int>(l), 0, r.same_sequence, r.sequence};
       const int o_workgroups = D / (64 / 16) / kOWaves;
-      k_attn_o<<<c.q_heads + o_workgroups, kAttnThreads, p16_lds(1, QW), s>>>(AttnOArgs{aa, oa, p->attn_sync});
+      k_attn_o<<<c.q_heads * kAttnSplit + o_workgroups, kAttnThreads, p16_lds(1, QW), s>>>(
+          AttnOArgs{aa, oa, p->attn_sync});
       break;
     }
     case 9: k_append_keys<<<dim3(c.kv_heads, B), 64, 0, s>>>(aa); break;
