@@ -16,10 +16,9 @@ tests/core/test_qwen3_chat.cpp):
   A Cursor carries the state across chunks at absolute positions.
 
 Encoding uses a tokenizer object with `encode(text) -> list[int]`; for a
-checkpoint's tokenizer.json, `ByteLevelTokenizer` wraps the installed
-Hugging Face `tokenizers` library (the library the reference's validation
-bundles record their tokenizer vectors with).  The reference's own byte-BPE
-(src/tokenizers/byte_bpe.h) is not restated here.
+checkpoint's tokenizer.json and tokenizer_config.json, `ByteLevelTokenizer`
+is this package's byte-level BPE (dolittle_amd/tokenizer.py, the
+restatement of src/tokenizers/byte_bpe.h).
 """
 from __future__ import annotations
 
@@ -105,16 +104,20 @@ def segment(ids: Sequence[int], position: int, thinking: bool = True) -> list:
 
 
 class ByteLevelTokenizer:
-    """A checkpoint's tokenizer.json through the installed `tokenizers`
-    library: encode without added BOS/EOS, decode keeping added-token
-    spellings."""
+    """A checkpoint's tokenizer through this package's byte-level BPE:
+    encode with no BOS/EOS, decode to text keeping added-token spellings
+    (bytes that do not form UTF-8 shown as U+FFFD; `tokenizer.decode` keeps
+    the raw bytes and each ID's range)."""
 
-    def __init__(self, tokenizer_json: str):
-        from tokenizers import Tokenizer
-        self._tok = Tokenizer.from_str(tokenizer_json)
+    def __init__(self, tokenizer_json, tokenizer_config_json, identity: str = "unverified",
+                 limits: Optional["ByteBpeLimits"] = None):
+        from .tokenizer import ByteBpeLimits, make_byte_bpe
+        limits = limits or ByteBpeLimits(64 << 20, 1 << 24, 1 << 20, 1 << 22)
+        self.tokenizer = make_byte_bpe(tokenizer_json, tokenizer_config_json, identity, limits)
 
     def encode(self, text: str) -> list:
-        return self._tok.encode(text, add_special_tokens=False).ids
+        return self.tokenizer.encode(text)
 
     def decode(self, ids: Sequence[int]) -> str:
-        return self._tok.decode(list(ids), skip_special_tokens=False)
+        from .tokenizer import presentation
+        return presentation(self.tokenizer.decode(ids))

@@ -58,13 +58,16 @@ def test_chunk_invariance(split):
     assert [(s.position, s.kind) for s in prefix + suffix] == [(19 + i, k) for i, k in enumerate(KINDS)]
 
 
-def test_tokenizer_json_wrapper():
-    from tokenizers import Tokenizer, models, pre_tokenizers
-    vocab = {"[UNK]": 0, "hello": 1, "world": 2}
-    tok = Tokenizer(models.WordLevel(vocab, unk_token="[UNK]"))
-    tok.pre_tokenizer = pre_tokenizers.Whitespace()
-    tok.add_special_tokens(["<|im_start|>", "<|im_end|>"])
-    wrapped = t.ByteLevelTokenizer(tok.to_str())
-    ids = wrapped.encode("<|im_start|>hello world<|im_end|>")
-    assert ids == [3, 1, 2, 4]
-    assert wrapped.decode([3]) == "<|im_start|>"
+def test_tokenizer_wrapper_encodes_the_chat_prompt():
+    """The chat prompt through this package's byte-level BPE on the
+    reference's tokenizer fixture: the chat markers are added tokens with
+    their declared IDs, and decoding returns the prompt."""
+    import os
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    tok = t.ByteLevelTokenizer(open(os.path.join(golden, "byte_bpe_tokenizer.json")).read(),
+                               open(os.path.join(golden, "qwen3_tokenizer_config.json")).read())
+    prompt = t.format_prompt("hi", thinking=False)
+    ids = tok.encode(prompt)
+    assert ids[0] == t.IM_START and t.IM_END in ids and t.THINK_OPEN in ids and t.THINK_CLOSE in ids
+    assert ids[1:5] == [117, 115, 101, 114]  # "user": one byte symbol each (the fixture has four merges)
+    assert tok.decode(ids) == prompt
