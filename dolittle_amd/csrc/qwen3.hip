@@ -1358,7 +1358,10 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
   return true;
 }
 
-__global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) { attn_fused_body(a, blockIdx.x, blockIdx.y); }
+template <int kSplit>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_fused(AttnArgs a) {
+  attn_fused_body<false, false, kSplit>(a, blockIdx.x, blockIdx.y);
+}
 
 // ------------------------------------------------- residual GEMV (O, down)
 struct ResidualArgs {
@@ -2867,7 +2870,14 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       else
         k_attn_pv_rows<<<dim3(c.kv_heads * (kHeadDim / kPwFeatures), B), kPwThreads, 0, s>>>(aa);
       break;
-    case 8: k_attn_fused<<<dim3(c.q_heads, B), kAttnThreads, 0, s>>>(aa); break;
+    case 8:
+      // Up to four rows, two workgroups per query head (see kAttnSplit);
+      // eight rows already fill the GPU with one.
+      if (B <= 4)
+        k_attn_fused<2><<<dim3(c.q_heads * 2, B), kAttnThreads, 0, s>>>(aa);
+      else
+        k_attn_fused<1><<<dim3(c.q_heads, B), kAttnThreads, 0, s>>>(aa);
+      break;
     case 12: {
       // QKV + attention + O of one row (fused_qkv_attention_o decides when it
       // applies).
