@@ -33,6 +33,16 @@ __device__ __forceinline__ float storage_round<float>(float v) {
 
 __device__ __forceinline__ float fma_rn(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 
+// The value of lane + kOff for kOff in {1, 2, 4, 8}, moved within a 16-lane
+// row by DPP (row_shl) instead of the LDS crossbar; lanes whose source lies
+// past their row receive 0.  A tree that only reads lanes of its own group of
+// 2 kOff lanes gets the same values as __shfl_down.
+template <int kOff>
+__device__ __forceinline__ float row_down(float v) {
+  static_assert(kOff == 1 || kOff == 2 || kOff == 4 || kOff == 8, "DPP row shifts within 16 lanes");
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + kOff, 0xf, 0xf, true));
+}
+
 // Streaming 16-byte load that bypasses cache retention (weights are read once).
 __device__ __forceinline__ u32x4 load_stream(const u32x4* p) { return __builtin_nontemporal_load(p); }
 

@@ -277,13 +277,18 @@ __device__ __forceinline__ void chain_body(const u32x4* __restrict__ tile, const
   for (; s0 < S; ++s0) chain_step<B>(load_stream(src + s0 * 64), xt, bstride, s0, acc);
 }
 
-// Merges the P partials of each row (offsets P/2 .. 1) into lane (row, 0).
+// Merges the P partials of each row (offsets P/2 .. 1) into lane (row, 0);
+// offsets below 16 move within a 16-lane row (DPP).
 template <int P, int B>
 __device__ __forceinline__ void chain_merge(float (&acc)[B]) {
+  static_assert(P == 16 || P == 32, "16 or 32 partials per row");
 #pragma unroll
   for (int b = 0; b < B; ++b) {
-#pragma unroll
-    for (int off = P / 2; off; off >>= 1) acc[b] = acc[b] + __shfl_down(acc[b], off, P);
+    if constexpr (P == 32) acc[b] = acc[b] + __shfl_down(acc[b], 16, P);
+    acc[b] = acc[b] + row_down<8>(acc[b]);
+    acc[b] = acc[b] + row_down<4>(acc[b]);
+    acc[b] = acc[b] + row_down<2>(acc[b]);
+    acc[b] = acc[b] + row_down<1>(acc[b]);
   }
 }
 

@@ -556,9 +556,11 @@ __global__ __launch_bounds__(kBlock) void k_attn_qk(AttnArgs a) {
         for (int i = 0; i < 16; ++i) acc[h] = fma_rn(q[h][i], kf[i], acc[h]);
     }
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
-#pragma unroll
-      for (int off = 4; off; off >>= 1) acc[h] = acc[h] + __shfl_down(acc[h], off, 8);
+    for (int h = 0; h < 4; ++h) {
+      acc[h] = acc[h] + row_down<4>(acc[h]);
+      acc[h] = acc[h] + row_down<2>(acc[h]);
+      acc[h] = acc[h] + row_down<1>(acc[h]);
+    }
     if (l == 0 && j < count) {
 #pragma unroll
       for (int h = 0; h < 4; ++h)
@@ -1194,8 +1196,9 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
       float acc = 0.0f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc = fma_rn(q[i], kf[i], acc);
-#pragma unroll
-      for (int off = 4; off; off >>= 1) acc = acc + __shfl_down(acc, off, 8);
+      acc = acc + row_down<4>(acc);
+      acc = acc + row_down<2>(acc);
+      acc = acc + row_down<1>(acc);
       if (l == 0 && j < count) sc[j] = acc * a.scale;
     };
     // A ring of kAttnKeyPasses passes: consuming pass p issues pass
