@@ -33,14 +33,25 @@ __device__ __forceinline__ float storage_round<float>(float v) {
 
 __device__ __forceinline__ float fma_rn(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 
-// The value of lane + kOff for kOff in {1, 2, 4, 8}, moved within a 16-lane
-// row by DPP (row_shl) instead of the LDS crossbar; lanes whose source lies
-// past their row receive 0.  A tree that only reads lanes of its own group of
-// 2 kOff lanes gets the same values as __shfl_down.
+// The value of lane + kOff (1 <= kOff <= 15), moved within a 16-lane row by
+// DPP (row_shl) instead of the LDS crossbar; lanes whose source lies past
+// their row receive 0.  A reduction whose needed lanes only read lanes of
+// their own row gets the same values as __shfl_down.
 template <int kOff>
 __device__ __forceinline__ float row_down(float v) {
-  static_assert(kOff == 1 || kOff == 2 || kOff == 4 || kOff == 8, "DPP row shifts within 16 lanes");
+  static_assert(kOff >= 1 && kOff <= 15, "DPP row shifts within 16 lanes");
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + kOff, 0xf, 0xf, true));
+}
+
+// The adjacent-first tree over 32 lanes (offsets 1, 2, 4, 8, 16 as
+// __shfl_down(s, off, 32)); lane 0 of each 32-lane half holds the total.
+// Offsets below 16 stay in the row of the lanes that feed lane 0.
+__device__ __forceinline__ float tree_sum32(float s) {
+  s = s + row_down<1>(s);
+  s = s + row_down<2>(s);
+  s = s + row_down<4>(s);
+  s = s + row_down<8>(s);
+  return s + __shfl_down(s, 16, 32);
 }
 
 // Streaming 16-byte load that bypasses cache retention (weights are read once).

@@ -316,16 +316,14 @@ __device__ __forceinline__ float block_rms_inverse(const uint16_t* __restrict__ 
       const float v = dl_bf16_to_f32(x[col]);
       comp = comp + v * v;
     }
-    const float second = __shfl_down(comp, 1, 4);
-    const float third = __shfl_down(comp, 2, 4);
-    const float fourth = __shfl_down(comp, 3, 4);
+    const float second = row_down<1>(comp);
+    const float third = row_down<2>(comp);
+    const float fourth = row_down<3>(comp);
     if ((tid & 3) == 0) scratch[tid >> 2] = ((comp + second) + third) + fourth;
   }
   __syncthreads();
   if (tid < 32) {
-    float s = scratch[tid];
-#pragma unroll
-    for (int off = 1; off < 32; off *= 2) s = s + __shfl_down(s, off, 32);
+    const float s = tree_sum32(scratch[tid]);
     if (tid == 0) scratch[32] = inverse_sqrt(s * (1.0f / static_cast<float>(D)) + eps);
   }
   __syncthreads();
@@ -381,18 +379,16 @@ __device__ __forceinline__ bool norm_stage_pass(const uint16_t* __restrict__ h, 
       float comp = 0.0f;
 #pragma unroll
       for (int k = 0; k < kNormK; ++k) comp = comp + hv[b][k] * hv[b][k];
-      const float second = __shfl_down(comp, 1, 4);
-      const float third = __shfl_down(comp, 2, 4);
-      const float fourth = __shfl_down(comp, 3, 4);
+      const float second = row_down<1>(comp);
+      const float third = row_down<2>(comp);
+      const float fourth = row_down<3>(comp);
       if ((t & 3) == 0) scratch[(R * g + b) * 40 + (t >> 2)] = ((comp + second) + third) + fourth;
     }
   }
   __syncthreads();
   if (has0 && t < 32 * R) {
     const int slot = R * g + t / 32;
-    float s = scratch[slot * 40 + (t & 31)];
-#pragma unroll
-    for (int off = 1; off < 32; off *= 2) s = s + __shfl_down(s, off, 32);
+    const float s = tree_sum32(scratch[slot * 40 + (t & 31)]);
     if ((t & 31) == 0) scratch[slot * 40 + 32] = inverse_sqrt(s * (1.0f / static_cast<float>(D)) + eps);
   }
   __syncthreads();

@@ -25,9 +25,7 @@ __device__ __forceinline__ void head_norm_rope(const HeadOperands& o, int lane, 
   const float xa = o.xa, xb = o.xb;
   const float xa_hi = __shfl(xa, (lane + 32) & 63);
   const float xb_hi = __shfl(xb, (lane + 32) & 63);
-  float s = ((xa * xa + xa_hi * xa_hi) + xb * xb) + xb_hi * xb_hi;
-#pragma unroll
-  for (int off = 1; off < 32; off *= 2) s = s + __shfl_down(s, off, 32);
+  const float s = tree_sum32(((xa * xa + xa_hi * xa_hi) + xb * xb) + xb_hi * xb_hi);
   const float total = __shfl(s, 0);
   const float inverse = inverse_sqrt(total * (1.0f / 128.0f) + eps);
   const float na = dl_round_bf16(dl_round_bf16(xa * inverse) * o.ga);
