@@ -3086,8 +3086,10 @@ void launch_steps(dl_plan* p, uint32_t steps) {
   for (uint32_t i = 0; i < steps; ++i) {
     // A plan whose cache ends at or below kFusedKeys has only the short
     // graph (capture_step); its steps past the capacity find the loop
-    // stopped and replay that one.
-    const bool short_context = p->host_position < static_cast<uint64_t>(dl::kFusedKeys) || p->execs[0] == nullptr;
+    // stopped and replay that one.  The choice depends on the capacity, not
+    // on which graphs exist: eager launches capture none.
+    const bool short_context = p->host_position < static_cast<uint64_t>(dl::kFusedKeys) ||
+                               p->cap <= static_cast<uint32_t>(dl::kFusedKeys);
     if (p->eager)
       p->record_step(p->queue->stream, short_context);
     else

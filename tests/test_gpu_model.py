@@ -152,6 +152,34 @@ def test_single_block_both_attention_paths(device, queue, oracle, position):
     assert np.array_equal(plan.hidden(0), run.h)
 
 
+@pytest.mark.parametrize("position", [1023, 1024, 4607])
+def test_eager_launches_pick_the_attention_path_by_position(device, queue, oracle, monkeypatch, position):
+    """DL_EAGER=1 launches the step kernels directly (no graphs are
+    captured); the attention path still follows the position, so a step at
+    1024 keys or more runs the three-kernel split and equals the oracle."""
+    from dolittle_amd.qwen3 import Plan, Qwen3Model
+    monkeypatch.setenv("DL_EAGER", "1")
+    model = Qwen3Model(device, queue, qwen_config(layers=1, vocab=2048))
+    model.fill_synthetic(SEED + 7, 0.02)
+    w = oracle_weights(oracle, model)
+    capacity = position + 64
+    plan = Plan(model, batch=1, capacity=capacity)
+    kw = 8 * 128
+    keys = oracle.normal_bf16(position * kw, SEED + 5, 2000, 1.0)
+    values = oracle.normal_bf16(position * kw, SEED + 5, 2001, 1.0)
+    plan.write_cache(0, 0, keys, values)
+    x = oracle.normal_bf16(4096, SEED + 5, 2002, 1.0)
+    plan.set_embedding_override(position, x, 1)
+    plan.seek(position)
+    plan.forward([0])
+    run = OracleRun(oracle, w, capacity)
+    run.k[0][: position * kw] = keys
+    run.v[0][: position * kw] = values
+    run.pos = position
+    run.step(0, logits=False, row=x)
+    assert np.array_equal(plan.hidden(0), run.h)
+
+
 def test_greedy_stream_bit_exact(small_model, oracle):
     """Prefill + greedy decode through the device-owned loop equals the
     contract mirror token for token, and the final logits bit for bit."""
