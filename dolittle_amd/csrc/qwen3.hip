@@ -628,32 +628,42 @@ __global__ __launch_bounds__(kSoftmaxThreads) void k_attn_softmax(AttnArgs a) {
   for (int j = tid; j < count; j += kSoftmaxThreads) a.probs[row + j] = es[j] / l;
 }
 
-// Grid (kv head * 32 feature blocks, sequence), 128 threads.  Wave 0 runs
+// Grid (kv head * 32 feature blocks, sequence), 192 threads.  Wave 0 runs
 // both PV key ranges (the first ceil(n/2) keys and the rest) for the group's
 // 4 query heads x 4 features: lane = (range, head, feature) in lanes 0-31;
 // each output feature is round(A + B), A and B ascending FMA chains
 // (attention.cu:331-375).  One wave holds both ranges, so the kernel's VALU
 // time is one wave's chain however the waves are placed on SIMDs.
 //
-// The keys go through LDS in chunks of kPvChunk.  Wave 1 only copies: each
-// chunk's 8 V rows (BF16, both ranges) and 8 probability rows (FP32) go from
-// global memory straight into a kPvSlots-slot LDS ring (global_load_lds, no
-// registers in flight), kPvSlots - 1 chunks ahead of the chains, with
-// explicit vmcnt waits and plain barriers (a fenced barrier would wait for
-// every copy in flight).  The copy rate of a workgroup is bounded by the
-// bytes it keeps in flight, so the work is spread over 256 workgroups, one
-// per CU.  A copy instruction writes 64 x 16 bytes contiguously; its lanes
-// fetch the rows interleaved 16 bytes at a time and its block is padded, so
-// the rows the chain wave reads at one key fall in distinct banks.
+// A wave issues at most one instruction per issue cycle of its SIMD, so the
+// chain wave's time is its instruction count per key: one FMA, a quarter of
+// a 16-byte LDS read for V and one for the probabilities, and its waits.
+// The other two waves keep everything else off it:
+// - wave 1 copies: each chunk's 8 V rows (BF16, both ranges) and 8
+//   probability rows (FP32) go from global memory straight into a
+//   kPvSlots-slot LDS ring (global_load_lds, no registers in flight),
+//   kPvSlots - 1 chunks ahead of the chains, with explicit vmcnt waits and
+//   plain barriers (a fenced barrier would wait for every copy in flight);
+// - wave 2 widens the V rows of the next chunk to FP32 into one of two
+//   buffers while the chains run the current one.
+// The copy rate of a workgroup is bounded by the bytes it keeps in flight,
+// so the work is spread over 256 workgroups, one per CU.  A copy instruction
+// writes 64 x 16 bytes contiguously; its lanes fetch the rows interleaved 16
+// bytes at a time and its block is padded; the widened rows are padded by
+// 16 bytes, so the rows the chain wave reads at one key fall in distinct
+// banks.
 constexpr int kPvFeatures = 4;
-constexpr int kPvThreads = 128;
+constexpr int kPvThreads = 192;
 constexpr int kPvChunk = 128;
-constexpr int kPvSlots = 9;             // chunks in the copy ring (static LDS stays under 64 KiB)
+constexpr int kPvSlots = 12;            // chunks in the copy ring
 constexpr int kPvVBlocks = 2;           // V blocks per chunk (4 rows each)
 constexpr int kPvCopies = 6;            // global_load_lds per chunk: 2 V blocks + 4 probability blocks
 constexpr int kPvBlock = 1024 + 64;     // bytes per copy block in LDS (64 lanes x 16 bytes + pad)
 constexpr int kPvSlotBytes = kPvCopies * kPvBlock;
-constexpr int kPvInFlight = (kPvSlots - 2) * kPvCopies;  // copies a step leaves outstanding
+constexpr int kPvInFlight = (kPvSlots - 3) * kPvCopies;  // copies a step leaves outstanding
+constexpr int kPvWideRow = kPvChunk * 4 + 16;              // bytes per widened V row (FP32, padded)
+constexpr int kPvWideBytes = 2 * kPvFeatures * kPvWideRow;  // one chunk's 8 widened rows
+constexpr size_t kPvLds = size_t(kPvSlots) * kPvSlotBytes + 2 * kPvWideBytes;
 
 typedef __attribute__((address_space(3))) void pv_lds_void;
 typedef __attribute__((address_space(1))) void pv_global_void;
@@ -662,9 +672,14 @@ typedef __attribute__((address_space(1))) void pv_global_void;
 // this wave are outstanding (vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt
 // left at their no-wait maxima).
 constexpr unsigned pv_vmcnt(unsigned n) { return 0x0f70u | (n & 0xfu) | ((n >> 4) << 14); }
+// s_waitcnt immediate waiting until no LDS operation of this wave is
+// outstanding (lgkmcnt bits 11:8 zero; vmcnt and expcnt at their maxima).
+constexpr unsigned kPvLdsDone = 0xc07fu;
 
 __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
-  __shared__ __align__(16) uint8_t ring[kPvSlots * kPvSlotBytes];
+  extern __shared__ __align__(16) uint8_t pv_lds[];
+  uint8_t* ring = pv_lds;
+  uint8_t* wide = pv_lds + kPvSlots * kPvSlotBytes;
   if (!a.ctl->active) return;
   // Group-minor numbering keeps the feature blocks of one K/V group on one
   // XCD (workgroups are dealt to the XCDs round-robin): its L2 serves the
@@ -685,7 +700,7 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
   const int chunks0 = (end0 + kPvChunk - 1) / kPvChunk;
   const int chunks1 = end1 > begin1 ? (end1 - jb0_1 + kPvChunk - 1) / kPvChunk : 0;
   const int chunks = max(chunks0, chunks1);
-  const bool producer = wave == 1;
+  auto slot_of = [&](int c) { return ring + (c % kPvSlots) * kPvSlotBytes; };
 
   // Copy k (0..5) of a chunk fills block k of its slot.  k < 2: V rows
   // 4k .. 4k + 3 (row = range * 4 + feature); lane L fetches row 4k + L % 4,
@@ -695,7 +710,8 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
   // keys, inside the cache rows; the chains never use those values.  The
   // chunk index is clamped to the last chunk, so every step issues the same
   // number of copies and waits with the same count.
-  auto copy = [&](uint8_t* slot, int c) {
+  auto copy = [&](int c) {
+    uint8_t* slot = slot_of(c);
     c = min(c, chunks - 1);
 #pragma unroll
     for (int k = 0; k < kPvCopies; ++k) {
@@ -714,39 +730,57 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
       }
     }
   };
-
-  if (producer && chunks > 0) {
+  // Widens the V blocks of a landed chunk: lane L of block k holds row
+  // 4k + L % 4, keys 8 (L / 4) .. + 7, which go to that row of buffer c % 2
+  // at key offset 8 (L / 4).
+  auto widen = [&](int c) {
+    const uint8_t* slot = slot_of(c);
+    uint8_t* to = wide + (c & 1) * kPvWideBytes;
 #pragma unroll
-    for (int c = 0; c < kPvSlots - 1; ++c) copy(ring + c * kPvSlotBytes, c);
-    __builtin_amdgcn_s_waitcnt(pv_vmcnt(kPvInFlight));  // chunk 0 has landed
+    for (int k = 0; k < kPvVBlocks; ++k) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(slot + k * kPvBlock + 16 * lane);
+      const float4 lo = make_float4(dl_bf16_lo(w.x), dl_bf16_hi(w.x), dl_bf16_lo(w.y), dl_bf16_hi(w.y));
+      const float4 hi = make_float4(dl_bf16_lo(w.z), dl_bf16_hi(w.z), dl_bf16_lo(w.w), dl_bf16_hi(w.w));
+      float4* dst = reinterpret_cast<float4*>(to + (4 * k + lane % 4) * kPvWideRow + 32 * (lane / 4));
+      dst[0] = lo;
+      dst[1] = hi;
+    }
+    __builtin_amdgcn_s_waitcnt(kPvLdsDone);
+  };
+
+  // Before step -1 the copy wave has chunks 0 .. kPvSlots - 3 in flight and
+  // chunk 0 landed.
+  if (wave == 1) {
+    for (int c = 0; c <= kPvSlots - 3; ++c) copy(c);
+    __builtin_amdgcn_s_waitcnt(pv_vmcnt(kPvInFlight));
   }
 
   // Chain lane L (lanes 32-63 repeat lanes 0-31 and write nothing): range
-  // r = L / 16 % 2, head hl, feature f.  V row r * 4 + f lives in block r at
-  // 16-byte piece 4 q + f for key group q (8 keys); probability row
-  // r * 4 + hl in block 2 + (r * 4 + hl) / 2 at piece 2 q + hl % 2 for key
-  // group q (4 keys).
+  // r = L / 16 % 2, head hl, feature f.  Widened V row r * 4 + f holds key
+  // group q (8 keys) at byte 32 q; probability row r * 4 + hl lives in block
+  // 2 + (r * 4 + hl) / 2 at piece 2 q + hl % 2 for key group q (4 keys).
   const int r = (lane / 16) & 1, hl = (lane % 16) / kPvFeatures, f = lane % kPvFeatures;
   const int begin = r ? begin1 : 0, end = r ? end1 : end0, jb0 = r ? jb0_1 : 0;
   const int prow = r * 4 + hl;
-  const int voff = r * kPvBlock + f * 16;
+  const int voff = (r * kPvFeatures + f) * kPvWideRow;
   const int poff = (kPvVBlocks + prow / 2) * kPvBlock + (prow % 2) * 16;
   float acc = 0.0f;
-  // Step c: after the barrier the chains run chunk c from slot c % kPvSlots
-  // while the producer copies chunk c + kPvSlots - 1 into chunk c - 1's slot
-  // and waits until chunk c + 1 has landed.  `chunks` is uniform, so both
-  // waves meet every barrier.
-  int slot = 0;
-  for (int c = 0; c < chunks; ++c) {
-    __builtin_amdgcn_s_barrier();  // chunk c is in its slot; the chains are done with chunk c - 1
-    uint8_t* cur = ring + slot * kPvSlotBytes;
-    if (producer) {
-      const int ahead = slot == 0 ? kPvSlots - 1 : slot - 1;
-      copy(ring + ahead * kPvSlotBytes, c + kPvSlots - 1);
+  // Step c (from -1): after the barrier the chains run chunk c (its
+  // probabilities in its slot, its V in buffer c % 2), wave 2 widens chunk
+  // c + 1 (landed by the copy wave's wait of step c - 1), and the copy wave
+  // copies chunk c + kPvSlots - 1 into the slot of chunk c - 1 (done with in
+  // step c - 1) and waits until chunk c + 2 has landed.  The step count is
+  // uniform, so all waves meet every barrier.
+  for (int c = -1; c < chunks; ++c) {
+    __builtin_amdgcn_s_barrier();
+    if (wave == 1) {
+      copy(c + kPvSlots - 1);
       __builtin_amdgcn_s_waitcnt(pv_vmcnt(kPvInFlight));
-    } else {
-      const uint8_t* vb = cur + voff;
-      const uint8_t* pb = cur + poff;
+    } else if (wave == 2) {
+      widen(c + 1);
+    } else if (c >= 0) {
+      const uint8_t* vb = wide + (c & 1) * kPvWideBytes + voff;
+      const uint8_t* pb = slot_of(c) + poff;
       // Both ranges' chunk c full: the unmasked path (wave-uniform).
       const int cs0 = kPvChunk * c, cs1 = jb0_1 + kPvChunk * c;
       const bool full = cs0 + kPvChunk <= end0 && begin1 <= cs1 && cs1 + kPvChunk <= end1;
@@ -754,12 +788,12 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
         // The reads of group q + kAhead are issued before the FMAs of group
         // q (the order is pinned with scheduling barriers), so the LDS
         // latency hides behind the chain and the waits stay partial (at most
-        // 3 kAhead reads are outstanding; the wait counter has 4 bits).
+        // 4 kAhead reads are outstanding; the wait counter has 4 bits).
         constexpr int kGroups = kPvChunk / 8, kAhead = 3;
-        u32x4 w[kGroups];
-        float4 pa[kGroups], pc[kGroups];
+        float4 va[kGroups], vc[kGroups], pa[kGroups], pc[kGroups];
         auto read = [&](int q) {
-          w[q] = *reinterpret_cast<const u32x4*>(vb + 64 * q);
+          va[q] = *reinterpret_cast<const float4*>(vb + 32 * q);
+          vc[q] = *reinterpret_cast<const float4*>(vb + 32 * q + 16);
           pa[q] = *reinterpret_cast<const float4*>(pb + 32 * (2 * q));
           pc[q] = *reinterpret_cast<const float4*>(pb + 32 * (2 * q + 1));
         };
@@ -770,8 +804,7 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
           __builtin_amdgcn_sched_barrier(0);
           if (q + kAhead < kGroups) read(q + kAhead);
           __builtin_amdgcn_sched_barrier(0);
-          const float vv[8] = {dl_bf16_lo(w[q].x), dl_bf16_hi(w[q].x), dl_bf16_lo(w[q].y), dl_bf16_hi(w[q].y),
-                               dl_bf16_lo(w[q].z), dl_bf16_hi(w[q].z), dl_bf16_lo(w[q].w), dl_bf16_hi(w[q].w)};
+          const float vv[8] = {va[q].x, va[q].y, va[q].z, va[q].w, vc[q].x, vc[q].y, vc[q].z, vc[q].w};
           const float pp[8] = {pa[q].x, pa[q].y, pa[q].z, pa[q].w, pc[q].x, pc[q].y, pc[q].z, pc[q].w};
 #pragma unroll
           for (int e = 0; e < 8; ++e) acc = fma_rn(pp[e], vv[e], acc);
@@ -783,11 +816,11 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
         const int lo = max(begin - cs, 0), hi = min(end - cs, kPvChunk);
         const int q_end = (min(max(end0 - cs0, end1 - cs1), kPvChunk) + 7) / 8;
         for (int q = 0; q < q_end; ++q) {
-          const u32x4 w = *reinterpret_cast<const u32x4*>(vb + 64 * q);
+          const float4 va = *reinterpret_cast<const float4*>(vb + 32 * q);
+          const float4 vc = *reinterpret_cast<const float4*>(vb + 32 * q + 16);
           const float4 pa = *reinterpret_cast<const float4*>(pb + 32 * (2 * q));
           const float4 pc = *reinterpret_cast<const float4*>(pb + 32 * (2 * q + 1));
-          const float vv[8] = {dl_bf16_lo(w.x), dl_bf16_hi(w.x), dl_bf16_lo(w.y), dl_bf16_hi(w.y),
-                               dl_bf16_lo(w.z), dl_bf16_hi(w.z), dl_bf16_lo(w.w), dl_bf16_hi(w.w)};
+          const float vv[8] = {va.x, va.y, va.z, va.w, vc.x, vc.y, vc.z, vc.w};
           const float pp[8] = {pa.x, pa.y, pa.z, pa.w, pc.x, pc.y, pc.z, pc.w};
 #pragma unroll
           for (int e = 0; e < 8; ++e)
@@ -795,13 +828,12 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
         }
       }
     }
-    slot = slot == kPvSlots - 1 ? 0 : slot + 1;
   }
-  static_assert(kPvInFlight <= 63, "the wait counter holds at most 63 outstanding copies");
+  static_assert((kPvSlots - 2) * kPvCopies <= 63, "the wait counter holds at most 63 outstanding copies");
   static_assert(kPvVBlocks * 4 == 2 * kPvFeatures && (kPvCopies - kPvVBlocks) * 2 == 2 * 4,
                 "blocks of 4 V rows for two ranges of kPvFeatures, of 2 probability rows for two ranges of 4 heads");
-  if (producer) {
-    __builtin_amdgcn_s_waitcnt(pv_vmcnt(0));  // no copy outstanding at exit
+  if (wave != 0) {
+    if (wave == 1) __builtin_amdgcn_s_waitcnt(pv_vmcnt(0));  // no copy outstanding at exit
     return;
   }
   const float second = __shfl_down(acc, 16);
@@ -2754,6 +2786,7 @@ void prepare_kernels_all(dl_plan* p) {
   using namespace dl;
   const auto& c = p->model->cfg;
   const int D = c.hidden, QW = c.q_heads * c.head_dim, F = c.ffn;
+  allow_lds(k_attn_pv, kPvLds);
   allow_lds(k_qkv<1>, qkv_lds(1, D));
   allow_lds(k_qkv<2>, qkv_lds(2, D));
   allow_lds(k_qkv<4>, qkv_lds(4, D));
@@ -2869,7 +2902,7 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
     case 2: k_attn_softmax<<<dim3(c.q_heads, B), kSoftmaxThreads, size_t(p->cap) * sizeof(float), s>>>(aa); break;
     case 3:
       if (B == 1)
-        k_attn_pv<<<dim3(c.kv_heads * (kHeadDim / kPvFeatures), 1), kPvThreads, 0, s>>>(aa);
+        k_attn_pv<<<dim3(c.kv_heads * (kHeadDim / kPvFeatures), 1), kPvThreads, kPvLds, s>>>(aa);
       else
         k_attn_pv_rows<<<dim3(c.kv_heads * (kHeadDim / kPwFeatures), B), kPwThreads, 0, s>>>(aa);
       break;
