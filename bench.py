@@ -140,6 +140,23 @@ def other_configs(device, queue, model, cfg, seed, pplan, long_prompt):
         out["config3_attention"] = attn
         log(f"config 3: attention at {keys} keys: {attn}")
 
+    # The north star's 1K-context point: batch-1 greedy decode of 64 tokens
+    # after the exact prompt pass of a 1024-id prompt (visible keys 1025 to
+    # 1087 in the timed steps).
+    prompt1k = np.random.default_rng(seed + 10).integers(0, cfg.vocab, 1024).astype(np.uint32)
+    plan1k = Plan(model, batch=1, capacity=1024 + 64 + 2)
+    plan1k.prefill(prompt1k)
+    ms1k, _, _ = timed_loop(device, queue, plan1k, prompt1k, 64, 1)
+    del plan1k
+    ctx1k = 1024 + 1 + 62 / 2.0
+    out["decode_1k_context"] = {
+        "prompt": 1024, "new_tokens": 64, "timed_positions": [1024, 1086], "ms_per_step": round(ms1k, 4),
+        "tokens_per_s": round(1000.0 / ms1k, 2),
+        "hbm_frac": round(step_bytes(cfg, ctx1k) / (ms1k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "north_star_tokens_per_s": 330}
+    log(f"1K context: decode at 1025..1087 keys {ms1k * 1e3:.1f} us/token = {1000.0 / ms1k:.1f} tok/s "
+        f"({out['decode_1k_context']['hbm_frac']:.1%} of HBM peak)")
+
     # Config 4: batch 2, 256-id prompt, 256 tokens; plain, then capture of
     # block 24 at every position for both sequences plus an FP32 steering
     # vector (unit N(0,1) direction x 8.0) added at block 24 of sequence 1.

@@ -1038,7 +1038,11 @@ __global__ __launch_bounds__(kPwThreads) void k_attn_pv_rows(AttnArgs a) {
 // the group).  32 groups of 8 lanes score keys (ranges merged at 4,2,1),
 // scores stay in LDS, the max and the 32-partial denominator follow, and
 // the two PV key ranges run as 2 x 128 threads over the transposed V rows.
-constexpr int kFusedKeys = 1024;
+// Below kFusedKeys keys one launch (and its fused QKV / O forms) beats the
+// three-kernel split: measured per decode step on MI355X, the crossover lies
+// between 1536 and 1800 keys (1280 keys: 3345 against 3432 us; 1536: 3409
+// against 3458; 1800: 3554 against 3524).
+constexpr int kFusedKeys = 1536;
 constexpr int kAttnThreads = 512;
 constexpr int kAttnKeysPerPass = kAttnThreads / 8;
 constexpr int kAttnKeyPasses = 8;     // key rows issued at kernel entry: 512 keys

@@ -125,10 +125,11 @@ def test_config1_single_block_decode(device, queue, oracle):
     assert np.array_equal(plan.logits(0), oracle.logits(w, run.h))
 
 
-@pytest.mark.parametrize("position", [1, 63, 64, 77, 383, 511, 512, 513, 777, 1023, 1024, 1089, 1500, 1543, 4607])
+@pytest.mark.parametrize("position", [1, 63, 64, 77, 383, 511, 512, 513, 777, 1023, 1024, 1089, 1500, 1535, 1536,
+                                      1543, 4607])
 def test_single_block_both_attention_paths(device, queue, oracle, position):
-    """Positions below 1024 run the fused short-context attention kernel,
-    positions from 1024 the three-kernel split; both equal the oracle, up to
+    """Positions below 1536 run the fused short-context attention kernel,
+    positions from 1536 the three-kernel split; both equal the oracle, up to
     BASELINE config 3's last decode position (4607)."""
     from dolittle_amd.qwen3 import Plan, Qwen3Model
     model = Qwen3Model(device, queue, qwen_config(layers=1, vocab=2048))
@@ -152,11 +153,11 @@ def test_single_block_both_attention_paths(device, queue, oracle, position):
     assert np.array_equal(plan.hidden(0), run.h)
 
 
-@pytest.mark.parametrize("position", [1023, 1024, 4607])
+@pytest.mark.parametrize("position", [1535, 1536, 4607])
 def test_eager_launches_pick_the_attention_path_by_position(device, queue, oracle, monkeypatch, position):
     """DL_EAGER=1 launches the step kernels directly (no graphs are
     captured); the attention path still follows the position, so a step at
-    1024 keys or more runs the three-kernel split and equals the oracle."""
+    1536 keys or more runs the three-kernel split and equals the oracle."""
     from dolittle_amd.qwen3 import Plan, Qwen3Model
     monkeypatch.setenv("DL_EAGER", "1")
     model = Qwen3Model(device, queue, qwen_config(layers=1, vocab=2048))

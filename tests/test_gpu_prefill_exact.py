@@ -74,11 +74,11 @@ def test_exact_prefill_equals_token_loop(model2, length):
 
 
 def test_exact_prefill_across_the_fused_attention_limit(model1):
-    """A 1100-id prompt: chunks below 1024 keys use the one-kernel attention,
+    """A 1600-id prompt: chunks below 1536 keys use the one-kernel attention,
     the later ones the split long-context kernels."""
-    prompt = [int(t) for t in np.random.default_rng(77).integers(0, 2048, 1100)]
-    a, b = run_pair(model1, prompt, 4, capacity=1152)
-    assert_same(model1, a, b, 1104)
+    prompt = [int(t) for t in np.random.default_rng(77).integers(0, 2048, 1600)]
+    a, b = run_pair(model1, prompt, 4, capacity=1664)
+    assert_same(model1, a, b, 1604)
 
 
 def test_exact_prefill_batch_with_capture_and_steering(model2, device, queue):

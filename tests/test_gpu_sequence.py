@@ -196,7 +196,7 @@ def test_idle_steps_past_a_short_capacity(small_model):
     plan = Plan(small_model, batch=1, capacity=64)
     plan.generate(p, 8)
     tokens, results = plan.collect()
-    plan.decode_steps(1100)
+    plan.decode_steps(1600)
     again, results_again = plan.collect()
     assert again.tolist() == tokens.tolist() and results_again == results
 
