@@ -1431,23 +1431,29 @@ __device__ __forceinline__ void wave_lds_sync() {
 // several rows the merged sums (in lanes i * P) go through the wavefront's
 // LDS area `ep` (RW * B floats) so that lane i * B + b finishes (i, b) and
 // all the h updates of a tile are issued together.
+// Output `row` of step row `b` (launch-relative): h = round(h + round(y)),
+// then the optional steering and capture.
+__device__ __forceinline__ void residual_store(const ResidualArgs& a, int row, int b, float y, uint64_t pos,
+                                               bool steer, bool capture, uint32_t steer_mask) {
+  const int r = a.row0 + b;
+  const int seq = a.same_sequence ? a.sequence : r;
+  const uint64_t at = static_cast<uint64_t>(r) * a.D + row;
+  float value = rbf(dl_bf16_to_f32(a.h[at]) + rbf(y));
+  if (steer && ((steer_mask >> seq) & 1u)) value = rbf(value + a.steer[static_cast<uint64_t>(seq) * a.D + row]);
+  a.h[at] = bf16_bits(value);
+  if (capture) {
+    const uint64_t at_pos = a.same_sequence ? pos + r : pos;
+    a.capture[(static_cast<uint64_t>(seq) * a.cap + at_pos) * a.D + row] = bf16_bits(value);
+  }
+}
+
 template <int P, int B>
 __device__ __forceinline__ void residual_outputs(const ResidualArgs& a, const float (&acc)[B], int tile, int lane,
                                                  float* ep, uint64_t pos, bool steer, bool capture,
                                                  uint32_t steer_mask) {
   constexpr int RW = 64 / P;
   auto finish = [&](int i, int b, float y) {
-    const int row = tile * RW + i;
-    const int r = a.row0 + b;
-    const int seq = a.same_sequence ? a.sequence : r;
-    const uint64_t at = static_cast<uint64_t>(r) * a.D + row;
-    float value = rbf(dl_bf16_to_f32(a.h[at]) + rbf(y));
-    if (steer && ((steer_mask >> seq) & 1u)) value = rbf(value + a.steer[static_cast<uint64_t>(seq) * a.D + row]);
-    a.h[at] = bf16_bits(value);
-    if (capture) {
-      const uint64_t at_pos = a.same_sequence ? pos + r : pos;
-      a.capture[(static_cast<uint64_t>(seq) * a.cap + at_pos) * a.D + row] = bf16_bits(value);
-    }
+    residual_store(a, tile * RW + i, b, y, pos, steer, capture, steer_mask);
   };
   if constexpr (B == 1) {
     if (lane % P == 0) finish(lane / P, 0, acc[0]);
@@ -1856,6 +1862,222 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_gateup(GateUpArgs a) {
             bf16_bits(silu_times(rbf(ep[o * B + b]), rbf(ep[(2 + o) * B + b])));
       }
       wave_lds_sync();
+    }
+  }
+}
+
+// ---------------------------------------------- exact GEMM over many rows
+// The projections of the chunked prompt pass when a chunk holds many rows
+// (positions of one sequence).  Every output is the same P-partial FMA chain
+// and upper-into-lower merge as in the GEMV kernels (projection.cu:139-482):
+// partial t of output f is the FMA chain over inputs t, t + P, ... in
+// ascending order.  Only the assignment of chains to lanes differs: lane
+// (g, t) of a wavefront owns partial t of kXgFeat consecutive outputs for
+// kXgPos rows, so each staged input feeds kXgFeat FMAs and each widened
+// weight kXgPos, and the weights are read once per kXgRows rows instead of
+// once per step row.
+//
+// Workgroup: 8 wavefronts = kXgWN output blocks x kXgWP row blocks, tile
+// kXgWN * (64 / P) * kXgFeat outputs x kXgRows rows.  The rows' inputs pass
+// through LDS kXgChunk inputs at a time as FP32 in the GEMV's staged layout
+// (partial-major rows padded by kXsPad floats, so the P lanes of a read hit
+// distinct banks); the next pass's inputs are loaded into registers while
+// the current one is multiplied.  The weights come straight from memory in
+// the packed layout, one 8-element step ahead.  Workgroups that share
+// weights (same blockIdx.x) land on one XCD when gridDim.x is a multiple of
+// 8, so its L2 serves the weights to the row blocks.
+constexpr int kXgThreads = 512;
+constexpr int kXgWN = 2, kXgWP = 4;
+constexpr int kXgFeat = 4;                  // outputs per lane (one P = 16 tile, two P = 32 tiles)
+constexpr int kXgPos = 8;                   // rows per lane
+constexpr int kXgRows = kXgWP * kXgPos;     // rows per workgroup
+constexpr int kXgChunk = 1024;              // inputs staged per pass
+constexpr int kXgMinRows = 16;              // fewer rows run through the batched GEMVs
+
+enum XgEpilogue : int {
+  kXgQ = 0,         // out[b][f] = BF16(acc): Q rows
+  kXgKV = 1,        // K rows (f < kw) to out[b][f], V rows to the transposed cache column of row b
+  kXgResidual = 2,  // residual_store (O and down)
+  kXgGateUp = 3,    // interleaved [g 2j, g 2j+1, u 2j, u 2j+1] -> SiLU(g) * u, P32-permuted act rows
+};
+
+struct XgemmArgs {
+  const Control* ctl;
+  const uint16_t* x;     // [B][K] BF16 input rows: P-permuted (`permuted`) or natural order
+  const u32x4* w;        // packed rows with P partials
+  int B, N, K, permuted;
+  uint16_t* out;         // kXgQ [B][N]; kXgKV k rows [B][kw]; kXgGateUp act [B][N / 2]
+  uint16_t* v_cache;     // kXgKV: V^T of this layer; row b's column is position + b * v_stride
+  uint64_t v_stride;
+  int kw, cap;
+  ResidualArgs res;      // kXgResidual
+};
+
+__host__ __device__ constexpr size_t xgemm_lds(int P) {
+  return size_t(kXgRows) * P * (kXgChunk / P + kXsPad) * sizeof(float);
+}
+
+template <int P, int EPI>
+__global__ __launch_bounds__(kXgThreads) void k_xgemm(XgemmArgs a) {
+  constexpr int G = 64 / P;                    // lane groups of a wavefront
+  constexpr int RW = 64 / P;                   // outputs per packed tile
+  constexpr int WF = G * kXgFeat;              // outputs per wavefront
+  constexpr int TF = kXgWN * WF;               // outputs per workgroup
+  constexpr int stride = kXgChunk / P + kXsPad;
+  constexpr int row_floats = P * stride;       // staged floats per row
+  constexpr int steps = kXgChunk / (8 * P);    // 8-element chain steps per pass
+  constexpr int kPieces = kXgRows * kXgChunk / 8 / kXgThreads;  // 16-byte input pieces per thread per pass
+  static_assert(kXgFeat % RW == 0 || RW % kXgFeat == 0, "whole tiles per lane");
+  static_assert(kXgWN * kXgWP * 64 == kXgThreads, "one wavefront per (output block, row block)");
+  extern __shared__ float xs[];                // [kXgRows][P][stride]
+  if (!a.ctl->active) return;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int g = lane / P, t = lane % P;
+  const int f0 = blockIdx.x * TF + (wave % kXgWN) * WF + g * kXgFeat;  // first output of this lane
+  const int b0 = blockIdx.y * kXgRows;                                 // first row of the workgroup
+  const int pb = (wave / kXgWN) * kXgPos;                              // first row of this lane in the tile
+  const int S = a.K / (8 * P), passes = a.K / kXgChunk;
+  const uint64_t pos = a.ctl->position;
+
+  // Packed chunk of output f, step s, partial t: ((f / RW) S + s) 64 + (f % RW) P + t.
+  const u32x4* wsrc[kXgFeat];
+#pragma unroll
+  for (int j = 0; j < kXgFeat; ++j) {
+    const int f = f0 + j;
+    wsrc[j] = a.w + static_cast<uint64_t>(f / RW) * S * 64 + (f % RW) * P + t;
+  }
+  // Weights of a step: kXgFeat 16-byte chunks; two register sets alternate
+  // (a pass has an even number of steps), each loaded one step ahead.
+  u32x4 wa[kXgFeat], wb[kXgFeat];
+  auto load_w = [&](u32x4* w, int sg) {
+    const uint64_t at = static_cast<uint64_t>(sg < S ? sg : S - 1) * 64;  // past the end: reload the last step
+#pragma unroll
+    for (int j = 0; j < kXgFeat; ++j) w[j] = wsrc[j][at];
+  };
+  load_w(wa, 0);
+
+  // Piece q of row r of a pass: inputs 8q .. 8q + 7 of the pass (rows past
+  // B repeat row B - 1 and are never stored).
+  u32x4 xr[kPieces];
+  auto load_x = [&](int c) {
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) {
+      const int piece = threadIdx.x + j * kXgThreads, r = piece / (kXgChunk / 8), q = piece % (kXgChunk / 8);
+      const int b = min(b0 + r, a.B - 1);
+      xr[j] = *reinterpret_cast<const u32x4*>(a.x + static_cast<uint64_t>(b) * a.K + c * kXgChunk + 8 * q);
+    }
+  };
+  auto store_x = [&] {
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) {
+      const int piece = threadIdx.x + j * kXgThreads, r = piece / (kXgChunk / 8), q = piece % (kXgChunk / 8);
+      const float v[8] = {dl_bf16_lo(xr[j].x), dl_bf16_hi(xr[j].x), dl_bf16_lo(xr[j].y), dl_bf16_hi(xr[j].y),
+                          dl_bf16_lo(xr[j].z), dl_bf16_hi(xr[j].z), dl_bf16_lo(xr[j].w), dl_bf16_hi(xr[j].w)};
+      float* row = xs + r * row_floats;
+      if (a.permuted) {
+        // P-permuted: piece q holds chain elements 8 (q / P) .. + 7 of
+        // partial q % P (the pass starts on a block of 8 P inputs).
+        float4* dst = reinterpret_cast<float4*>(row + (q % P) * stride + 8 * (q / P));
+        dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+        dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = 8 * q + e;
+          row[(i % P) * stride + i / P] = v[e];
+        }
+      }
+    }
+  };
+
+  float acc[kXgFeat * kXgPos];
+#pragma unroll
+  for (int i = 0; i < kXgFeat * kXgPos; ++i) acc[i] = 0.0f;
+  // One chain step (8 elements) of every (output, row) pair of the lane.
+  auto step = [&](const u32x4* w, int s) {
+    float wf[kXgFeat][8];
+#pragma unroll
+    for (int j = 0; j < kXgFeat; ++j) {
+      wf[j][0] = dl_bf16_lo(w[j].x); wf[j][1] = dl_bf16_hi(w[j].x);
+      wf[j][2] = dl_bf16_lo(w[j].y); wf[j][3] = dl_bf16_hi(w[j].y);
+      wf[j][4] = dl_bf16_lo(w[j].z); wf[j][5] = dl_bf16_hi(w[j].z);
+      wf[j][6] = dl_bf16_lo(w[j].w); wf[j][7] = dl_bf16_hi(w[j].w);
+    }
+#pragma unroll
+    for (int i = 0; i < kXgPos; ++i) {
+      const float* xp = xs + (pb + i) * row_floats + t * stride + 8 * s;
+      const float4 xa = *reinterpret_cast<const float4*>(xp);
+      const float4 xb = *reinterpret_cast<const float4*>(xp + 4);
+#pragma unroll
+      for (int j = 0; j < kXgFeat; ++j) {
+        float v = acc[j * kXgPos + i];
+        v = fma_rn(xa.x, wf[j][0], v);
+        v = fma_rn(xa.y, wf[j][1], v);
+        v = fma_rn(xa.z, wf[j][2], v);
+        v = fma_rn(xa.w, wf[j][3], v);
+        v = fma_rn(xb.x, wf[j][4], v);
+        v = fma_rn(xb.y, wf[j][5], v);
+        v = fma_rn(xb.z, wf[j][6], v);
+        v = fma_rn(xb.w, wf[j][7], v);
+        acc[j * kXgPos + i] = v;
+      }
+    }
+  };
+  static_assert(steps % 2 == 0, "the weight register sets alternate within a pass");
+  load_x(0);
+  for (int c = 0; c < passes; ++c) {
+    __syncthreads();  // every wavefront is done with the previous pass
+    store_x();
+    if (c + 1 < passes) load_x(c + 1);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < steps; s += 2) {
+      const int sg = c * steps + s;
+      load_w(wb, sg + 1);
+      step(wa, s);
+      load_w(wa, sg + 2);
+      step(wb, s + 1);
+    }
+  }
+  chain_merge<P, kXgFeat * kXgPos>(acc);
+  if (t != 0) return;
+
+  bool steer = false, capture = false;
+  uint32_t steer_mask = 0;
+  if constexpr (EPI == kXgResidual) {
+    steer = a.res.steer != nullptr && a.res.layer == a.ctl->steer_layer;
+    capture = a.res.capture != nullptr && a.res.layer == a.ctl->capture_layer;
+    steer_mask = a.ctl->steer_mask;
+  }
+#pragma unroll
+  for (int i = 0; i < kXgPos; ++i) {
+    const int b = b0 + pb + i;
+    if (b >= a.B) break;
+    if constexpr (EPI == kXgGateUp) {
+      // One P = 16 tile: [g 2j, g 2j+1, u 2j, u 2j+1], j = f0 / 4.
+#pragma unroll
+      for (int o = 0; o < 2; ++o) {
+        const uint32_t n = static_cast<uint32_t>(f0 / 2 + o);
+        a.out[static_cast<uint64_t>(b) * (a.N / 2) + prefill::permuted(n, 32)] =
+            bf16_bits(silu_times(rbf(acc[o * kXgPos + i]), rbf(acc[(2 + o) * kXgPos + i])));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kXgFeat; ++j) {
+        const int f = f0 + j;
+        const float y = acc[j * kXgPos + i];
+        if constexpr (EPI == kXgQ) {
+          a.out[static_cast<uint64_t>(b) * a.N + f] = bf16_bits(y);
+        } else if constexpr (EPI == kXgKV) {
+          if (f < a.kw)
+            a.out[static_cast<uint64_t>(b) * a.kw + f] = bf16_bits(y);
+          else
+            a.v_cache[static_cast<uint64_t>(b) * a.v_stride + static_cast<uint64_t>(f - a.kw) * a.cap + pos] =
+                bf16_bits(y);
+        } else {
+          residual_store(a.res, f, b, y, pos, steer, capture, steer_mask);
+        }
+      }
     }
   }
 }
@@ -2706,10 +2928,11 @@ struct dl_plan {
              *att = nullptr, *act = nullptr;
     uint32_t rows = 0;  // allocated rows (multiple of 128)
   } pf;
-  // Exact chunked prompt pass: row buffers for kMaxBatch consecutive
+  // Exact chunked prompt pass: row buffers for kExactChunk consecutive
   // positions of one sequence and the chunk's control (first use).
   struct Chunk {
-    uint16_t *h = nullptr, *q = nullptr, *k = nullptr, *att = nullptr, *act = nullptr;
+    uint16_t *h = nullptr, *q = nullptr, *k = nullptr, *att = nullptr, *act = nullptr, *x16 = nullptr,
+             *x32 = nullptr;
     float *scores = nullptr, *probs = nullptr;
     dl::Control* ctl = nullptr;
   } ex;
@@ -2791,6 +3014,11 @@ void prepare_kernels_all(dl_plan* p) {
   const auto& c = p->model->cfg;
   const int D = c.hidden, QW = c.q_heads * c.head_dim, F = c.ffn;
   allow_lds(k_attn_pv, kPvLds);
+  allow_lds(k_xgemm<16, kXgQ>, xgemm_lds(16));
+  allow_lds(k_xgemm<32, kXgKV>, xgemm_lds(32));
+  allow_lds(k_xgemm<16, kXgResidual>, xgemm_lds(16));
+  allow_lds(k_xgemm<32, kXgResidual>, xgemm_lds(32));
+  allow_lds(k_xgemm<16, kXgGateUp>, xgemm_lds(16));
   allow_lds(k_qkv<1>, qkv_lds(1, D));
   allow_lds(k_qkv<2>, qkv_lds(2, D));
   allow_lds(k_qkv<4>, qkv_lds(4, D));
@@ -2850,6 +3078,14 @@ template <int G>
 void launch_head(dl_plan* p, hipStream_t s, const dl::HeadArgs& a) {
   dl::k_lm_head<G><<<p->head_blocks, dl::gemv_waves(G) * 64, p16_lds(G, a.D), s>>>(a);
 }
+// The many-row exact GEMM: grid (output blocks, row blocks).
+template <int P, int EPI>
+void launch_xgemm(hipStream_t s, const dl::XgemmArgs& a) {
+  constexpr int tile_outputs = dl::kXgWN * (64 / P) * dl::kXgFeat;
+  require(a.N % tile_outputs == 0 && a.K % dl::kXgChunk == 0 && a.B > 0, "exact GEMM shape");
+  const dim3 grid(a.N / tile_outputs, (a.B + dl::kXgRows - 1) / dl::kXgRows);
+  dl::k_xgemm<P, EPI><<<grid, dl::kXgThreads, dl::xgemm_lds(P), s>>>(a);
+}
 
 // The rows one step works on.  For the token loop they are the plan's
 // sequences at one position; for the exact chunked prompt pass they are up
@@ -2863,11 +3099,25 @@ struct StepRows {
   uint64_t attn_seq_stride;  // attention: cache offset from row r to row r + 1
   int pos_step;              // row r is at ctl->position + r * pos_step
   int same_sequence, sequence;
+  // Normalized rows in P16 / P32 order for the many-row exact GEMM (null
+  // where the step never has kXgMinRows rows).
+  uint16_t *x16, *x32;
 };
 
 StepRows plan_rows(const dl_plan* p) {
   return StepRows{p->h, p->q_raw, p->k_raw, p->att, p->act, p->scores, p->probs, p->batch, 0,
                   p->cache_seq_stride, p->cache_seq_stride, 0, 0, 0};
+}
+
+// Whether step rows `r` run their projections through the many-row exact
+// GEMM (its shapes: widths that are whole passes of staged inputs).
+bool use_xgemm(const dl_plan* p, const StepRows& r) {
+  const auto& c = p->model->cfg;
+  const dl_qwen3* m = p->model;
+  return r.rows >= static_cast<uint32_t>(dl::kXgMinRows) && r.x16 != nullptr && r.x32 != nullptr &&
+         m->p_q == 16 && m->p_kv == 32 && m->p_o == 16 && m->p_gu == 16 && m->p_down == 32 &&
+         c.hidden % dl::kXgChunk == 0 && (uint64_t(c.q_heads) * c.head_dim) % dl::kXgChunk == 0 &&
+         c.ffn % dl::kXgChunk == 0;
 }
 
 // Launches one decode-step kernel `which` of layer `l` with control `ctl`
@@ -2884,8 +3134,21 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
   AttnArgs aa{ctl, r.q_raw, r.k_raw, m->q_norm[l], m->k_norm[l], p->rope, kc, vc, r.attn_seq_stride,
               r.scores, r.probs, r.att, static_cast<int>(c.q_heads), static_cast<int>(c.kv_heads),
               static_cast<int>(p->cap), c.rms_eps, scale, r.pos_step};
+  const bool xg = use_xgemm(p, r);
   switch (which) {
     case 0:
+      if (xg) {
+        prefill::launch_norm(s, prefill::NormArgs{r.h, m->input_norm[l], r.x16, r.x32, static_cast<int>(B), D,
+                                                  c.rms_eps});
+        XgemmArgs qa{ctl, r.x16, reinterpret_cast<const u32x4*>(m->qkv[l]), static_cast<int>(B), QW, D, 1,
+                     r.q_raw, nullptr, 0, KW, static_cast<int>(p->cap), {}};
+        launch_xgemm<16, kXgQ>(s, qa);
+        XgemmArgs kva{ctl, r.x32, reinterpret_cast<const u32x4*>(m->qkv[l] + uint64_t(QW) * D),
+                      static_cast<int>(B), 2 * KW, D, 1, r.k_raw, vc, r.v_append_stride, KW,
+                      static_cast<int>(p->cap), {}};
+        launch_xgemm<32, kXgKV>(s, kva);
+        break;
+      }
       for_row_groups(B, kQkvRows, [&](uint32_t r0, int g) {
         QkvArgs qa{ctl, r.h + uint64_t(r0) * D, m->input_norm[l], reinterpret_cast<const u32x4*>(m->qkv[l]),
                    r.q_raw + uint64_t(r0) * QW, r.k_raw + uint64_t(r0) * KW, vc + r0 * r.v_append_stride,
@@ -2943,6 +3206,13 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
     }
     case 9: k_append_keys<<<dim3(c.kv_heads, B), 64, 0, s>>>(aa); break;
     case 4:
+      if (xg) {
+        ResidualArgs oa{ctl, r.att, reinterpret_cast<const u32x4*>(m->o[l]), r.h, nullptr, nullptr, QW, D,
+                        static_cast<int>(p->cap), static_cast<int>(l), 0, r.same_sequence, r.sequence};
+        launch_xgemm<16, kXgResidual>(
+            s, XgemmArgs{ctl, r.att, oa.w, static_cast<int>(B), D, QW, 0, nullptr, nullptr, 0, 0, 0, oa});
+        break;
+      }
       for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
         ResidualArgs oa{ctl, r.att, reinterpret_cast<const u32x4*>(m->o[l]), r.h, nullptr, nullptr, QW, D,
                         static_cast<int>(p->cap), static_cast<int>(l), static_cast<int>(r0), r.same_sequence,
@@ -2954,6 +3224,14 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       });
       break;
     case 5:
+      if (xg) {
+        prefill::launch_norm(s, prefill::NormArgs{r.h, m->post_norm[l], r.x16, nullptr, static_cast<int>(B), D,
+                                                  c.rms_eps});
+        // SiLU(g) * u rows go to act in P32 order, the order the down GEMM stages.
+        launch_xgemm<16, kXgGateUp>(s, XgemmArgs{ctl, r.x16, reinterpret_cast<const u32x4*>(m->gu[l]),
+                                                 static_cast<int>(B), 2 * F, D, 1, r.act, nullptr, 0, 0, 0, {}});
+        break;
+      }
       for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
         GateUpArgs ga{ctl, r.h + uint64_t(r0) * D, m->post_norm[l], reinterpret_cast<const u32x4*>(m->gu[l]),
                       r.act + uint64_t(r0) * F, D, F, c.rms_eps};
@@ -2964,6 +3242,13 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       });
       break;
     case 6:
+      if (xg) {
+        ResidualArgs da{ctl, r.act, reinterpret_cast<const u32x4*>(m->down[l]), r.h, p->capture, p->steer, F, D,
+                        static_cast<int>(p->cap), static_cast<int>(l), 0, r.same_sequence, r.sequence};
+        launch_xgemm<32, kXgResidual>(
+            s, XgemmArgs{ctl, r.act, da.w, static_cast<int>(B), D, F, 1, nullptr, nullptr, 0, 0, 0, da});
+        break;
+      }
       // Staging in blocks needs whole blocks of inputs; other widths keep
       // two-row launches.
       for_row_groups(B, F % kChunkInputs == 0 ? kDownRows : 2, [&](uint32_t r0, int g) {
@@ -4020,6 +4305,11 @@ int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_lengt
 // a single-position step, the chunk's keys are in the cache before its
 // attention, and each row attends to keys [0, its position], so the caches
 // are bit-identical to consuming the prompt one position per step.
+// Consecutive prompt positions per step of the exact chunked prompt pass:
+// their projections run as many-row exact GEMMs (each weight read once per
+// chunk), their attention row by row.
+constexpr uint32_t kExactChunk = 128;
+
 int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length) {
   return guard([&] {
     require(plan && prompt, "null argument");
@@ -4039,7 +4329,7 @@ int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt
     const uint32_t rows = prompt_length - 1;
     if (rows == 0) return;
     const uint64_t D = c.hidden, QW = uint64_t(c.q_heads) * c.head_dim, KW = uint64_t(c.kv_heads) * c.head_dim,
-                   F = c.ffn, R = dl::kMaxBatch;
+                   F = c.ffn, R = kExactChunk;
     auto& ex = plan->ex;
     if (!ex.ctl) {
       ex.h = plan->alloc<uint16_t>(R * D);
@@ -4047,6 +4337,8 @@ int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt
       ex.k = plan->alloc<uint16_t>(R * KW);
       ex.att = plan->alloc<uint16_t>(R * QW);
       ex.act = plan->alloc<uint16_t>(R * F);
+      ex.x16 = plan->alloc<uint16_t>(R * D);
+      ex.x32 = plan->alloc<uint16_t>(R * D);
       ex.scores = plan->alloc<float>(R * c.q_heads * plan->cap);
       ex.probs = plan->alloc<float>(R * c.q_heads * plan->cap);
       ex.ctl = plan->alloc<dl::Control>(1);
@@ -4065,7 +4357,7 @@ int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt
                                 plan->override_position};
         dl::k_prefill_embed<<<n, dl::kBlock, 0, s>>>(ea);
         const StepRows r{ex.h, ex.q, ex.k, ex.att, ex.act, ex.scores, ex.probs, n,
-                         uint64_t(seq) * plan->cache_seq_stride, 1, 0, 1, 1, static_cast<int>(seq)};
+                         uint64_t(seq) * plan->cache_seq_stride, 1, 0, 1, 1, static_cast<int>(seq), ex.x16, ex.x32};
         const bool short_context = p0 + n <= static_cast<uint32_t>(dl::kFusedKeys);
         for (uint32_t l = 0; l < c.layers; ++l) {
           launch_step_kernel(plan, s, 0, l, ex.ctl, r);  // Q, K, V (V into the cache)
