@@ -1887,9 +1887,9 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_gateup(GateUpArgs a) {
 // weights (same blockIdx.x) land on one XCD when gridDim.x is a multiple of
 // 8, so its L2 serves the weights to the row blocks.
 constexpr int kXgThreads = 512;
-constexpr int kXgWN = 2, kXgWP = 4;
+constexpr int kXgWN = 4, kXgWP = 2;
 constexpr int kXgFeat = 4;                  // outputs per lane (one P = 16 tile, two P = 32 tiles)
-constexpr int kXgPos = 8;                   // rows per lane
+constexpr int kXgPos = 16;                  // rows per lane
 constexpr int kXgRows = kXgWP * kXgPos;     // rows per workgroup
 constexpr int kXgChunk = 1024;              // inputs staged per pass
 constexpr int kXgMinRows = 16;              // fewer rows run through the batched GEMVs
