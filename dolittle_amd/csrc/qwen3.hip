@@ -569,6 +569,86 @@ __global__ __launch_bounds__(kBlock) void k_attn_qk(AttnArgs a) {
   }
 }
 
+// k_attn_qk for the rows of the chunked prompt pass (consecutive positions
+// of one sequence, pos_step 1, every row's rotated key already in the cache
+// by k_append_keys): grid (kv head, 64-key tile, block of kQkRows rows).
+// The tile's key rows are loaded and widened once for all the block's rows,
+// and the group's query heads of those rows are normalized and rotated up
+// front (wave w takes head w of every row).  Each score is k_attn_qk's:
+// 8 lanes per key, an FMA chain over 16 contiguous features each, merged at
+// offsets 4, 2, 1, times the scale (attention.cu:231-300).
+constexpr int kQkRows = 8;
+
+__global__ __launch_bounds__(kBlock) void k_attn_qk_rows(AttnArgs a, int rows) {
+  __shared__ float qs[kQkRows][4][kHeadDim];
+  const int g = blockIdx.x, key0 = blockIdx.y * 64, rb = blockIdx.z * kQkRows;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int kl = lane / 8, l = lane % 8;
+  const int group = a.q_heads / a.kv_heads;
+  const int n = min(kQkRows, rows - rb);
+  const uint64_t qw = static_cast<uint64_t>(a.q_heads) * kHeadDim;
+  const uint16_t* kc = a.k_cache + static_cast<uint64_t>(g) * a.cap * kHeadDim;
+  // Rows key0 .. key0 + 63 lie inside the cache (its capacity is a multiple
+  // of 64); rows past a query's position are loaded but never used.
+  u32x4 kpre[2][2];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const u32x4* src =
+        reinterpret_cast<const u32x4*>(kc + static_cast<uint64_t>(key0 + wave * 16 + it * 8 + kl) * kHeadDim + 16 * l);
+    kpre[it][0] = src[0];
+    kpre[it][1] = src[1];
+  }
+  if (!a.ctl->active) return;
+  const uint64_t pos0 = a.ctl->position + static_cast<uint64_t>(rb);
+  if (static_cast<uint64_t>(key0) > pos0 + n - 1) return;  // past every row's last key
+  for (int rr = 0; rr < n; ++rr) {
+    const uint64_t pos = pos0 + rr;
+    const uint16_t* x = a.q_raw + (rb + rr) * qw + static_cast<uint64_t>(g * group + wave) * kHeadDim;
+    head_norm_rope(x, a.q_norm, a.rope + pos * kHeadDim, lane, a.eps, qs[rr][wave]);
+  }
+  float kf[2][16];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const u32x4 w0 = kpre[it][0], w1 = kpre[it][1];
+    kf[it][0] = dl_bf16_lo(w0.x); kf[it][1] = dl_bf16_hi(w0.x); kf[it][2] = dl_bf16_lo(w0.y); kf[it][3] = dl_bf16_hi(w0.y);
+    kf[it][4] = dl_bf16_lo(w0.z); kf[it][5] = dl_bf16_hi(w0.z); kf[it][6] = dl_bf16_lo(w0.w); kf[it][7] = dl_bf16_hi(w0.w);
+    kf[it][8] = dl_bf16_lo(w1.x); kf[it][9] = dl_bf16_hi(w1.x); kf[it][10] = dl_bf16_lo(w1.y); kf[it][11] = dl_bf16_hi(w1.y);
+    kf[it][12] = dl_bf16_lo(w1.z); kf[it][13] = dl_bf16_hi(w1.z); kf[it][14] = dl_bf16_lo(w1.w); kf[it][15] = dl_bf16_hi(w1.w);
+  }
+  __syncthreads();
+  for (int rr = 0; rr < n; ++rr) {
+    const int count = static_cast<int>(pos0 + rr) + 1;
+    const int b = rb + rr;
+    float q[4][16];
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) q[h][i] = qs[rr][h][16 * l + i];
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int j = key0 + wave * 16 + it * 8 + kl;
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (j < count) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[h] = fma_rn(q[h][i], kf[it][i], acc[h]);
+      }
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        acc[h] = acc[h] + row_down<4>(acc[h]);
+        acc[h] = acc[h] + row_down<2>(acc[h]);
+        acc[h] = acc[h] + row_down<1>(acc[h]);
+      }
+      if (l == 0 && j < count) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          a.scores[(static_cast<uint64_t>(b) * a.q_heads + g * group + h) * a.cap + j] = acc[h] * a.scale;
+      }
+    }
+  }
+}
+
 // Grid (query head, sequence), 1024 threads.  m = max, e = exp(s - m),
 // denominator from 32 partials owning j mod 32 merged at offsets 16..1,
 // p = e / l (attention.cu:301-330).  Every thread issues all of its score
@@ -1029,6 +1109,203 @@ __global__ __launch_bounds__(kPwThreads) void k_attn_pv_rows(AttnArgs a) {
   if (wave == 0)
     a.att[static_cast<uint64_t>(b) * a.q_heads * kHeadDim + (g * group + hl) * kHeadDim + fb * kPwFeatures + f] =
         bf16_bits(acc + second[lane]);
+}
+
+// k_attn_pv_rows for the rows of the chunked prompt pass (consecutive
+// positions of one sequence, pos_step 1): a workgroup runs kPbRows rows, so
+// each V row it stages and widens feeds kPbRows chains.  Grid (kv head * 8
+// feature blocks, row blocks), 256 threads.  Waves 0 and 2 run the two PV
+// key ranges: for row r with n_r keys, range 0 is [0, ceil(n_r / 2)) and
+// range 1 the rest; lane = (head, feature) holds one accumulator per row of
+// each range, so every output feature is round(A + B) of the same two
+// ascending FMA chains as in k_attn_pv_rows (attention.cu:331-375).  A
+// wave stages the union of its rows' ranges; a key group inside every row's
+// range runs unmasked, the groups at the range ends run masked per row.
+// Waves 1 and 3 copy each chunk's 32 V rows and the 4 heads' probability
+// rows of every row of the block into a kPbSlots-slot LDS ring
+// (global_load_lds), kPbSlots - 1 chunks ahead, as k_attn_pv_rows does.
+constexpr int kPbRows = 4;
+constexpr int kPbSlots = 3;
+constexpr int kPbVBlocks = 8;                      // 2 ranges x 16 features, 4 rows per block
+constexpr int kPbPBlocks = 2 * kPbRows * 4 / 2;    // 2 ranges x kPbRows rows x 4 heads, 2 rows per block
+constexpr int kPbCopies = (kPbVBlocks + kPbPBlocks) / 2;  // per copy wave and chunk
+constexpr int kPbSlotBytes = (kPbVBlocks + kPbPBlocks) * kPwBlock;
+constexpr size_t kPbLds = size_t(kPbSlots) * kPbSlotBytes;
+
+__global__ __launch_bounds__(kPwThreads) void k_attn_pv_block(AttnArgs a, int rows) {
+  extern __shared__ __align__(16) uint8_t pb_lds[];
+  __shared__ float second[kPbRows][64];
+  static_assert((kPbSlots - 1) * kPbCopies <= 63, "the wait counter holds at most 63 outstanding copies");
+  if (!a.ctl->active) return;
+  const int g = blockIdx.x % a.kv_heads, fb = blockIdx.x / a.kv_heads, rb = blockIdx.y * kPbRows;
+  const int n = min(kPbRows, rows - rb);
+  const int pos0 = static_cast<int>(a.ctl->position) + rb;
+  // Row rr attends to keys [0, pos0 + rr]; its ranges split at
+  // ceil(count / 2).  The union of range 0 is [0, split of the last row),
+  // of range 1 [split of the first row, count of the last row).
+  auto count_of = [&](int rr) { return pos0 + rr + 1; };
+  auto split_of = [&](int rr) { return (count_of(rr) - 1) / 2 + 1; };
+  const int end0 = split_of(n - 1), begin1 = split_of(0), end1 = count_of(n - 1);
+  const int jb0_1 = begin1 & ~7;
+  const int chunks0 = (end0 + kPwChunk - 1) / kPwChunk;
+  const int chunks1 = end1 > begin1 ? (end1 - jb0_1 + kPwChunk - 1) / kPwChunk : 0;
+  const int chunks = max(chunks0, chunks1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+  const int group = a.q_heads / a.kv_heads;
+  const uint16_t* vbase = a.v_cache + static_cast<uint64_t>(g * kHeadDim + fb * kPwFeatures) * a.cap;
+  const float* pbase = a.probs + (static_cast<uint64_t>(rb) * a.q_heads + g * group) * a.cap;
+  const bool producer = (wave & 1) != 0;
+  auto slot_of = [&](int c) { return pb_lds + (c % kPbSlots) * kPbSlotBytes; };
+
+  // Copy k of a chunk fills block k of its slot.  k < 8: V rows 4k .. 4k + 3
+  // (row = range * 16 + feature); lane L fetches row 4k + L % 4, keys
+  // 8 (L / 4) .. + 7.  k >= 8: probability rows 2 (k - 8) + {0, 1} (row =
+  // (range * kPbRows + rr) * 4 + head); lane L fetches row 2 (k - 8) + L % 2,
+  // keys 4 (L / 2) .. + 3.  Sources past a range are clamped to its last 8
+  // (4) keys, rows past the block's last row repeat it; the chains never use
+  // those values.  Producer wave w takes the copies k = w / 2 + 2 m.
+  auto copy = [&](int c) {
+    uint8_t* slot = slot_of(c);
+    c = min(c, chunks - 1);
+#pragma unroll
+    for (int m = 0; m < kPbCopies; ++m) {
+      const int k = wave / 2 + 2 * m;
+      if (k < kPbVBlocks) {
+        const int row = 4 * k + lane % 4, r = row / kPwFeatures, f = row % kPwFeatures;
+        const int jb0 = r ? jb0_1 : 0, last8 = ((r ? end1 : end0) - 1) & ~7;
+        const int key = max(0, min(jb0 + kPwChunk * c + 8 * (lane / 4), last8));
+        __builtin_amdgcn_global_load_lds((const pv_global_void*)(vbase + static_cast<uint64_t>(f) * a.cap + key),
+                                         (pv_lds_void*)(slot + k * kPwBlock), 16, 0, 0);
+      } else {
+        const int prow = 2 * (k - kPbVBlocks) + lane % 2;
+        const int r = prow / (4 * kPbRows), rr = min((prow / 4) % kPbRows, n - 1), hl = prow % 4;
+        const int jb0 = r ? jb0_1 : 0, last4 = ((r ? end1 : end0) - 1) & ~3;
+        const int key = max(0, min(jb0 + kPwChunk * c + 4 * (lane / 2), last4));
+        __builtin_amdgcn_global_load_lds(
+            (const pv_global_void*)(pbase + (static_cast<uint64_t>(rr) * a.q_heads + hl) * a.cap + key),
+            (pv_lds_void*)(slot + k * kPwBlock), 16, 0, 0);
+      }
+    }
+  };
+
+  if (producer) {
+    for (int c = 0; c < kPbSlots - 1; ++c) copy(c);
+    __builtin_amdgcn_s_waitcnt(pv_vmcnt((kPbSlots - 2) * kPbCopies));  // chunk 0 has landed
+  }
+
+  // Chains: wave 2 r runs range r; lane = (head hl, feature f).  V row
+  // r * 16 + f lives in block (r * 16 + f) / 4 at 16-byte piece 4 q + f % 4
+  // for key group q (8 keys); probability row (r * kPbRows + rr) * 4 + hl in
+  // block 8 + row / 2 at piece 2 q + row % 2 for key group q (4 keys).
+  const int hl = lane / kPwFeatures, f = lane % kPwFeatures;
+  const int r = wave / 2;
+  const int jb0 = r ? jb0_1 : 0;
+  const int vrow = r * kPwFeatures + f;
+  const int voff = (vrow / 4) * kPwBlock + (vrow % 4) * 16;
+  int poff[kPbRows];
+#pragma unroll
+  for (int rr = 0; rr < kPbRows; ++rr) {
+    const int prow = (r * kPbRows + rr) * 4 + hl;
+    poff[rr] = (kPbVBlocks + prow / 2) * kPwBlock + (prow % 2) * 16;
+  }
+  // Row rr's range in keys: [begin_rr, end_rr).
+  auto begin_of = [&](int rr) { return r ? split_of(rr) : 0; };
+  auto end_of = [&](int rr) { return r ? count_of(rr) : split_of(rr); };
+  float acc[kPbRows];
+#pragma unroll
+  for (int rr = 0; rr < kPbRows; ++rr) acc[rr] = 0.0f;
+
+  for (int c = 0; c < chunks; ++c) {
+    __builtin_amdgcn_s_barrier();  // chunk c is in its slot; every chain is done with chunk c - 1
+    if (producer) {
+      copy(c + kPbSlots - 1);
+      __builtin_amdgcn_s_waitcnt(pv_vmcnt((kPbSlots - 2) * kPbCopies));
+      continue;
+    }
+    const uint8_t* cur = slot_of(c);
+    const uint8_t* vb = cur + voff;
+    const int cs = jb0 + kPwChunk * c;
+    // Keys [lo, hi) of the chunk lie in every row's range; [lo_any, hi_any)
+    // in some row's (wave-uniform: the rows and ranges are).
+    int lo = 0, hi = kPwChunk, lo_any = kPwChunk, hi_any = 0;
+#pragma unroll
+    for (int rr = 0; rr < kPbRows; ++rr) {
+      if (rr < n) {
+        const int l0 = max(begin_of(rr) - cs, 0), h0 = min(end_of(rr) - cs, kPwChunk);
+        lo = max(lo, l0);
+        hi = min(hi, h0);
+        if (h0 > l0) {
+          lo_any = min(lo_any, l0);
+          hi_any = max(hi_any, h0);
+        }
+      }
+    }
+    // Key group q: its V row (8 keys) and each row's 8 probabilities.
+    struct Group {
+      u32x4 w;
+      float4 pa[kPbRows], pc[kPbRows];
+    };
+    auto read = [&](Group& x, int q) {
+      x.w = *reinterpret_cast<const u32x4*>(vb + 64 * q);
+#pragma unroll
+      for (int rr = 0; rr < kPbRows; ++rr) {
+        x.pa[rr] = *reinterpret_cast<const float4*>(cur + poff[rr] + 32 * (2 * q));
+        x.pc[rr] = *reinterpret_cast<const float4*>(cur + poff[rr] + 32 * (2 * q + 1));
+      }
+    };
+    auto run = [&](const Group& x, int q, bool masked) {
+      const float vv[8] = {dl_bf16_lo(x.w.x), dl_bf16_hi(x.w.x), dl_bf16_lo(x.w.y), dl_bf16_hi(x.w.y),
+                           dl_bf16_lo(x.w.z), dl_bf16_hi(x.w.z), dl_bf16_lo(x.w.w), dl_bf16_hi(x.w.w)};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = cs + 8 * q + e;
+#pragma unroll
+        for (int rr = 0; rr < kPbRows; ++rr) {
+          const float4& v4 = e < 4 ? x.pa[rr] : x.pc[rr];
+          const int i4 = e & 3;
+          const float pe = i4 == 0 ? v4.x : i4 == 1 ? v4.y : i4 == 2 ? v4.z : v4.w;
+          if (!masked || (rr < n && j >= begin_of(rr) && j < end_of(rr))) acc[rr] = fma_rn(pe, vv[e], acc[rr]);
+        }
+      }
+    };
+    if (lo == 0 && hi == kPwChunk) {
+      // Every group of the chunk lies in every row's range: the reads of
+      // group q + 1 are issued before the FMAs of group q (the order is
+      // pinned with scheduling barriers), so the LDS latency hides behind
+      // the chains.
+      constexpr int kGroups = kPwChunk / 8;
+      Group x[2];
+      read(x[0], 0);
+#pragma unroll
+      for (int q = 0; q < kGroups; ++q) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (q + 1 < kGroups) read(x[(q + 1) & 1], q + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        run(x[q & 1], q, false);
+      }
+    } else {
+      for (int q = lo_any / 8; q * 8 < hi_any; ++q) {
+        Group x;
+        read(x, q);
+        run(x, q, !(8 * q >= lo && 8 * q + 8 <= hi));
+      }
+    }
+  }
+  if (producer) {
+    __builtin_amdgcn_s_waitcnt(pv_vmcnt(0));  // no copy outstanding at exit
+  }
+  if (wave == 2) {
+#pragma unroll
+    for (int rr = 0; rr < kPbRows; ++rr) second[rr][lane] = acc[rr];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int rr = 0; rr < kPbRows; ++rr)
+      if (rr < n)
+        a.att[static_cast<uint64_t>(rb + rr) * a.q_heads * kHeadDim + (g * group + hl) * kHeadDim +
+              fb * kPwFeatures + f] = bf16_bits(acc[rr] + second[rr][lane]);
+  }
 }
 
 // Short-context attention in one kernel (the reference's retained-score
@@ -3014,6 +3291,7 @@ void prepare_kernels_all(dl_plan* p) {
   const auto& c = p->model->cfg;
   const int D = c.hidden, QW = c.q_heads * c.head_dim, F = c.ffn;
   allow_lds(k_attn_pv, kPvLds);
+  allow_lds(k_attn_pv_block, kPbLds);
   allow_lds(k_xgemm<16, kXgQ>, xgemm_lds(16));
   allow_lds(k_xgemm<32, kXgKV>, xgemm_lds(32));
   allow_lds(k_xgemm<16, kXgResidual>, xgemm_lds(16));
@@ -3165,11 +3443,22 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
         }
       });
       break;
-    case 1: k_attn_qk<<<dim3(c.kv_heads, p->cap / 64, B), kBlock, 0, s>>>(aa); break;
+    case 1:
+      // Consecutive positions of one sequence (their keys appended first)
+      // share each key tile over a block of rows.
+      if (r.pos_step == 1 && B >= static_cast<uint32_t>(kQkRows))
+        k_attn_qk_rows<<<dim3(c.kv_heads, p->cap / 64, (B + kQkRows - 1) / kQkRows), kBlock, 0, s>>>(
+            aa, static_cast<int>(B));
+      else
+        k_attn_qk<<<dim3(c.kv_heads, p->cap / 64, B), kBlock, 0, s>>>(aa);
+      break;
     case 2: k_attn_softmax<<<dim3(c.q_heads, B), kSoftmaxThreads, size_t(p->cap) * sizeof(float), s>>>(aa); break;
     case 3:
       if (B == 1)
         k_attn_pv<<<dim3(c.kv_heads * (kHeadDim / kPvFeatures), 1), kPvThreads, kPvLds, s>>>(aa);
+      else if (r.pos_step == 1 && B >= static_cast<uint32_t>(2 * kPbRows))
+        k_attn_pv_block<<<dim3(c.kv_heads * (kHeadDim / kPwFeatures), (B + kPbRows - 1) / kPbRows), kPwThreads,
+                          kPbLds, s>>>(aa, static_cast<int>(B));
       else
         k_attn_pv_rows<<<dim3(c.kv_heads * (kHeadDim / kPwFeatures), B), kPwThreads, 0, s>>>(aa);
       break;
