@@ -1,7 +1,10 @@
 """GPU checks of the exact chunked prompt pass (dl_plan_prefill_exact).
 
-The pass runs the prompt positions through the decode kernels up to eight
-positions at a time.  Parity is bit-exact: for every case the caches, the
+The pass runs the prompt positions in chunks of up to 128 positions: the
+projections of a chunk of 16 positions or more as many-row exact GEMMs,
+fewer through the batched decode GEMVs; from 1536 keys the attention of a
+chunk of 8 rows or more shares key tiles and V rows across rows.  Parity is
+bit-exact: for every case the caches, the
 token streams and the last logits equal those of a plan that consumes the
 same prompt one position per step through the token loop (itself bit-exact
 with the CPU contract mirror, tests/test_gpu_model.py).
@@ -79,6 +82,18 @@ def test_exact_prefill_across_the_fused_attention_limit(model1):
     prompt = [int(t) for t in np.random.default_rng(77).integers(0, 2048, 1600)]
     a, b = run_pair(model1, prompt, 4, capacity=1664)
     assert_same(model1, a, b, 1604)
+
+
+@pytest.mark.parametrize("length", [1545, 1551, 1561, 1669])
+def test_exact_prefill_chunk_remainders_past_the_fused_limit(model1, length):
+    """Prompts whose last chunk lies past 1536 keys with 8, 14, 24 and 4
+    rows: the row-block attention with whole and partial last blocks (8, 14
+    and 24 rows), the batched GEMVs (8 and 14 rows), the many-row GEMM (24
+    rows) and the one-row-per-workgroup kernels (4 rows), each row at its
+    own split point."""
+    prompt = [int(t) for t in np.random.default_rng(length).integers(0, 2048, length)]
+    a, b = run_pair(model1, prompt, 3, capacity=1728)
+    assert_same(model1, a, b, length + 3)
 
 
 def test_exact_prefill_batch_with_capture_and_steering(model2, device, queue):
