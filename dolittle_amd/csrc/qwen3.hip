@@ -1112,32 +1112,37 @@ __global__ __launch_bounds__(kPwThreads) void k_attn_pv_rows(AttnArgs a) {
 }
 
 // k_attn_pv_rows for the rows of the chunked prompt pass (consecutive
-// positions of one sequence, pos_step 1): a workgroup runs kPbRows rows, so
-// each V row it stages and widens feeds kPbRows chains.  Grid (kv head * 8
-// feature blocks, row blocks), 256 threads.  Waves 0 and 2 run the two PV
-// key ranges: for row r with n_r keys, range 0 is [0, ceil(n_r / 2)) and
-// range 1 the rest; lane = (head, feature) holds one accumulator per row of
-// each range, so every output feature is round(A + B) of the same two
-// ascending FMA chains as in k_attn_pv_rows (attention.cu:331-375).  A
-// wave stages the union of its rows' ranges; a key group inside every row's
-// range runs unmasked, the groups at the range ends run masked per row.
-// Waves 1 and 3 copy each chunk's 32 V rows and the 4 heads' probability
-// rows of every row of the block into a kPbSlots-slot LDS ring
-// (global_load_lds), kPbSlots - 1 chunks ahead, as k_attn_pv_rows does.
+// positions of one sequence, pos_step 1): a workgroup runs kPbRows rows of
+// half the features of one K/V group.  Grid (kv head * 2 feature halves, row
+// blocks), 256 threads.  Waves 0 and 2 run the two PV key ranges: for row r
+// with n_r keys, range 0 is [0, ceil(n_r / 2)) and range 1 the rest.  Lane
+// (head, feature group) owns 4 features of one head for every row of the
+// block, one accumulator per (row, feature), so each output feature is
+// round(A + B) of the same two ascending FMA chains as in k_attn_pv_rows
+// (attention.cu:331-375), while each widened V value feeds kPbRows FMAs and
+// each probability 4.  A wave runs the union of its rows' ranges; a key
+// group inside every row's range runs unmasked, the groups at the range
+// ends masked per row (wave-uniform: a wave's rows are its lanes' rows).
+// The lanes read their V rows (BF16, 8 keys per 16-byte load, two groups
+// ahead) straight from memory; waves 1 and 3 copy the probability rows of
+// the block's rows into a kPbSlots-slot LDS ring (global_load_lds),
+// kPbSlots - 1 chunks ahead, as k_attn_pv_rows does.
 constexpr int kPbRows = 4;
-constexpr int kPbSlots = 3;
-constexpr int kPbVBlocks = 8;                      // 2 ranges x 16 features, 4 rows per block
-constexpr int kPbPBlocks = 2 * kPbRows * 4 / 2;    // 2 ranges x kPbRows rows x 4 heads, 2 rows per block
-constexpr int kPbCopies = (kPbVBlocks + kPbPBlocks) / 2;  // per copy wave and chunk
-constexpr int kPbSlotBytes = (kPbVBlocks + kPbPBlocks) * kPwBlock;
+constexpr int kPbSlots = 4;
+constexpr int kPbFeat = 4;                          // features per chain lane
+constexpr int kPbHalf = 64;                         // features per workgroup
+constexpr int kPbPBlocks = 2 * kPbRows * 4 / 2;     // 2 ranges x kPbRows rows x 4 heads, 2 rows per block
+constexpr int kPbCopies = kPbPBlocks / 2;           // per copy wave and chunk
+constexpr int kPbSlotBytes = kPbPBlocks * kPwBlock;
 constexpr size_t kPbLds = size_t(kPbSlots) * kPbSlotBytes;
 
 __global__ __launch_bounds__(kPwThreads) void k_attn_pv_block(AttnArgs a, int rows) {
   extern __shared__ __align__(16) uint8_t pb_lds[];
-  __shared__ float second[kPbRows][64];
+  __shared__ float second[kPbRows][kPbFeat][64];
   static_assert((kPbSlots - 1) * kPbCopies <= 63, "the wait counter holds at most 63 outstanding copies");
+  static_assert(4 * (kPbHalf / kPbFeat) == 64, "lane = (head, feature group)");
   if (!a.ctl->active) return;
-  const int g = blockIdx.x % a.kv_heads, fb = blockIdx.x / a.kv_heads, rb = blockIdx.y * kPbRows;
+  const int g = blockIdx.x / 2, fh = blockIdx.x % 2, rb = blockIdx.y * kPbRows;
   const int n = min(kPbRows, rows - rb);
   const int pos0 = static_cast<int>(a.ctl->position) + rb;
   // Row rr attends to keys [0, pos0 + rr]; its ranges split at
@@ -1152,39 +1157,28 @@ __global__ __launch_bounds__(kPwThreads) void k_attn_pv_block(AttnArgs a, int ro
   const int chunks = max(chunks0, chunks1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
   const int group = a.q_heads / a.kv_heads;
-  const uint16_t* vbase = a.v_cache + static_cast<uint64_t>(g * kHeadDim + fb * kPwFeatures) * a.cap;
   const float* pbase = a.probs + (static_cast<uint64_t>(rb) * a.q_heads + g * group) * a.cap;
   const bool producer = (wave & 1) != 0;
   auto slot_of = [&](int c) { return pb_lds + (c % kPbSlots) * kPbSlotBytes; };
 
-  // Copy k of a chunk fills block k of its slot.  k < 8: V rows 4k .. 4k + 3
-  // (row = range * 16 + feature); lane L fetches row 4k + L % 4, keys
-  // 8 (L / 4) .. + 7.  k >= 8: probability rows 2 (k - 8) + {0, 1} (row =
-  // (range * kPbRows + rr) * 4 + head); lane L fetches row 2 (k - 8) + L % 2,
-  // keys 4 (L / 2) .. + 3.  Sources past a range are clamped to its last 8
-  // (4) keys, rows past the block's last row repeat it; the chains never use
-  // those values.  Producer wave w takes the copies k = w / 2 + 2 m.
+  // Copy k of a chunk fills block k of its slot: probability rows
+  // 2 k + {0, 1} (row = (range * kPbRows + rr) * 4 + head); lane L fetches
+  // row 2 k + L % 2, keys 4 (L / 2) .. + 3.  Sources past a range are clamped
+  // to its last 4 keys, rows past the block's last row repeat it; the chains
+  // never use those values.  Producer wave w takes the copies k = w / 2 + 2 m.
   auto copy = [&](int c) {
     uint8_t* slot = slot_of(c);
     c = min(c, chunks - 1);
 #pragma unroll
     for (int m = 0; m < kPbCopies; ++m) {
       const int k = wave / 2 + 2 * m;
-      if (k < kPbVBlocks) {
-        const int row = 4 * k + lane % 4, r = row / kPwFeatures, f = row % kPwFeatures;
-        const int jb0 = r ? jb0_1 : 0, last8 = ((r ? end1 : end0) - 1) & ~7;
-        const int key = max(0, min(jb0 + kPwChunk * c + 8 * (lane / 4), last8));
-        __builtin_amdgcn_global_load_lds((const pv_global_void*)(vbase + static_cast<uint64_t>(f) * a.cap + key),
-                                         (pv_lds_void*)(slot + k * kPwBlock), 16, 0, 0);
-      } else {
-        const int prow = 2 * (k - kPbVBlocks) + lane % 2;
-        const int r = prow / (4 * kPbRows), rr = min((prow / 4) % kPbRows, n - 1), hl = prow % 4;
-        const int jb0 = r ? jb0_1 : 0, last4 = ((r ? end1 : end0) - 1) & ~3;
-        const int key = max(0, min(jb0 + kPwChunk * c + 4 * (lane / 2), last4));
-        __builtin_amdgcn_global_load_lds(
-            (const pv_global_void*)(pbase + (static_cast<uint64_t>(rr) * a.q_heads + hl) * a.cap + key),
-            (pv_lds_void*)(slot + k * kPwBlock), 16, 0, 0);
-      }
+      const int prow = 2 * k + lane % 2;
+      const int r = prow / (4 * kPbRows), rr = min((prow / 4) % kPbRows, n - 1), hl = prow % 4;
+      const int jb0 = r ? jb0_1 : 0, last4 = ((r ? end1 : end0) - 1) & ~3;
+      const int key = max(0, min(jb0 + kPwChunk * c + 4 * (lane / 2), last4));
+      __builtin_amdgcn_global_load_lds(
+          (const pv_global_void*)(pbase + (static_cast<uint64_t>(rr) * a.q_heads + hl) * a.cap + key),
+          (pv_lds_void*)(slot + k * kPwBlock), 16, 0, 0);
     }
   };
 
@@ -1193,27 +1187,41 @@ __global__ __launch_bounds__(kPwThreads) void k_attn_pv_block(AttnArgs a, int ro
     __builtin_amdgcn_s_waitcnt(pv_vmcnt((kPbSlots - 2) * kPbCopies));  // chunk 0 has landed
   }
 
-  // Chains: wave 2 r runs range r; lane = (head hl, feature f).  V row
-  // r * 16 + f lives in block (r * 16 + f) / 4 at 16-byte piece 4 q + f % 4
-  // for key group q (8 keys); probability row (r * kPbRows + rr) * 4 + hl in
-  // block 8 + row / 2 at piece 2 q + row % 2 for key group q (4 keys).
-  const int hl = lane / kPwFeatures, f = lane % kPwFeatures;
+  // Chains: wave 2 r runs range r; lane = (head hl, feature group fg), the
+  // features fh * 64 + 4 fg .. + 3.  Probability row (r * kPbRows + rr) * 4
+  // + hl lives in block row / 2 at piece 2 q + row % 2 for key group q (4
+  // keys).
+  const int hl = lane / (kPbHalf / kPbFeat), fg = lane % (kPbHalf / kPbFeat);
   const int r = wave / 2;
   const int jb0 = r ? jb0_1 : 0;
-  const int vrow = r * kPwFeatures + f;
-  const int voff = (vrow / 4) * kPwBlock + (vrow % 4) * 16;
+  const int f0 = fh * kPbHalf + kPbFeat * fg;
+  const uint16_t* vrow = a.v_cache + static_cast<uint64_t>(g * kHeadDim + f0) * a.cap;
   int poff[kPbRows];
 #pragma unroll
   for (int rr = 0; rr < kPbRows; ++rr) {
     const int prow = (r * kPbRows + rr) * 4 + hl;
-    poff[rr] = (kPbVBlocks + prow / 2) * kPwBlock + (prow % 2) * 16;
+    poff[rr] = (prow / 2) * kPwBlock + (prow % 2) * 16;
   }
-  // Row rr's range in keys: [begin_rr, end_rr).
   auto begin_of = [&](int rr) { return r ? split_of(rr) : 0; };
   auto end_of = [&](int rr) { return r ? count_of(rr) : split_of(rr); };
-  float acc[kPbRows];
+  // The last 8 keys of the wave's union range: V loads past it are clamped
+  // there (inside the cache rows) and never used.
+  const int last8 = ((r ? end1 : end0) - 1) & ~7;
+  float acc[kPbRows][kPbFeat];
 #pragma unroll
-  for (int rr = 0; rr < kPbRows; ++rr) acc[rr] = 0.0f;
+  for (int rr = 0; rr < kPbRows; ++rr)
+#pragma unroll
+    for (int i = 0; i < kPbFeat; ++i) acc[rr][i] = 0.0f;
+  // V of the key group starting at key `key`: 8 keys of each of the lane's
+  // 4 feature rows.
+  struct VGroup {
+    u32x4 w[kPbFeat];
+  };
+  auto load_v = [&](VGroup& x, int key) {
+    const int k = min(max(key, 0), last8);
+#pragma unroll
+    for (int i = 0; i < kPbFeat; ++i) x.w[i] = *reinterpret_cast<const u32x4*>(vrow + static_cast<uint64_t>(i) * a.cap + k);
+  };
 
   for (int c = 0; c < chunks; ++c) {
     __builtin_amdgcn_s_barrier();  // chunk c is in its slot; every chain is done with chunk c - 1
@@ -1223,7 +1231,6 @@ __global__ __launch_bounds__(kPwThreads) void k_attn_pv_block(AttnArgs a, int ro
       continue;
     }
     const uint8_t* cur = slot_of(c);
-    const uint8_t* vb = cur + voff;
     const int cs = jb0 + kPwChunk * c;
     // Keys [lo, hi) of the chunk lie in every row's range; [lo_any, hi_any)
     // in some row's (wave-uniform: the rows and ranges are).
@@ -1240,71 +1247,90 @@ __global__ __launch_bounds__(kPwThreads) void k_attn_pv_block(AttnArgs a, int ro
         }
       }
     }
-    // Key group q: its V row (8 keys) and each row's 8 probabilities.
-    struct Group {
-      u32x4 w;
-      float4 pa[kPbRows], pc[kPbRows];
-    };
-    auto read = [&](Group& x, int q) {
-      x.w = *reinterpret_cast<const u32x4*>(vb + 64 * q);
+    const int q0 = lo_any / 8, q1 = (hi_any + 7) / 8;
+    if (q1 <= q0) continue;
+    auto run = [&](const VGroup& x, int q) {
+      const bool masked = !(8 * q >= lo && 8 * q + 8 <= hi);
+      float pp[kPbRows][8];
 #pragma unroll
       for (int rr = 0; rr < kPbRows; ++rr) {
-        x.pa[rr] = *reinterpret_cast<const float4*>(cur + poff[rr] + 32 * (2 * q));
-        x.pc[rr] = *reinterpret_cast<const float4*>(cur + poff[rr] + 32 * (2 * q + 1));
+        const float4 pa = *reinterpret_cast<const float4*>(cur + poff[rr] + 32 * (2 * q));
+        const float4 pc = *reinterpret_cast<const float4*>(cur + poff[rr] + 32 * (2 * q + 1));
+        pp[rr][0] = pa.x; pp[rr][1] = pa.y; pp[rr][2] = pa.z; pp[rr][3] = pa.w;
+        pp[rr][4] = pc.x; pp[rr][5] = pc.y; pp[rr][6] = pc.z; pp[rr][7] = pc.w;
       }
-    };
-    auto run = [&](const Group& x, int q, bool masked) {
-      const float vv[8] = {dl_bf16_lo(x.w.x), dl_bf16_hi(x.w.x), dl_bf16_lo(x.w.y), dl_bf16_hi(x.w.y),
-                           dl_bf16_lo(x.w.z), dl_bf16_hi(x.w.z), dl_bf16_lo(x.w.w), dl_bf16_hi(x.w.w)};
+      auto widen = [&](int e, float (&vf)[kPbFeat]) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int j = cs + 8 * q + e;
+        for (int i = 0; i < kPbFeat; ++i) {
+          const uint32_t word = (e >> 1) == 0 ? x.w[i].x : (e >> 1) == 1 ? x.w[i].y : (e >> 1) == 2 ? x.w[i].z : x.w[i].w;
+          vf[i] = (e & 1) ? dl_bf16_hi(word) : dl_bf16_lo(word);
+        }
+      };
+      if (!masked) {
 #pragma unroll
-        for (int rr = 0; rr < kPbRows; ++rr) {
-          const float4& v4 = e < 4 ? x.pa[rr] : x.pc[rr];
-          const int i4 = e & 3;
-          const float pe = i4 == 0 ? v4.x : i4 == 1 ? v4.y : i4 == 2 ? v4.z : v4.w;
-          if (!masked || (rr < n && j >= begin_of(rr) && j < end_of(rr))) acc[rr] = fma_rn(pe, vv[e], acc[rr]);
+        for (int e = 0; e < 8; ++e) {
+          float vf[kPbFeat];
+          widen(e, vf);
+#pragma unroll
+          for (int rr = 0; rr < kPbRows; ++rr)
+#pragma unroll
+            for (int i = 0; i < kPbFeat; ++i) acc[rr][i] = fma_rn(pp[rr][e], vf[i], acc[rr][i]);
+        }
+      } else {
+        // Each step kept only where the key lies in the row's range (a
+        // select, so the chain is unchanged elsewhere).
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int j = cs + 8 * q + e;
+          float vf[kPbFeat];
+          widen(e, vf);
+#pragma unroll
+          for (int rr = 0; rr < kPbRows; ++rr) {
+            const bool in = rr < n && j >= begin_of(rr) && j < end_of(rr);
+#pragma unroll
+            for (int i = 0; i < kPbFeat; ++i) {
+              const float t = fma_rn(pp[rr][e], vf[i], acc[rr][i]);
+              acc[rr][i] = in ? t : acc[rr][i];
+            }
+          }
         }
       }
     };
-    if (lo == 0 && hi == kPwChunk) {
-      // Every group of the chunk lies in every row's range: the reads of
-      // group q + 1 are issued before the FMAs of group q (the order is
-      // pinned with scheduling barriers), so the LDS latency hides behind
-      // the chains.
-      constexpr int kGroups = kPwChunk / 8;
-      Group x[2];
-      read(x[0], 0);
-#pragma unroll
-      for (int q = 0; q < kGroups; ++q) {
-        __builtin_amdgcn_sched_barrier(0);
-        if (q + 1 < kGroups) read(x[(q + 1) & 1], q + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        run(x[q & 1], q, false);
-      }
-    } else {
-      for (int q = lo_any / 8; q * 8 < hi_any; ++q) {
-        Group x;
-        read(x, q);
-        run(x, q, !(8 * q >= lo && 8 * q + 8 <= hi));
-      }
+    // Two key groups of V in flight ahead of the one being multiplied.
+    VGroup x0, x1, x2;
+    load_v(x0, cs + 8 * q0);
+    load_v(x1, cs + 8 * (q0 + 1));
+    int q = q0;
+    for (; q + 3 <= q1; q += 3) {
+      load_v(x2, cs + 8 * (q + 2));
+      run(x0, q);
+      load_v(x0, cs + 8 * (q + 3));
+      run(x1, q + 1);
+      load_v(x1, cs + 8 * (q + 4));
+      run(x2, q + 2);
     }
+    if (q < q1) run(x0, q);
+    if (q + 1 < q1) run(x1, q + 1);
   }
   if (producer) {
     __builtin_amdgcn_s_waitcnt(pv_vmcnt(0));  // no copy outstanding at exit
   }
   if (wave == 2) {
 #pragma unroll
-    for (int rr = 0; rr < kPbRows; ++rr) second[rr][lane] = acc[rr];
+    for (int rr = 0; rr < kPbRows; ++rr)
+#pragma unroll
+      for (int i = 0; i < kPbFeat; ++i) second[rr][i][lane] = acc[rr][i];
   }
   __syncthreads();
   if (wave == 0) {
 #pragma unroll
     for (int rr = 0; rr < kPbRows; ++rr)
-      if (rr < n)
-        a.att[static_cast<uint64_t>(rb + rr) * a.q_heads * kHeadDim + (g * group + hl) * kHeadDim +
-              fb * kPwFeatures + f] = bf16_bits(acc[rr] + second[rr][lane]);
+      if (rr < n) {
+#pragma unroll
+        for (int i = 0; i < kPbFeat; ++i)
+          a.att[static_cast<uint64_t>(rb + rr) * a.q_heads * kHeadDim + (g * group + hl) * kHeadDim + f0 + i] =
+              bf16_bits(acc[rr][i] + second[rr][i][lane]);
+      }
   }
 }
 
@@ -3457,8 +3483,8 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       if (B == 1)
         k_attn_pv<<<dim3(c.kv_heads * (kHeadDim / kPvFeatures), 1), kPvThreads, kPvLds, s>>>(aa);
       else if (r.pos_step == 1 && B >= static_cast<uint32_t>(2 * kPbRows))
-        k_attn_pv_block<<<dim3(c.kv_heads * (kHeadDim / kPwFeatures), (B + kPbRows - 1) / kPbRows), kPwThreads,
-                          kPbLds, s>>>(aa, static_cast<int>(B));
+        k_attn_pv_block<<<dim3(c.kv_heads * (kHeadDim / kPbHalf), (B + kPbRows - 1) / kPbRows), kPwThreads, kPbLds,
+                          s>>>(aa, static_cast<int>(B));
       else
         k_attn_pv_rows<<<dim3(c.kv_heads * (kHeadDim / kPwFeatures), B), kPwThreads, 0, s>>>(aa);
       break;
