@@ -4673,7 +4673,11 @@ int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt
         dl::k_prefill_embed<<<n, dl::kBlock, 0, s>>>(ea);
         const StepRows r{ex.h, ex.q, ex.k, ex.att, ex.act, ex.scores, ex.probs, n,
                          uint64_t(seq) * plan->cache_seq_stride, 1, 0, 1, 1, static_cast<int>(seq), ex.x16, ex.x32};
-        const bool short_context = p0 + n <= static_cast<uint32_t>(dl::kFusedKeys);
+        // Chunks of 8 rows or more share key tiles and V rows across rows in
+        // the split kernels (k_attn_qk_rows, k_attn_pv_block) at any context;
+        // fewer rows run the one-kernel attention below kFusedKeys.
+        const bool short_context = n < static_cast<uint32_t>(2 * dl::kPbRows) &&
+                                   p0 + n <= static_cast<uint32_t>(dl::kFusedKeys);
         for (uint32_t l = 0; l < c.layers; ++l) {
           launch_step_kernel(plan, s, 0, l, ex.ctl, r);  // Q, K, V (V into the cache)
           launch_step_kernel(plan, s, 9, l, ex.ctl, r);  // rotated K into the cache
