@@ -630,7 +630,7 @@ def main() -> int:
         },
         "prefill_tokens_per_s": round(prefill_positions / (prefill_ms * 1e-3), 1),
         "prefill_exact": {"positions": prefill_positions, "ms": round(prefill_ms, 3),
-                          "path": "dl_plan_prefill_exact: chunks of up to 128 positions through many-row "
+                          "path": "dl_plan_prefill_exact: chunks of up to 512 positions through many-row "
                                   "exact GEMMs and row-block attention, caches bit-identical to the token loop"},
         "prefill_mfma": mfma,
         "hbm_roofline_step": {"bytes_per_step": int(bytes_step), "achieved_GBs": round(step_gbs, 1),

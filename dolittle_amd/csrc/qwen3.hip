@@ -4622,8 +4622,10 @@ int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_lengt
 // are bit-identical to consuming the prompt one position per step.
 // Consecutive prompt positions per step of the exact chunked prompt pass:
 // their projections run as many-row exact GEMMs (each weight read once per
-// chunk), their attention row by row.
-constexpr uint32_t kExactChunk = 128;
+// chunk), their attention row by row.  The chunk's score and probability
+// rows take kExactChunk x q_heads x capacity floats each (128 KiB per cache
+// position at 512 rows and 32 heads).
+constexpr uint32_t kExactChunk = 512;
 
 int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length) {
   return guard([&] {

@@ -453,7 +453,7 @@ int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_lengt
 /* The exact prompt pass, replacing the reference's row-by-row forward of a
  * prompt (executor.cpp:285-716 with the row kernels of projection.cu,
  * attention.cu and normalization.cu): positions [0, prompt_length - 1) in
- * chunks of up to 128 consecutive positions, every row the same reduction
+ * chunks of up to 512 consecutive positions, every row the same reduction
  * chains as a single-position step (the projections of a chunk of 16 rows
  * or more as many-row GEMMs over the same chains).  The caches end
  * bit-identical to consuming the prompt through dl_plan_generate; a

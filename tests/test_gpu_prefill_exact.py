@@ -1,6 +1,6 @@
 """GPU checks of the exact chunked prompt pass (dl_plan_prefill_exact).
 
-The pass runs the prompt positions in chunks of up to 128 positions: the
+The pass runs the prompt positions in chunks of up to 512 positions: the
 projections of a chunk of 16 positions or more as many-row exact GEMMs,
 fewer through the batched decode GEMVs; from 1536 keys the attention of a
 chunk of 8 rows or more shares key tiles and V rows across rows.  Parity is
@@ -84,7 +84,7 @@ def test_exact_prefill_across_the_fused_attention_limit(model1):
     assert_same(model1, a, b, 1604)
 
 
-@pytest.mark.parametrize("length", [1545, 1551, 1561, 1669])
+@pytest.mark.parametrize("length", [1545, 1551, 1561, 1541])
 def test_exact_prefill_chunk_remainders_past_the_fused_limit(model1, length):
     """Prompts whose last chunk lies past 1536 keys with 8, 14, 24 and 4
     rows: the row-block attention with whole and partial last blocks (8, 14
