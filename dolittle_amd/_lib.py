@@ -205,7 +205,7 @@ SIGNATURES = {
     "dl_plan_set_step_window": [vp, u32],
     "dl_plan_steps_enqueued": [vp, C.POINTER(u64)],
     "dl_plan_prefill": [vp, u32p, u32],
-    "dl_plan_prefill_exact": [vp, u32p, u32],
+    "dl_plan_prefill_mfma": [vp, u32p, u32],
     "dl_plan_read_prefill_hidden": [vp, u64, u64, u16p],
     "dl_plan_read_prefill_buffer": [vp, u32, u64, u64, u16p],
     "dl_prefill_projection": [vp, vp, vp, vp, vp, u64, u64, u64],

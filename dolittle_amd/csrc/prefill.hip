@@ -49,14 +49,28 @@ __device__ __forceinline__ uint64_t packed_offset(int n, int P, int K, int kpos)
 }
 
 // SiluMultiply on BF16-rounded operands (elementwise.cu:62-87), two-sided
-// as there, with the hardware exponential and reciprocal (a few ulp in FP32)
-// instead of the decode path's correctly rounded FP64-evaluated exponential:
-// the MFMA prefill is compared with a tolerance.
-__device__ __forceinline__ float silu_times_fast(float a, float b) {
-  const float e = __expf(-fabsf(a));
-  const float r = __builtin_amdgcn_rcpf(1.0f + e);
-  const float sigmoid = a >= 0.0f ? r : e * r;
+// as there, with the decode path's correctly rounded exponential, so an
+// activation row equals the exact chain's whenever its gate and up inputs do.
+__device__ __forceinline__ float silu_times(float a, float b) {
+  const float e = dl_expf(a >= 0.0f ? -a : a);
+  const float sigmoid = a >= 0.0f ? 1.0f / (1.0f + e) : e / (1.0f + e);
   return dl_round_bf16(a * sigmoid) * b;
+}
+
+// exp(x) for x <= 0 within about 2 ulp: 2^(x log2 e) with the product split
+// into its rounded value t and its rounding error (an FMA recovers it; the
+// tail of log2 e adds the rest), so exp(x) = 2^t (1 + err ln 2 + O(err^2)),
+// |err| < 2^-17, and the hardware 2^t (v_exp_f32, 1 ulp) is corrected by one
+// FMA.  Used for the probabilities of the MFMA pass; the exact pass uses the
+// correctly rounded dl_expf.
+__device__ __forceinline__ float exp_nonpositive(float x) {
+  constexpr float kLog2e = 0x1.715476p+0f;          // log2(e) rounded to binary32
+  constexpr float kLog2eTail = 0x1.4ae0c0p-26f;     // log2(e) - kLog2e
+  constexpr float kLn2 = 0x1.62e430p-1f;
+  const float t = x * kLog2e;
+  const float err = __builtin_fmaf(x, kLog2e, -t) + x * kLog2eTail;
+  const float p = __builtin_amdgcn_exp2f(t);
+  return __builtin_fmaf(p, err * kLn2, p);
 }
 
 // ------------------------------------------------------------------ GEMM
@@ -109,7 +123,7 @@ __device__ __forceinline__ void gemm_tile_epilogue(const GemmArgs& a, const floa
           const int r = gate_lane ? k : 8 + k;
           const int m = rows + 8 * (r / 4) + r % 4;
           out[static_cast<uint64_t>(m) * (a.N / 2)] =
-              dl_f32_to_bf16(silu_times_fast(dl_round_bf16(gate), dl_round_bf16(up)));
+              dl_f32_to_bf16(silu_times(dl_round_bf16(gate), dl_round_bf16(up)));
         }
       } else {
 #pragma unroll
@@ -455,12 +469,25 @@ __global__ __launch_bounds__(64) void k_heads(HeadArgs a) {
 // in that XCD's L2), each head's tiles heaviest (longest causal span) first.
 // Scores are computed transposed, S^T = K Q^T (16x16x32 MFMA), so each lane
 // owns one query: lane l holds keys 4 (l / 16) + t of every 16-key block for
-// query l % 16, the online softmax (FP32) reduces in-lane and across the
-// four lane groups, and O^T += V^T P^T takes P straight from registers.  In
-// the PV product the 32 keys of a K step are taken in the order the lane
-// holds them (keys 4g..4g+3 of two 16-key blocks for lane group g) on both
-// operands, and P is split exactly into three BF16 parts.
-__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_attention(AttnArgs a) {
+// query l % 16, and O^T += V^T E^T takes the exponentials straight from
+// registers.
+//
+// The softmax follows the reference's order (transformer-execution.md:
+// 149-170, attention.cu:231-383): a first pass over the keys finds the exact
+// maximum m of the query's visible scores; a second pass recomputes the same
+// scores (the same products in the same order, so the same bits), forms
+// e_j = exp(s_j - m) and sums them in 32 strided partials (partial j mod 32,
+// ascending j), merged by the descending half tree (offsets 16, 8, 4, 2, 1).
+// Partial j mod 32 of a 64-key tile is 16 (sub & 1) + 4 lg + t, so lane group
+// lg keeps partials 4 lg + t and 16 + 4 lg + t; the tree's first step is in
+// the lane, the next two across lane groups (xor 32, then xor 16), the last
+// two in the lane again.  In the PV product the 32 keys of a K step are taken
+// in the order the lane holds them (keys 4g..4g+3 of two 16-key blocks for
+// lane group g) on both operands, each e is split exactly into three BF16
+// parts, and the output is (sum e v) / l: the one division per feature takes
+// the place of the reference's per-key p = e / l, since the MFMA sum has its
+// own order anyway.
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_attention(AttnArgs a) {
   __shared__ __align__(16) uint16_t Ks[kKeyTile * kQRow];
   __shared__ __align__(16) uint16_t Vs[kHd * kVRow];
   const int tiles = (a.rows + kAttnRows - 1) / kAttnRows;
@@ -491,43 +518,54 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint16_t* kc = a.k_cache + static_cast<uint64_t>(g) * a.cap * kHd;
   const uint16_t* vc = a.v_cache + static_cast<uint64_t>(g) * kHd * a.cap;
 
-  // This lane's query and its softmax state; o[d] holds O^T rows
-  // 16 d + 4 lg + t (features) for the lane's query.
+  // This lane's query; o[d] holds O^T rows 16 d + 4 lg + t (features) for it.
   const int qrow = 16 * wave + lq;
   const int qpos = a.first_position + q0 + qrow;
   const int wave_first = a.first_position + q0 + 16 * wave;
-  float m_run = -INFINITY, l_run = 0.0f;
   floatx4 o[8];
 #pragma unroll
   for (int d = 0; d < 8; ++d) o[d] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int last_row = min(q0 + kAttnRows, a.rows) - 1;
   const int key_end = a.first_position + last_row + 1;
-  // K and V tiles go through registers: the next tile's loads are issued
-  // before this tile's products and stored to LDS once every wave is done
-  // with this tile.  One 35 KB buffer lets three workgroups share a CU.
+  // K (and in the second pass V) tiles go through registers: the next
+  // tile's loads are issued before this tile's products and stored to LDS
+  // once every wave is done with this tile.  Two workgroups share a CU (the
+  // second pass holds 178 VGPRs; at three waves per SIMD it spilled).
   u32x4 kr[4], vr[4];
-  auto load_tile = [&](int kt0) {
+  auto load_keys = [&](int kt0) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int i = tid + kAttnThreads * j;
       const int key = i / 16, col = (i % 16) * 8;
       const int kk = min(kt0 + key, a.cap - 1);
       kr[j] = *reinterpret_cast<const u32x4*>(kc + (kk * kHd + col));  // offsets fit 32 bits
+    }
+  };
+  auto load_values = [&](int kt0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = tid + kAttnThreads * j;
       const int d = i / 8, vcol = (i % 8) * 8;
       vr[j] = *reinterpret_cast<const u32x4*>(vc + (d * a.cap + min(kt0 + vcol, a.cap - 8)));
     }
   };
-  auto store_tile = [&](int kt0) {
+  auto store_keys = [&] {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int i = tid + kAttnThreads * j;
       const int key = i / 16, col = (i % 16) * 8;
       *reinterpret_cast<u32x4*>(&Ks[key * kQRow + 8 * ((col / 8) ^ key_swizzle(key % 16))]) = kr[j];
+    }
+  };
+  auto store_values = [&](int kt0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = tid + kAttnThreads * j;
       const int d = i / 8, vcol = (i % 8) * 8;
       u32x4 vv = vr[j];
       // Keys at or past key_end are masked for every query of this tile
-      // (p = 0); zero them so stale cache contents cannot turn 0 * v into NaN.
+      // (e = 0); zero them so stale cache contents cannot turn 0 * v into NaN.
       const int left = key_end - (kt0 + vcol);
       if (left < 8) {
         uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
@@ -541,18 +579,9 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3)
       vdst[1] = uint2{vv.z, vv.w};
     }
   };
-  load_tile(0);
-  for (int kt0 = 0; kt0 < key_end; kt0 += kKeyTile) {
-    if (kt0 > 0) __syncthreads();
-    store_tile(kt0);
-    __syncthreads();
-    if (kt0 + kKeyTile < key_end) load_tile(kt0 + kKeyTile);
-    const uint16_t* Kt = Ks;
-    const uint16_t* Vt = Vs;
-
-    // S^T for four 16-key blocks: s[sub][t] = score of key kt0 + 16 sub +
-    // 4 lg + t for the lane's query.
-    floatx4 s[4];
+  // Scaled scores of the tile's 64 keys for the lane's query: s[sub][t] is
+  // key kt0 + 16 sub + 4 lg + t.  Both passes run exactly this.
+  auto tile_scores = [&](floatx4 (&s)[4]) {
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) s[sub] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -560,62 +589,76 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3)
 #pragma unroll
       for (int sub = 0; sub < 4; ++sub) {
         const bf16x8 ka = as_bf16x8(
-            *reinterpret_cast<const u32x4*>(&Kt[(16 * sub + lq) * kQRow + 8 * (kpiece ^ (4 * ks))]));
+            *reinterpret_cast<const u32x4*>(&Ks[(16 * sub + lq) * kQRow + 8 * (kpiece ^ (4 * ks))]));
         s[sub] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[ks], s[sub], 0, 0, 0);
       }
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) s[sub][t] = s[sub][t] * a.scale;
+  };
+  // Key kt0 + 16 sub + 4 lg + t is visible to the lane's query when
+  // 16 sub + t <= lim; only a tile reaching past the wave's first query
+  // masks anything.
+  auto visible = [&](int kt0, int sub, int t) { return 16 * sub + t <= qpos - kt0 - 4 * lg; };
 
-    // Online softmax of the lane's query over the tile's 64 keys.  Only a
-    // tile that reaches past the wave's first query needs the causal mask:
-    // key kt0 + 16 sub + 4 lg + t is masked when 16 sub + t > lim.
-    auto scale_scores = [&](auto masked_tag) {
-      constexpr bool kMasked = decltype(masked_tag)::value;
-      const int lim = qpos - kt0 - 4 * lg;
-      float mx = -INFINITY;
+  // Pass 1: the exact maximum of the visible scores (order-free).
+  float m = -INFINITY;
+  load_keys(0);
+  for (int kt0 = 0; kt0 < key_end; kt0 += kKeyTile) {
+    if (kt0 > 0) __syncthreads();
+    store_keys();
+    __syncthreads();
+    if (kt0 + kKeyTile < key_end) load_keys(kt0 + kKeyTile);
+    floatx4 s[4];
+    tile_scores(s);
+    const bool masking = kt0 + kKeyTile - 1 > wave_first;
 #pragma unroll
-      for (int sub = 0; sub < 4; ++sub)
+    for (int sub = 0; sub < 4; ++sub)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          float v = s[sub][t] * a.scale;
-          if constexpr (kMasked) v = 16 * sub + t > lim ? -INFINITY : v;
-          s[sub][t] = v;
-          mx = fmaxf(mx, v);
-        }
-      return mx;
-    };
-    float tile_max = kt0 + kKeyTile - 1 > wave_first ? scale_scores(std::true_type{})
-                                                     : scale_scores(std::false_type{});
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-    // Key 0 is unmasked for every query, so m_new is finite from the first
-    // tile on: masked scores give exp(-inf) = 0, and the first alpha is 0.
-    const float m_new = fmaxf(m_run, tile_max);
-    const float alpha = __expf(m_run - m_new);
-    float row_sum = 0.0f;
+      for (int t = 0; t < 4; ++t)
+        if (!masking || visible(kt0, sub, t)) m = fmaxf(m, s[sub][t]);
+  }
+  // Key 0 is visible to every query, so m is finite.
+  m = fmaxf(m, __shfl_xor(m, 16));
+  m = fmaxf(m, __shfl_xor(m, 32));
+
+  // Pass 2: e = exp(s - m), the strided partials, and O^T += V^T E^T.
+  float part[8];  // partials 4 lg + t (t < 4) and 16 + 4 lg + (t - 4)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) part[i] = 0.0f;
+  __syncthreads();  // every wave is done with the last key tile of pass 1
+  load_keys(0);
+  load_values(0);
+  for (int kt0 = 0; kt0 < key_end; kt0 += kKeyTile) {
+    if (kt0 > 0) __syncthreads();
+    store_keys();
+    store_values(kt0);
+    __syncthreads();
+    if (kt0 + kKeyTile < key_end) {
+      load_keys(kt0 + kKeyTile);
+      load_values(kt0 + kKeyTile);
+    }
+    floatx4 s[4];
+    tile_scores(s);
+    const bool masking = kt0 + kKeyTile - 1 > wave_first;
+    // Partial (sub & 1, t) takes key 16 sub + 4 lg + t of sub 0, then 2
+    // (even) or 1, then 3 (odd): ascending keys within every partial.
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub)
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const float p = __expf(s[sub][t] - m_new);
-        s[sub][t] = p;
-        row_sum += p;
+        const float e = (!masking || visible(kt0, sub, t)) ? exp_nonpositive(s[sub][t] - m) : 0.0f;
+        s[sub][t] = e;
+        part[4 * (sub & 1) + t] = part[4 * (sub & 1) + t] + e;
       }
-    row_sum += __shfl_xor(row_sum, 16);
-    row_sum += __shfl_xor(row_sum, 32);
-    l_run = l_run * alpha + row_sum;
-    m_run = m_new;
-    // The running maximum rarely moves once a few tiles are in; multiplying
-    // by exactly 1 changes nothing, so the wave skips it then.
-    if (__ballot(alpha != 1.0f) != 0) {
-#pragma unroll
-      for (int d = 0; d < 8; ++d) o[d] *= alpha;
-    }
 
-    // O^T += V^T P^T, one 32-key K step per pair of 16-key blocks.
+    // O^T += V^T E^T, one 32-key K step per pair of 16-key blocks.
 #pragma unroll
     for (int ks = 0; ks < kKeyTile / 32; ++ks) {
       const float p[8] = {s[2 * ks][0], s[2 * ks][1], s[2 * ks][2], s[2 * ks][3],
                           s[2 * ks + 1][0], s[2 * ks + 1][1], s[2 * ks + 1][2], s[2 * ks + 1][3]};
-      // p = hi + mid + lo exactly: hi is p cut to its top 8 significant
+      // e = hi + mid + lo exactly: hi is e cut to its top 8 significant
       // bits, mid the residual cut the same way, and lo the rest, which has
       // at most 8 significant bits left; both subtractions are exact.  The
       // parts are the upper halves of the FP32 words, packed by byte permute.
@@ -638,7 +681,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3)
       const int k0 = 32 * ks + 4 * lg;  // keys k0..k0+3 and k0+16..k0+19 of the tile
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
-        const uint16_t* vrow = &Vt[(16 * d + lq) * kVRow];
+        const uint16_t* vrow = &Vs[(16 * d + lq) * kVRow];
         const uint2 va = *reinterpret_cast<const uint2*>(vrow + k0);
         const uint2 vb = *reinterpret_cast<const uint2*>(vrow + k0 + 16);
         const bf16x8 vt = as_bf16x8(u32x4{va.x, va.y, vb.x, vb.y});
@@ -649,6 +692,17 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3)
     }
   }
 
+  // The half tree: offset 16 in the lane, 8 across lane groups lg ^ 2, 4
+  // across lg ^ 1, then 2 and 1 in the lane (every lane ends with l).
+  float q4[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) q4[t] = part[t] + part[4 + t];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) q4[t] = q4[t] + __shfl_xor(q4[t], 32);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) q4[t] = q4[t] + __shfl_xor(q4[t], 16);
+  const float l = (q4[0] + q4[2]) + (q4[1] + q4[3]);
+
   const int row = q0 + qrow;
   if (row < a.rows) {
     uint16_t* dst = a.out + static_cast<uint64_t>(row) * qw;
@@ -657,7 +711,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3)
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const uint32_t feature = h * kHd + 16 * d + 4 * lg + t;
-        dst[permuted(feature, 16)] = dl_f32_to_bf16(o[d][t] / l_run);
+        dst[permuted(feature, 16)] = dl_f32_to_bf16(o[d][t] / l);
       }
   }
 }

@@ -4480,7 +4480,7 @@ static void copy_prefix_to_other_sequences(dl_plan* plan, uint32_t rows) {
   }
 }
 
-int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length) {
+int dl_plan_prefill_mfma(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length) {
   return guard([&] {
     require(plan && prompt, "null argument");
     dl::enter(plan->queue);
@@ -4627,7 +4627,7 @@ int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_lengt
 // position at 512 rows and 32 heads).
 constexpr uint32_t kExactChunk = 512;
 
-int dl_plan_prefill_exact(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length) {
+int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length) {
   return guard([&] {
     require(plan && prompt, "null argument");
     dl::enter(plan->queue);

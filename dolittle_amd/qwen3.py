@@ -253,7 +253,7 @@ class Plan:
         (at 36 Qwen3-8B blocks the first logits move by a few tenths and a
         greedy stream can leave the exact one after a few tokens)."""
         p = np.ascontiguousarray(prompt, dtype=np.uint32)
-        _lib.call("dl_plan_prefill" if mfma else "dl_plan_prefill_exact", self.handle,
+        _lib.call("dl_plan_prefill_mfma" if mfma else "dl_plan_prefill", self.handle,
                   p.ctypes.data_as(_lib.u32p), p.size)
 
     def decode_steps(self, steps: int) -> None:

@@ -8,17 +8,19 @@
   the north star's "greedy token streams identical for the first 64 tokens"
   at full size.
 - Config 3's 4096-id prompt at 2 blocks against the oracle: the exact
-  chunked prompt pass is bit-exact (caches, logits, tokens); the MFMA
-  prefill is held to the north star's logits bound (2e-2 absolute + 1e-2
-  relative, every logit), which it misses (an expected failure, below).
-- Config 3 at 36 blocks: the MFMA prefill's first logits against the
-  oracle-pinned exact pass, reported against the north star's bound and
-  asserted against the reference's own 36-block acceptance budget
+  chunked prompt pass is bit-exact (caches, logits, tokens).  The MFMA
+  prefill is as close to the exact pass as the exact pass with one-ulp flips
+  on 0.1% of block 0's cached K/V entries (the sensitivity floor), and both
+  miss the north star's logits bound (2e-2 absolute + 1e-2 relative, every
+  logit): an expected failure, kept below.
+- Config 3 at 36 blocks: the same floor comparison against the
+  oracle-pinned exact pass; the floor and the MFMA pass both exceed the
+  reference's own 36-block acceptance budget
   (scripts/validation/README.md:128-142: max |d| <= max(1e-4, peak / 16),
-  relative L2 <= 0.03), which it misses on relative L2 (an expected
-  failure); and greedy decode grown to 4608 keys, where the
-  exact prompt pass then 512 tokens equals consuming all 4096 prompt ids
-  through the loop (tokens, logits, caches of blocks 0, 24, 35).
+  relative L2 <= 0.03), an expected failure; and greedy decode grown to
+  4608 keys, where the exact prompt pass then 512 tokens equals consuming
+  all 4096 prompt ids through the loop (tokens, logits, caches of blocks 0,
+  24, 35).
 """
 import numpy as np
 import pytest
@@ -114,19 +116,76 @@ def test_config3_exact_prefill_4096_two_blocks_matches_oracle(two_blocks, config
         assert np.array_equal(k, wk) and np.array_equal(v, wv), layer
 
 
-# The MFMA prefill is the tolerance path and does not meet the north star's
-# logits bound on this synthetic model (measured on MI355X: 99.5% of the
-# 151,936 logits inside 2e-2 + 1e-2 |x| at 2 blocks, max |d| 0.047); the
-# assertion is kept as stated and the test is an expected failure: config 3's
-# parity path is the exact prompt pass
-# (test_config3_exact_prefill_4096_two_blocks_matches_oracle).  strict: a
-# pass would report as a failure, so a change that meets the bound shows.
-MFMA_MISSES_NORTH_STAR = pytest.mark.xfail(
-    strict=True, reason="MFMA accumulation order: the tolerance prefill misses the north star's logits bound; "
-                        "the exact prompt pass is config 3's parity path")
+def one_ulp_flips(bits, fraction, rng):
+    """bits with +-1 in the last place on a seeded random `fraction` of its
+    nonzero finite entries (never producing a zero, infinity or NaN)."""
+    out = bits.copy()
+    mag = out & 0x7FFF
+    candidates = np.nonzero((mag != 0) & (mag < 0x7F00))[0]
+    idx = candidates[rng.random(candidates.size) < fraction]
+    step = np.where(rng.random(idx.size) < 0.5, 1, -1)
+    out[idx] = (out[idx].astype(np.int64) + step).astype(np.uint16)
+    return out, idx.size
 
 
-@MFMA_MISSES_NORTH_STAR
+def exact_mfma_and_floor(model, p, fraction):
+    """First logits of config 3's prompt three ways: the exact pass, the
+    exact pass with one-ulp flips on `fraction` of block 0's cached K and V
+    entries (the floor), and the MFMA pass."""
+    from dolittle_amd.qwen3 import Plan
+    n = len(p) - 1
+
+    def first_logits(mfma=False, perturb=False):
+        plan = Plan(model, batch=1, capacity=len(p) + 2)
+        plan.prefill(p, mfma=mfma)
+        flipped = 0
+        if perturb:
+            k, v = plan.read_cache(0, 0, n)
+            rng = np.random.default_rng(7)
+            k2, fk = one_ulp_flips(k, fraction, rng)
+            v2, fv = one_ulp_flips(v, fraction, rng)
+            plan.write_cache(0, 0, k2, v2)
+            flipped = fk + fv
+        plan.generate(p, 1)
+        plan.collect()
+        return plan.logits(0), flipped
+
+    exact, _ = first_logits()
+    floor, flipped = first_logits(perturb=True)
+    mfma, _ = first_logits(mfma=True)
+    return exact, floor, flipped, mfma
+
+
+# The MFMA pass cannot meet the north star's logits bound or the reference's
+# 36-block budget on this synthetic model, and neither can any other path
+# that is not bit-exact: +-1 BF16 ulp on a handful of block 0's cached K/V
+# entries of the exact pass already moves the first logits outside both
+# (measured on MI355X with the prompts below: 9 flipped entries of 8.4
+# million give max |d| 0.041 and 99.75% of logits inside at 2 blocks, and
+# relative L2 0.039 at 36 blocks; 8,503 flips, 0.1%, give 0.047 / 98.8% and
+# 0.041).  The MFMA GEMMs flip about that fraction of every projection's
+# outputs.  The tests below assert that the bound cannot tell the MFMA pass
+# from a one-ulp perturbation of the exact pass, and keep the bounds
+# themselves as strict expected failures (a pass would report as a failure,
+# so a change that meets a bound shows).  Config 3's parity path is the exact
+# prompt pass (test_config3_exact_prefill_4096_two_blocks_matches_oracle).
+FLOOR_FRACTION = 1e-3
+
+
+@pytest.mark.timeout(900)
+def test_config3_mfma_prefill_within_the_one_ulp_floor_two_blocks(two_blocks, config3_oracle, oracle):
+    p, _, _, _, first_logits, _ = config3_oracle
+    exact, floor, flipped, mfma = exact_mfma_and_floor(two_blocks, p, FLOOR_FRACTION)
+    assert np.array_equal(exact, first_logits)  # the exact pass is the oracle's
+    f = logit_errors(floor, exact, oracle)
+    e = logit_errors(mfma, exact, oracle)
+    print(f"2 blocks, first logits vs the oracle: {flipped} one-ulp K/V flips in block 0 {f}; MFMA pass {e}")
+    assert flipped > 0 and f["north_star_frac"] < 1.0, f  # the floor already misses the bound
+    assert e["rel_l2"] <= 1.5 * f["rel_l2"] and e["max_abs"] <= 1.5 * f["max_abs"], (e, f)
+
+
+@pytest.mark.xfail(strict=True, reason="no path that is not bit-exact meets the north star's bound on this model: "
+                                       "one-ulp flips in block 0's cache of the exact pass already miss it")
 @pytest.mark.timeout(900)
 def test_config3_mfma_prefill_4096_two_blocks_north_star_bound(two_blocks, config3_oracle, oracle):
     from dolittle_amd.qwen3 import Plan
@@ -140,11 +199,18 @@ def test_config3_mfma_prefill_4096_two_blocks_north_star_bound(two_blocks, confi
     assert e["north_star_frac"] == 1.0, e
 
 
-# At 36 blocks (measured on MI355X: max |d| 0.25 within peak / 16 = 0.377,
-# relative L2 0.040 above 0.03) the MFMA prefill also misses the reference's
-# own 36-block acceptance budget; expected failure, assertion unchanged.
-@pytest.mark.xfail(strict=True, reason="MFMA prefill: relative L2 0.040 against the exact pass at 36 blocks "
-                                       "exceeds the reference's 0.03 budget")
+@pytest.mark.timeout(900)
+def test_config3_mfma_prefill_within_the_one_ulp_floor_full_depth(full_model, oracle):
+    exact, floor, flipped, mfma = exact_mfma_and_floor(full_model, prompt(4097, 4096), FLOOR_FRACTION)
+    f = logit_errors(floor, exact, oracle)
+    e = logit_errors(mfma, exact, oracle)
+    print(f"36 blocks, first logits vs the exact pass: {flipped} one-ulp K/V flips in block 0 {f}; MFMA pass {e}")
+    assert flipped > 0 and f["rel_l2"] > 0.03, f  # the floor already exceeds the reference's budget
+    assert e["rel_l2"] <= 1.5 * f["rel_l2"] and e["max_abs"] <= 1.5 * f["max_abs"], (e, f)
+
+
+@pytest.mark.xfail(strict=True, reason="no path that is not bit-exact meets the reference's 36-block budget on "
+                                       "this model: one-ulp flips in block 0's cache of the exact pass exceed it")
 @pytest.mark.timeout(900)
 def test_config3_mfma_prefill_full_depth_against_exact(full_model, oracle):
     from dolittle_amd.qwen3 import Plan

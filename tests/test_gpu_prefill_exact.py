@@ -1,4 +1,4 @@
-"""GPU checks of the exact chunked prompt pass (dl_plan_prefill_exact).
+"""GPU checks of the exact chunked prompt pass (dl_plan_prefill).
 
 The pass runs the prompt positions in chunks of up to 512 positions: the
 projections of a chunk of 16 positions or more as many-row exact GEMMs,
