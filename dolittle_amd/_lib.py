@@ -203,6 +203,25 @@ SIGNATURES = {
     "dl_plan_collect_event": [vp, u32, u64, cint, vp, C.POINTER(cint)],
     "dl_plan_event_count": [vp, u32, C.POINTER(u64)],
     "dl_plan_set_step_window": [vp, u32],
+    "dl_queue_transfer": [vp, vp, vp, u64],
+    "dl_sequence_device_bytes": [u64p],
+    "dl_sequence_host_bytes": [u64, u64, u64, u64p],
+    "dl_sequence_create": [vp, u64, u64, u64, cint, vpp],
+    "dl_sequence_destroy": [vp],
+    "dl_sequence_position_address": [vp, vpp],
+    "dl_sequence_begin": [vp, vp, vp, vp, u64, vp, u64, vp, vp, vp, vp],
+    "dl_sequence_begin_stage": [vp, cint],
+    "dl_sequence_end_stage": [vp],
+    "dl_sequence_begin_selection": [vp],
+    "dl_sequence_capture": [vp, vp, u64, vp, u64, u64, u64],
+    "dl_sequence_replace": [vp, vp, u64, vp, u64, u64, u64],
+    "dl_sequence_complete": [vp],
+    "dl_sequence_resources": [vp, u64p, u64p],
+    "dl_sequence_start": [vp],
+    "dl_sequence_request_stop": [vp],
+    "dl_sequence_drain": [vp],
+    "dl_sequence_collect": [vp, u64, cint, vp, C.POINTER(cint)],
+    "dl_sequence_event_count": [vp, u64p],
     "dl_plan_steps_enqueued": [vp, C.POINTER(u64)],
     "dl_plan_prefill": [vp, u32p, u32],
     "dl_plan_prefill_mfma": [vp, u32p, u32],

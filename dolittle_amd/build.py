@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libdlhip.so")
-SOURCES = ["runtime.cpp", "ops.hip", "packed.hip", "qwen3.hip", "sampler.hip", "prefill.hip", "nla.hip", "archive.cpp"]
+SOURCES = ["runtime.cpp", "ops.hip", "packed.hip", "qwen3.hip", "sampler.hip", "prefill.hip", "nla.hip", "sequence.hip", "archive.cpp"]
 ARCH = os.environ.get("DL_OFFLOAD_ARCH", "gfx950")
 
 

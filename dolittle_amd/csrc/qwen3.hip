@@ -3138,6 +3138,10 @@ int dl_qwen3_read_tensor(dl_qwen3* model, dl_queue* queue, int role, uint32_t la
 }  // extern "C"
 
 // ===================================================================== plan
+// Steps per window of the default bounded step window (at most 32 idle step
+// replays, ~20 ms on Qwen3-8B, after a stop).
+constexpr uint32_t kDefaultWindow = 16;
+
 struct dl_plan {
   dl_qwen3* model = nullptr;
   dl_queue* queue = nullptr;
@@ -3168,10 +3172,11 @@ struct dl_plan {
   dl::Publication* publication_host = nullptr;
   dl::Mirror* mirror_host = nullptr;
   dl::Event* events_host = nullptr;
-  // Bounded step window: 0 enqueues every step of a generation at once (the
-  // loop then completes without the host); n keeps at most 2n steps ahead of
-  // the device and enqueues no more once the loop has stopped.
-  uint32_t window = 0;
+  // Bounded step window: n (default kDefaultWindow) keeps at most 2n steps
+  // ahead of the device and enqueues no more once the loop has stopped, so a
+  // stop costs at most 2n idle step replays; 0 enqueues every step of a
+  // generation at once (the loop then completes without the host).
+  uint32_t window = kDefaultWindow;
   uint64_t steps_total = 0, steps_enqueued = 0;
   uint64_t cache_seq_stride = 0, cache_layer_stride = 0;
   hipGraph_t graphs[2] = {nullptr, nullptr};  // [0] long context, [1] short context
@@ -4401,7 +4406,8 @@ int dl_plan_collect_event(dl_plan* plan, uint32_t seq, uint64_t index, int wait,
         *ready = 1;
         return;
       }
-      if (!wait) return;
+      // An idle queue with nothing left to enqueue ends the journal, and a
+      // failed queue fails the wait, whether or not the caller blocks.
       const hipError_t q = hipStreamQuery(s);
       if (q == hipSuccess) {
         if (__atomic_load_n(&plan->publication_host[seq].completed, __ATOMIC_ACQUIRE) > index) continue;
@@ -4412,6 +4418,7 @@ int dl_plan_collect_event(dl_plan* plan, uint32_t seq, uint64_t index, int wait,
         plan->queue->device->poisoned = true;
         dl::check_hip(q, "generation");
       }
+      if (!wait) return;
       std::this_thread::sleep_for(std::chrono::microseconds(50));
     }
   });
@@ -4428,6 +4435,9 @@ int dl_plan_event_count(dl_plan* plan, uint32_t seq, uint64_t* count) {
 int dl_plan_set_step_window(dl_plan* plan, uint32_t steps) {
   return guard([&] {
     require(plan != nullptr, "null plan");
+    // A windowed generation that still has steps to enqueue keeps its window
+    // (switching to 0 would leave those steps unenqueued).
+    require(!pumping(plan), "step window change while a windowed generation is live");
     plan->window = steps;
   });
 }

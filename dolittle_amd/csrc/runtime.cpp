@@ -256,6 +256,15 @@ int dl_queue_read(dl_queue* queue, void* host, dl_buffer* src, uint64_t src_offs
   });
 }
 
+int dl_queue_transfer(dl_queue* queue, void* dst, const void* src, uint64_t bytes) {
+  return guard([&] {
+    dl::enter(queue);
+    require((dst != nullptr && src != nullptr) || bytes == 0, "null transfer address");
+    if (!bytes) return;
+    dl::check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, queue->stream), "transfer");
+  });
+}
+
 int dl_queue_mark(dl_queue* queue, uint64_t* point) {
   return guard([&] {
     dl::enter(queue);

@@ -105,6 +105,12 @@ int dl_queue_copy(dl_queue* queue, dl_buffer* dst, uint64_t dst_offset, dl_buffe
 int dl_queue_write(dl_queue* queue, dl_buffer* dst, uint64_t dst_offset, const void* host,
                    uint64_t bytes);
 int dl_queue_read(dl_queue* queue, void* host, dl_buffer* src, uint64_t src_offset, uint64_t bytes);
+/* Ordered copy between two addresses, each a device address (of a
+ * dl_buffer, or a device word the library hands out, such as the sampler's
+ * result) or the host address of a staging buffer: the transfer the
+ * reference's Queue::download / Queue::copy perform on any region, borrowed
+ * ones included (src/gpu/device.h:170-172).  Enqueues only. */
+int dl_queue_transfer(dl_queue* queue, void* dst, const void* src, uint64_t bytes);
 /* Completion points: mark returns a monotonically increasing point; wait
  * blocks until the queue reaches it and reports asynchronous failures. */
 int dl_queue_mark(dl_queue* queue, uint64_t* point);
@@ -535,24 +541,90 @@ typedef struct dl_sequence_event {
 /* DeviceSequence::collect (decoding/device.h:136; decode.cu:579-610): event
  * `index` of sequence `seq`.  With wait = 0 the call never blocks: *ready is
  * 1 and *event filled when the event is published, else *ready is 0.  With
- * wait != 0 it polls until the event is published, failing with
- * DL_RUNTIME_ERROR if the queue drains without it.  An index beyond the
+ * wait != 0 it polls until the event is published.  Either way a queue that
+ * has drained with nothing left to enqueue and without the event, or that
+ * has failed, is a DL_RUNTIME_ERROR.  An index beyond the
  * journal's capacity is a DL_LENGTH_ERROR. */
 int dl_plan_collect_event(dl_plan* plan, uint32_t seq, uint64_t index, int wait,
                           dl_sequence_event* event, int* ready);
 /* Events of sequence `seq` published so far (never blocks). */
 int dl_plan_event_count(dl_plan* plan, uint32_t seq, uint64_t* count);
 /* Bounded step window (no reference counterpart: HIP graphs have no
- * conditional nodes, so each step is a host-enqueued graph replay).  0, the
- * default, enqueues every step of a generation at once and the loop
- * completes with no further host call, as the reference's conditional graph
- * does; a stop leaves the remaining steps to replay as no-ops.  steps = n
- * keeps at most 2n steps enqueued ahead of the device: dl_plan_collect and
- * dl_plan_collect_event enqueue more while the loop is live and none after
- * it stopped, so a stopped loop replays at most 2n idle steps. */
+ * conditional nodes, so each step of the plan's loop is a host-enqueued
+ * graph replay).  steps = n, the default being 16, keeps at most 2n steps
+ * enqueued ahead of the device: dl_plan_collect and dl_plan_collect_event
+ * enqueue more while the loop is live and none after it stopped, so a
+ * stopped loop replays at most 2n idle steps (each a few hundred us on
+ * Qwen3-8B).  0 enqueues every step of a generation at once and the loop
+ * completes with no further host call; a stop then leaves the remaining
+ * steps to replay as no-ops.  A change while a windowed generation still has
+ * steps to enqueue is a DL_INVALID_ARGUMENT. */
 int dl_plan_set_step_window(dl_plan* plan, uint32_t steps);
 /* Diagnostic: steps enqueued since the current generation started. */
 int dl_plan_steps_enqueued(dl_plan* plan, uint64_t* steps);
+
+/* ------------------------------------------------------ device sequence */
+/* DeviceSequence (src/inference/decoding/device.h:84-137), the autonomous
+ * prepared sequence the reference records as one conditional CUDA graph
+ * (src/kernels/cuda/decode.cu).  HIP graphs have no conditional nodes, so
+ * what the caller submits to the queue between begin and complete is
+ * captured into one graph per segment: the set-up before the prompt, the
+ * full-chunk prompt body, the remainder body, the first selection, the
+ * decode forward, the decode selection tail and the terminal publication.
+ * Every decision the CUDA graph's conditional nodes take (repeat the prompt
+ * chunk, run the remainder, select, keep decoding) is taken by a device
+ * kernel from the same device words at the same point and published to
+ * host-mapped memory; a driver thread started by dl_sequence_start launches
+ * the segment each decision names, so each body runs exactly as often as
+ * the CUDA graph runs it and nothing runs speculatively.  Stages: 0 prefill,
+ * 1 tail, 2 first selection, 3 decode.  Events are dl_sequence_event. */
+typedef struct dl_sequence dl_sequence;
+/* DeviceSequence::device_bytes / host_bytes (device.h:102-103). */
+int dl_sequence_device_bytes(uint64_t* bytes);
+int dl_sequence_host_bytes(uint64_t prompt, uint64_t generated, uint64_t chunk, uint64_t* bytes);
+/* Constructor with its Shape (device.h:91-96). */
+int dl_sequence_create(dl_queue* queue, uint64_t prompt, uint64_t generated, uint64_t chunk, int forward_only,
+                       dl_sequence** out);
+/* Destructor: requests a stop, ends a partial capture, joins the driver and
+ * drains the queue before freeing. */
+int dl_sequence_destroy(dl_sequence* sequence);
+/* DeviceSequence::position (device.h:104): device address of the uint64
+ * position that recorded bodies read. */
+int dl_sequence_position_address(dl_sequence* sequence, void** out);
+/* DeviceSequence::begin (device.h:105-110): device addresses of the
+ * sampler's {token, status} and terminal words (null, forward-only), the
+ * token-input rows of the recipe, the uploaded prompt, and the optional
+ * injection {status, norm} and intervention {status, count} words. */
+int dl_sequence_begin(dl_sequence* sequence, const uint32_t* selection, const uint32_t* terminal,
+                      uint32_t* token_input, uint64_t token_input_bytes, const uint32_t* prompt,
+                      uint64_t prompt_bytes, const uint32_t* injection_status, const float* injection_norm,
+                      const uint32_t* intervention_status, const uint32_t* intervention_count);
+/* begin_stage / end_stage / begin_selection (device.h:111-114). */
+int dl_sequence_begin_stage(dl_sequence* sequence, int stage);
+int dl_sequence_end_stage(dl_sequence* sequence);
+int dl_sequence_begin_selection(dl_sequence* sequence);
+/* capture (device.h:115-116): `rows` rows of `source` copied into the arena
+ * `destination` (prompt + generated rows) at the device position. */
+int dl_sequence_capture(dl_sequence* sequence, const void* source, uint64_t source_bytes, void* destination,
+                        uint64_t destination_bytes, uint64_t row_bytes, uint64_t rows);
+/* replace (device.h:117-118): prompt position `marker`'s embedding row
+ * replaced by `row` in the body that holds it. */
+int dl_sequence_replace(dl_sequence* sequence, const void* row, uint64_t row_bytes, void* embeddings,
+                        uint64_t embeddings_bytes, uint64_t marker, uint64_t rows);
+/* complete (device.h:119) and prepared_resources (device.h:124). */
+int dl_sequence_complete(dl_sequence* sequence);
+int dl_sequence_resources(dl_sequence* sequence, uint64_t* device_bytes, uint64_t* host_bytes);
+/* start / request_stop / drain (device.h:125-127).  request_stop may run on
+ * any thread; drain joins the driver and reports its failure. */
+int dl_sequence_start(dl_sequence* sequence);
+int dl_sequence_request_stop(dl_sequence* sequence);
+int dl_sequence_drain(dl_sequence* sequence);
+/* collect (device.h:128; decode.cu:579-600): event `index`.  wait = 0 never
+ * blocks (*ready 0 until published); either way a sequence that ended
+ * without the event, or whose stream failed, is a DL_RUNTIME_ERROR, and an
+ * index past the journal's P + 2G + 2 events a DL_LENGTH_ERROR. */
+int dl_sequence_collect(dl_sequence* sequence, uint64_t index, int wait, dl_sequence_event* event, int* ready);
+int dl_sequence_event_count(dl_sequence* sequence, uint64_t* count);
 
 /* ------------------------------------------ NLA injection and steering */
 /* DeviceInjection (src/inference/injection/device.h:29-47; kernel

@@ -1,9 +1,23 @@
 """The reference-side adapter (integration/hip_backend.cpp) compiled against
-the reference's own headers and linked against libdlhip.so: the classes of
-src/gpu/device.h:73-184 and src/inference/sampling/device.h:54-85 and
-DeviceSequence's event type (src/inference/decoding/device.h:84-137) are
-implemented on the C ABI with nothing left undefined.  Compile and link
-only; skipped where the reference tree is absent."""
+the reference's own headers and linked against libdlhip.so:
+
+- alone, with -Wall -Wextra -Werror and nothing left undefined: the classes
+  of src/gpu/device.h:73-184, the operation catalog's prepare and
+  PreparedOperation (src/kernels/operations.h:204-271), DeviceCategorical
+  (src/inference/sampling/device.h:54-85), DeviceSequence
+  (src/inference/decoding/device.h:84-137), DeviceInjection
+  (src/inference/injection/device.h:26-47) and DeviceDirection /
+  DeviceIntervention (src/inference/steering/device.h:30-68) are implemented
+  on the C ABI;
+- together with the reference's own executor.cpp, generation.cpp,
+  kernels/operations.cpp, models/qwen3/model.cpp, cache/contiguous.cpp and
+  storage_plan.cpp (and the host sources they call: tensors, model,
+  observations, categorical, progression), compiled where they lie, into
+  one shared object with -Wl,--no-undefined: every backend symbol the
+  reference's inference path calls resolves to the adapter or libdlhip.so
+  (integration/Makefile `link`).
+Compile and link only (tests/test_gpu_adapter.py runs the adapter on the
+GPU); skipped where the reference tree is absent."""
 import os
 import shutil
 import subprocess
@@ -28,8 +42,8 @@ def adapter(tmp_path_factory):
     out = str(tmp_path_factory.mktemp("adapter") / "libdolittle_hip_backend.so")
     cmd = [gxx, "-std=c++20", "-O1", "-Wall", "-Wextra", "-Werror", "-fPIC", "-shared", f"-I{REFERENCE}",
            f"-I{os.path.join(ROOT, 'include')}", os.path.join(ROOT, "integration", "hip_backend.cpp"),
-           f"-L{os.path.dirname(LIB)}", "-ldlhip", "-Wl,--no-undefined", "-Wl,-rpath-link,/opt/rocm/lib",
-           "-o", out]
+           f"-L{os.path.dirname(LIB)}", "-ldlhip", "-Wl,-rpath-link,/opt/rocm/lib",
+           "-Wl,--unresolved-symbols=ignore-in-object-files", "-o", out]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stderr[-4000:]
     return out
@@ -40,8 +54,34 @@ def defined_symbols(path):
     return r.stdout
 
 
-def test_adapter_links_with_nothing_undefined(adapter):
-    assert os.path.getsize(adapter) > 0
+def undefined_symbols(path):
+    r = subprocess.run(["nm", "-DC", "--undefined-only", path], capture_output=True, text=True, check=True)
+    return r.stdout
+
+
+def test_adapter_compiles_warning_free_and_needs_only_reference_host_code(adapter):
+    """Alone, the adapter leaves undefined only the reference's own
+    backend-independent host functions it calls (validate_operation and the
+    tensor layout helpers), which the reference tree defines."""
+    missing = [line.split(None, 1)[-1] for line in undefined_symbols(adapter).splitlines() if "dolittle::" in line]
+    allowed = ("dolittle::kernels::validate_operation", "dolittle::tensors::element_bytes",
+               "dolittle::tensors::required_bytes")
+    assert all(m.startswith(allowed) for m in missing), missing
+
+
+@pytest.mark.timeout(600)
+def test_reference_executor_links_against_the_adapter_with_nothing_undefined():
+    if not os.path.exists(LIB):
+        pytest.skip("libdlhip.so not built")
+    r = subprocess.run(["make", "-s", "-B", "-C", os.path.join(ROOT, "integration"), "link"], capture_output=True,
+                       text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-6000:]
+    linked = os.path.join(ROOT, "integration", "_build", "libdolittle_reference_hip.so")
+    symbols = defined_symbols(linked)
+    for member in ("dolittle::inference::CachedForwardPlan::prepare_device_generation",
+                   "dolittle::inference::generate", "dolittle::kernels::prepare(",
+                   "dolittle::inference::DeviceSequence::collect"):
+        assert member in symbols, member
 
 
 @pytest.mark.parametrize("symbol", [
@@ -54,12 +94,43 @@ def test_adapter_links_with_nothing_undefined(adapter):
     "dolittle::gpu::DeviceBuffer::size_bytes() const",
     "dolittle::gpu::HostBuffer::bytes()",
     "dolittle::gpu::hip::open_device(int)",
+    "dolittle::kernels::prepare(",
+    "dolittle::kernels::PreparedOperation::workspace() const",
+    "dolittle::kernels::PreparedOperation::initialize(",
+    "dolittle::kernels::PreparedOperation::operands() const",
+    "dolittle::kernels::PreparedOperation::implementation_name() const",
+    "dolittle::kernels::PreparedOperation::submit(",
     "dolittle::inference::sampling::DeviceCategorical::required_bytes(unsigned long)",
     "dolittle::inference::sampling::DeviceCategorical::submit_next(dolittle::gpu::ConstDeviceRegion)",
     "dolittle::inference::sampling::DeviceCategorical::start(",
     "dolittle::inference::sampling::DeviceCategorical::result_storage() const",
     "dolittle::inference::sampling::DeviceCategorical::terminal_state() const",
     "dolittle::inference::sampling::DeviceCategorical::current_token() const",
+    "dolittle::inference::DeviceSequence::DeviceSequence(",
+    "dolittle::inference::DeviceSequence::device_bytes()",
+    "dolittle::inference::DeviceSequence::host_bytes(",
+    "dolittle::inference::DeviceSequence::position() const",
+    "dolittle::inference::DeviceSequence::begin(",
+    "dolittle::inference::DeviceSequence::begin_stage(",
+    "dolittle::inference::DeviceSequence::end_stage()",
+    "dolittle::inference::DeviceSequence::begin_selection()",
+    "dolittle::inference::DeviceSequence::capture(",
+    "dolittle::inference::DeviceSequence::replace(",
+    "dolittle::inference::DeviceSequence::complete()",
+    "dolittle::inference::DeviceSequence::prepared_resources() const",
+    "dolittle::inference::DeviceSequence::start()",
+    "dolittle::inference::DeviceSequence::request_stop()",
+    "dolittle::inference::DeviceSequence::drain()",
+    "dolittle::inference::DeviceSequence::collect(",
+    "dolittle::inference::DeviceInjection::DeviceInjection(",
+    "dolittle::inference::DeviceInjection::submit()",
+    "dolittle::inference::DeviceInjection::required_bytes(",
+    "dolittle::inference::DeviceDirection::DeviceDirection(",
+    "dolittle::inference::DeviceDirection::submit()",
+    "dolittle::inference::DeviceDirection::finish()",
+    "dolittle::inference::DeviceIntervention::DeviceIntervention(",
+    "dolittle::inference::DeviceIntervention::initialize()",
+    "dolittle::inference::DeviceIntervention::submit(",
     "dolittle::inference::hip::collect(dl_plan*, unsigned int, unsigned long, std::stop_token const&)",
 ])
 def test_adapter_defines_the_reference_members(adapter, symbol):
