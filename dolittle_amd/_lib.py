@@ -204,6 +204,7 @@ SIGNATURES = {
     "dl_plan_event_count": [vp, u32, C.POINTER(u64)],
     "dl_plan_set_step_window": [vp, u32],
     "dl_queue_transfer": [vp, vp, vp, u64],
+    "dl_plan_device_bytes": [vp, u64p],
     "dl_sequence_device_bytes": [u64p],
     "dl_sequence_host_bytes": [u64, u64, u64, u64p],
     "dl_sequence_create": [vp, u64, u64, u64, cint, vpp],

@@ -3149,6 +3149,7 @@ struct dl_plan {
   int head_blocks = 256;
   uint64_t compute_units = 256;  // queried at creation
   std::vector<void*> allocations;
+  std::vector<uint64_t> allocation_bytes;
   dl::Control* ctl = nullptr;
   dl::Control* bench_ctl = nullptr;
   uint16_t *h = nullptr, *q_raw = nullptr, *k_raw = nullptr, *att = nullptr, *act = nullptr, *logits = nullptr;
@@ -3236,13 +3237,15 @@ struct dl_plan {
              *att = nullptr, *act = nullptr;
     uint32_t rows = 0;  // allocated rows (multiple of 128)
   } pf;
-  // Exact chunked prompt pass: row buffers for kExactChunk consecutive
-  // positions of one sequence and the chunk's control (first use).
+  // Exact chunked prompt pass: row buffers for `rows` consecutive positions
+  // of one sequence (the longest chunk a pass has needed so far, at most
+  // kExactChunk) and the chunk's control.
   struct Chunk {
     uint16_t *h = nullptr, *q = nullptr, *k = nullptr, *att = nullptr, *act = nullptr, *x16 = nullptr,
              *x32 = nullptr;
     float *scores = nullptr, *probs = nullptr;
     dl::Control* ctl = nullptr;
+    uint32_t rows = 0;
   } ex;
   std::vector<uint32_t> prefilled_prompt;
   uint32_t prefilled = 0;
@@ -3257,7 +3260,24 @@ struct dl_plan {
       dl::fail(DL_LENGTH_ERROR, std::string("plan allocation failed: ") + hipGetErrorString(e));
     }
     allocations.push_back(p);
+    allocation_bytes.push_back(count * sizeof(T));
     return static_cast<T*>(p);
+  }
+  // Frees one allocation of this plan (the stream must be idle).
+  void release(void* p) {
+    for (size_t i = 0; i < allocations.size(); ++i) {
+      if (allocations[i] == p) {
+        (void)hipFree(p);
+        allocations.erase(allocations.begin() + static_cast<long>(i));
+        allocation_bytes.erase(allocation_bytes.begin() + static_cast<long>(i));
+        return;
+      }
+    }
+  }
+  uint64_t device_bytes() const {
+    uint64_t total = 0;
+    for (uint64_t b : allocation_bytes) total += b;
+    return total;
   }
 
   ~dl_plan() {
@@ -4216,6 +4236,13 @@ int dl_plan_read_cache(dl_plan* plan, uint32_t seq, uint32_t layer, uint64_t fir
   return cache_transfer(plan, seq, layer, first_position, count, keys, values, true);
 }
 
+int dl_plan_device_bytes(dl_plan* plan, uint64_t* bytes) {
+  return guard([&] {
+    require(plan && bytes, "null argument");
+    *bytes = plan->device_bytes();
+  });
+}
+
 int dl_plan_seek(dl_plan* plan, uint64_t position) {
   return guard([&] {
     require(plan != nullptr, "null plan");
@@ -4625,16 +4652,16 @@ int dl_plan_prefill_mfma(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_
 }
 
 // The exact prompt pass: positions [0, prompt_length - 1) in chunks of up to
-// kMaxBatch consecutive positions through the decode kernels, rows = positions
-// (StepRows with pos_step 1).  Every projection row is the same FMA chain as
-// a single-position step, the chunk's keys are in the cache before its
+// kExactChunk consecutive positions through the decode kernels, rows =
+// positions (StepRows with pos_step 1).  Every projection row is the same FMA
+// chain as a single-position step (many-row exact GEMMs from 16 rows, each
+// weight read once per chunk), the chunk's keys are in the cache before its
 // attention, and each row attends to keys [0, its position], so the caches
-// are bit-identical to consuming the prompt one position per step.
-// Consecutive prompt positions per step of the exact chunked prompt pass:
-// their projections run as many-row exact GEMMs (each weight read once per
-// chunk), their attention row by row.  The chunk's score and probability
-// rows take kExactChunk x q_heads x capacity floats each (128 KiB per cache
-// position at 512 rows and 32 heads).
+// are bit-identical to consuming the prompt one position per step.  The
+// chunk's score and probability rows take rows x q_heads x capacity floats
+// each: 64 KiB each per cache position at 512 rows and 32 heads, sized to
+// the longest chunk a pass has needed (at most kExactChunk rows) and counted
+// by dl_plan_device_bytes.
 constexpr uint32_t kExactChunk = 512;
 
 int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_length) {
@@ -4658,7 +4685,15 @@ int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_lengt
     const uint64_t D = c.hidden, QW = uint64_t(c.q_heads) * c.head_dim, KW = uint64_t(c.kv_heads) * c.head_dim,
                    F = c.ffn, R = kExactChunk;
     auto& ex = plan->ex;
-    if (!ex.ctl) {
+    const uint32_t need = std::min<uint32_t>(kExactChunk, rows);
+    if (ex.rows < need) {
+      for (void* old : {static_cast<void*>(ex.h), static_cast<void*>(ex.q), static_cast<void*>(ex.k),
+                        static_cast<void*>(ex.att), static_cast<void*>(ex.act), static_cast<void*>(ex.x16),
+                        static_cast<void*>(ex.x32), static_cast<void*>(ex.scores), static_cast<void*>(ex.probs),
+                        static_cast<void*>(ex.ctl)})
+        if (old) plan->release(old);
+      ex = {};
+      const uint64_t R = need;
       ex.h = plan->alloc<uint16_t>(R * D);
       ex.q = plan->alloc<uint16_t>(R * QW);
       ex.k = plan->alloc<uint16_t>(R * KW);
@@ -4669,6 +4704,7 @@ int dl_plan_prefill(dl_plan* plan, const uint32_t* prompt, uint32_t prompt_lengt
       ex.scores = plan->alloc<float>(R * c.q_heads * plan->cap);
       ex.probs = plan->alloc<float>(R * c.q_heads * plan->cap);
       ex.ctl = plan->alloc<dl::Control>(1);
+      ex.rows = need;
     }
     dl::check_hip(hipMemcpyAsync(plan->tokens, prompt, prompt_length * 4ull, hipMemcpyHostToDevice, s), "prompt");
     const bool per_sequence = sequences_differ(plan);

@@ -123,6 +123,11 @@ class Plan:
         a = np.ascontiguousarray(tokens, dtype=np.uint32)
         _lib.call("dl_plan_forward", self.handle, a.ctypes.data_as(_lib.u32p), a.size)
 
+    def device_bytes(self) -> int:
+        out = C.c_uint64(0)
+        _lib.call("dl_plan_device_bytes", self.handle, C.byref(out))
+        return out.value
+
     def seek(self, position: int) -> None:
         _lib.call("dl_plan_seek", self.handle, position)
 

@@ -385,6 +385,10 @@ int dl_plan_write_cache(dl_plan* plan, uint32_t seq, uint32_t layer, uint64_t fi
 /* Reads the same rows back in the reference layout. */
 int dl_plan_read_cache(dl_plan* plan, uint32_t seq, uint32_t layer, uint64_t first_position,
                        uint64_t count, uint16_t* keys, uint16_t* values);
+/* Device bytes the plan holds (KV caches, scores, row buffers, the prompt
+ * passes' scratch once a pass has run; the model's weights are
+ * dl_qwen3_resident_bytes). */
+int dl_plan_device_bytes(dl_plan* plan, uint64_t* bytes);
 /* Moves the plan to `position`: rows below it are treated as cached. */
 int dl_plan_seek(dl_plan* plan, uint64_t position);
 /* Residual row of sequence `seq` after the last consumed position (the

@@ -188,3 +188,39 @@ def test_wrapped_ranges_are_length_errors(model2):
     plan.prefill([1, 2, 3, 4, 5])
     with pytest.raises(_lib.LengthError):
         _lib.call("dl_plan_read_prefill_hidden", plan.handle, huge, 4, ptr)
+
+
+def test_scratch_follows_the_longest_chunk_and_is_counted(model1):
+    """The pass's row buffers and score/probability rows are sized to the
+    longest chunk a pass has needed (at most 512 rows), not to 512 rows up
+    front, and dl_plan_device_bytes counts them; a shorter pass after a
+    longer one reuses the larger buffers and stays bit-exact."""
+    from dolittle_amd.qwen3 import Plan
+    cfg = model1.config
+    cap = 640
+    plan = Plan(model1, batch=1, capacity=cap)
+    base = plan.device_bytes()
+    rng = np.random.default_rng(77)
+    short = [int(t) for t in rng.integers(0, cfg.vocab, 10)]
+    long = [int(t) for t in rng.integers(0, cfg.vocab, 600)]
+    qw, kw = cfg.q_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+
+    def scratch(rows):
+        per_row = 2 * (3 * cfg.hidden + 2 * qw + kw + cfg.ffn) + 2 * 4 * cfg.q_heads * cap
+        return rows * per_row
+
+    plan.prefill(short)
+    grown = plan.device_bytes() - base
+    assert scratch(9) <= grown <= scratch(9) + 4096, (grown, scratch(9))
+    plan.prefill(long)
+    grown = plan.device_bytes() - base
+    assert scratch(512) <= grown <= scratch(512) + 4096, (grown, scratch(512))
+    plan.prefill(short)
+    assert plan.device_bytes() - base == grown
+    plan.generate(short, 4)
+    tokens, _ = plan.collect()
+    loop = Plan(model1, batch=1, capacity=cap)
+    loop.generate(short, 4)
+    want, _ = loop.collect()
+    assert tokens.tolist() == want.tolist()
+    assert np.array_equal(plan.logits(0), loop.logits(0))
