@@ -21,6 +21,14 @@
   4608 keys, where the exact prompt pass then 512 tokens equals consuming
   all 4096 prompt ids through the loop (tokens, logits, caches of blocks 0,
   24, 35).
+- Config 4 at 36 blocks with its 256-id prompt (16 tokens): batch 2,
+  block-24 capture at every position, sequence 1 steered there by the unit
+  vector times 8; tokens, all 272 captured rows and the last logits of both
+  sequences bit-exact with the oracle.
+- Config 5 at 36 blocks with its 192-id prefix (8 tokens per sample): the
+  x40 injected embedding slot, batch 8, top-p 0.95; the first selection's
+  logits bit-exact with the oracle for every sample and every sampled id
+  equal to the host law on that step's device logits.
 """
 import numpy as np
 import pytest
@@ -44,8 +52,15 @@ def full_model(device, queue):
     return model
 
 
+@pytest.fixture(scope="module")
+def full_weights(full_model, oracle):
+    """The 36-block model's weights read back into the oracle's layout
+    (checked against the seeded generator)."""
+    return read_weights(oracle, full_model, seed=SEED)
+
+
 @pytest.mark.timeout(900)
-def test_config2_full_depth_matches_oracle(full_model, oracle):
+def test_config2_full_depth_matches_oracle(full_model, full_weights, oracle):
     from dolittle_amd.qwen3 import Plan
     p, new = prompt(128, 128), 64
     loop = Plan(full_model, batch=1, capacity=len(p) + new + 1)
@@ -58,8 +73,7 @@ def test_config2_full_depth_matches_oracle(full_model, oracle):
     pre_tokens, pre_results = pre.collect()
     assert pre_results[0]["generated"] == new and pre_results[0]["status"] == 0
 
-    w = read_weights(oracle, full_model, seed=SEED)
-    run = OracleLoop(oracle, w, len(p) + new + 1)
+    run = OracleLoop(oracle, full_weights, len(p) + new + 1)
     want_tokens, want_logits = run.generate(p, new)
     assert loop_tokens[0].tolist() == want_tokens
     assert np.array_equal(loop.logits(0), want_logits)
@@ -248,3 +262,120 @@ def test_config3_decode_to_4608_keys_exact_prefill_equals_loop(full_model):
         k0, v0 = loop.read_cache(layer, 0, len(p) + new - 1)
         k1, v1 = pre.read_cache(layer, 0, len(p) + new - 1)
         assert np.array_equal(k0, k1) and np.array_equal(v0, v1), layer
+
+
+@pytest.mark.timeout(900)
+def test_config4_full_depth_capture_and_steering_match_oracle(full_model, full_weights, oracle):
+    """BASELINE config 4 at its depth and prompt, reduced generation: 36
+    blocks, batch 2, a 256-id prompt through the exact prompt pass, block-24
+    capture at every consumed position, sequence 1 steered there at every
+    position by a seeded N(0,1) FP32 vector normalised to unit length times
+    8.0 (h <- BF16(FP32(h) + v)), 16 greedy tokens.  Tokens, the 272 captured
+    rows of both sequences and their last logits equal the oracle's."""
+    from dolittle_amd.qwen3 import Plan
+    w, d = full_weights, full_weights.dims
+    p, new, layer = prompt(4104, 256), 16, 24
+    rng = np.random.default_rng(4105)
+    v = rng.standard_normal(d.hidden).astype(np.float32)
+    v = (v / np.float32(np.linalg.norm(v.astype(np.float64)))).astype(np.float32) * np.float32(8.0)
+    plan = Plan(full_model, batch=2, capacity=len(p) + new + 1)
+    plan.set_capture(layer)
+    plan.set_steering(1, layer, v)
+    plan.prefill(p)
+    plan.generate(p, new)
+    tokens, results = plan.collect()
+    consumed = len(p) + new
+    print(f"config 4: GPU done, {results}", flush=True)
+
+    # Oracle: blocks 0..24 of the 255 prompt rows are shared; sequence 1 is
+    # steered after block 24 and both continue through blocks 25..35.
+    kw, cap, rows = d.kv_heads * d.head_dim, consumed + 1, len(p) - 1
+    emb = w.embedding.reshape(d.vocab, d.hidden)
+    caches = [([np.zeros(cap * kw, np.uint16) for _ in w.blocks], [np.zeros(cap * kw, np.uint16) for _ in w.blocks])
+              for _ in range(2)]
+    h = np.ascontiguousarray(emb[np.asarray(p[:-1], np.int64)].reshape(-1))
+    for l in range(layer + 1):
+        oracle.block_forward(w, l, h, rows, 0, caches[0][0][l], caches[0][1][l])
+    hs = [h, h.copy()]
+    for l in range(layer + 1):
+        caches[1][0][l][:] = caches[0][0][l]
+        caches[1][1][l][:] = caches[0][1][l]
+    for r in range(rows):
+        oracle.steer(hs[1][r * d.hidden:(r + 1) * d.hidden], v)
+    captures = [hs[0].reshape(rows, d.hidden).copy(), hs[1].reshape(rows, d.hidden).copy()]
+    for seq in (0, 1):
+        for l in range(layer + 1, len(w.blocks)):
+            oracle.block_forward(w, l, hs[seq], rows, 0, caches[seq][0][l], caches[seq][1][l])
+    print("config 4: oracle prompt done", flush=True)
+    for seq in (0, 1):
+        stream, caps, logits = list(p), [captures[seq]], None
+        for pos in range(rows, consumed):
+            x = emb[stream[pos]].copy()
+            for l in range(len(w.blocks)):
+                oracle.block_forward(w, l, x, 1, pos, caches[seq][0][l], caches[seq][1][l])
+                if l == layer:
+                    if seq == 1:
+                        oracle.steer(x, v)
+                    caps.append(x.reshape(1, d.hidden).copy())
+            if pos + 1 < consumed:
+                logits = oracle.logits(w, x)
+                status, nxt = oracle.greedy(logits)
+                assert status == 0
+                stream.append(nxt)
+        assert results[seq]["generated"] == new and results[seq]["status"] == 0
+        assert tokens[seq].tolist() == stream[len(p):], seq
+        assert np.array_equal(plan.read_capture(seq, 0, consumed), np.concatenate(caps)), seq
+        assert np.array_equal(plan.logits(seq), logits), seq
+    assert tokens[0].tolist() != tokens[1].tolist()
+
+
+@pytest.mark.timeout(900)
+def test_config5_full_depth_injected_prefix_and_top_p_follow_the_law(full_model, full_weights, oracle):
+    """BASELINE config 5 at its depth, batch and prefix, reduced generation:
+    36 blocks, 8 samples sharing a 192-id prefix (exact prompt pass) whose
+    embedding slot 57 is replaced by a BF16 N(0,1) x 40 row, then 8 tokens
+    per sample at T 1.0, top-p 0.95 with per-sample MT19937-64 seeds.  The
+    first selection's logits of every sample equal the oracle's (36 blocks
+    over the injected prefix), and every sampled id equals the host law
+    (categorical.cpp:146-201) applied to that step's device logits with the
+    sample's k-th draw."""
+    from dolittle_amd.qwen3 import Plan, SamplingSettings
+    w, d = full_weights, full_weights.dims
+    p, new, slot = prompt(4106, 192), 8, 57
+    row = oracle.normal_bf16(d.hidden, SEED + 11, 3000, 40.0)
+    seeds = [1000 + 17 * b for b in range(8)]
+    settings = SamplingSettings("categorical", 1.0, 0, 0.95)
+    plan = Plan(full_model, batch=8, capacity=len(p) + new + 1)
+    plan.set_embedding_override(slot, row, 0xFF)
+    plan.prefill(p)
+    plan.prepare_generation(p, new, settings, seeds)
+    plan.decode_steps(1)  # consumes the last prefix position, selects token 0
+    logits = []
+    for step in range(new):
+        logits.append([plan.logits(b) for b in range(8)])
+        plan.decode_steps(1)
+    tokens, results = plan.collect()
+    print(f"config 5: GPU done, {[r['generated'] for r in results]}", flush=True)
+
+    emb = w.embedding.reshape(d.vocab, d.hidden)
+    kw, cap, rows = d.kv_heads * d.head_dim, len(p) + 1, len(p) - 1
+    h = np.ascontiguousarray(emb[np.asarray(p[:-1], np.int64)])
+    h[slot] = row
+    h = h.reshape(-1)
+    k = [np.zeros(cap * kw, np.uint16) for _ in w.blocks]
+    vv = [np.zeros(cap * kw, np.uint16) for _ in w.blocks]
+    for l in range(len(w.blocks)):
+        oracle.block_forward(w, l, h, rows, 0, k[l], vv[l])
+    x = emb[p[-1]].copy()
+    for l in range(len(w.blocks)):
+        oracle.block_forward(w, l, x, 1, rows, k[l], vv[l])
+    first = oracle.logits(w, x)
+    for b in range(8):
+        assert np.array_equal(logits[0][b], first), b
+    for b in range(8):
+        assert results[b]["generated"] == new and results[b]["status"] == 0, results[b]
+        draws = oracle.MT19937_64(seeds[b])
+        for i in range(new):
+            status, want = oracle.categorical_bits(oracle.f32_from_bf16(logits[i][b]), 1, 1.0, 0, 0.95, draws())
+            assert status == 0 and tokens[b][i] == want, (b, i)
+    assert len({tuple(t) for t in tokens.tolist()}) > 1
