@@ -239,3 +239,33 @@ def test_prefilled_positions_open_the_journal(small_model):
                          "norm": 0.0}
     _, term = check_journal(events, len(p), tokens[0].tolist())
     assert REASONS[term["status"]] == "limit" and term["position"] == len(p) + new
+
+
+def test_an_index_past_the_terminal_event_fails_instead_of_waiting(small_model):
+    """decode.cu:579-600: a sequence that ended without the asked event is an
+    error, for the non-blocking read as for the blocking one."""
+    from dolittle_amd import DeviceError
+    from dolittle_amd.qwen3 import Plan
+    plan = Plan(small_model, batch=1, capacity=32)
+    plan.generate([1, 2, 3], 4)
+    plan.collect()
+    events = plan.events(0)
+    assert events[-1]["kind"] == "terminal"
+    for wait in (False, True):
+        with pytest.raises(DeviceError, match="ended without event"):
+            plan.collect_event(0, len(events), wait=wait)
+
+
+def test_window_change_is_rejected_while_a_windowed_generation_is_live(small_model):
+    """Switching the window to 0 mid-run would leave the remaining steps
+    unenqueued: the plan refuses it until the generation has ended."""
+    from dolittle_amd import InvalidArgument
+    from dolittle_amd.qwen3 import Plan
+    plan = Plan(small_model, batch=1, capacity=256)
+    plan.set_step_window(2)
+    plan.generate([1, 2, 3], 200)
+    with pytest.raises(InvalidArgument):
+        plan.set_step_window(0)
+    tokens, results = plan.collect()
+    assert results[0]["generated"] == 200 and results[0]["reason"] == "limit"
+    plan.set_step_window(0)  # the generation has ended
