@@ -1392,11 +1392,61 @@ __device__ __forceinline__ void handoff_raise(const Handoff& hs, int go) {
     __hip_atomic_store(handoff_line(hs, go + x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Tagged hand-off words: each 64-bit word carries two BF16 values in its low
+// half and the writing launch's tag in its high half, stored and loaded as
+// one naturally aligned 64-bit atomic (single-copy atomic, device-coherent:
+// `global_store_dwordx2 ... sc1` / `global_load_dwordx2 ... sc1`).  A reader
+// polls its own words until every tag is the launch's, so it needs neither
+// the writer's store acknowledgements nor a counter or a go flag: the values
+// are in the word that tells it they are current.  The tag is the launch's
+// epoch + 1; the epoch word is advanced once per live launch by its last
+// workgroup, so a word left over from any earlier launch carries another tag.
+struct Tagged {
+  uint64_t* words;
+  uint32_t tag;
+  int k, v, att;  // word offsets of the k row, the new v row and the attention output (q at 0)
+};
+
+__device__ __forceinline__ void tagged_put(uint64_t* w, uint32_t data, uint32_t tag) {
+  __hip_atomic_store(w, static_cast<uint64_t>(data) | (static_cast<uint64_t>(tag) << 32), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Reads the N words src[k] once each is tagged `tag`: all loads are issued
+// first, then only the stale ones are read again.  A wait that expires
+// records the failure and goes on.
+template <int N>
+__device__ __forceinline__ void tagged_gather(const uint64_t* const (&src)[N], uint32_t tag, uint32_t* failure,
+                                              uint32_t (&out)[N]) {
+  uint64_t x[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) x[k] = __hip_atomic_load(src[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t polls = 0;
+  for (;;) {
+    bool ready = true;
+#pragma unroll
+    for (int k = 0; k < N; ++k) ready = ready && static_cast<uint32_t>(x[k] >> 32) == tag;
+    if (ready) break;
+    if (++polls == kHandoffPolls) {
+      __hip_atomic_store(failure, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+      if (static_cast<uint32_t>(x[k] >> 32) != tag)
+        x[k] = __hip_atomic_load(src[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+#pragma unroll
+  for (int k = 0; k < N; ++k) out[k] = static_cast<uint32_t>(x[k]);
+}
+
 // kFromQkv: q, k and the new v row are written in this launch (by the QKV
-// workgroups before the attention ones in the grid): the head rows are read
-// device-coherently after the go flag `qkv_go` (a Handoff whose `go` names
-// those lines), and the chain holding the current position takes its value
-// from `v_new` (the V cache column is written in this launch too).
+// workgroups before the attention ones in the grid) as the tagged words of
+// `tg`: the head rows are read from them once tagged, the chain holding the
+// current position takes its value from the tagged v row (the V cache column
+// is written in this launch too), and the output goes out as tagged words
+// (an expired wait records its failure on `hs`'s failure line).
 //
 // kSplit > 1 spreads one head's PV over kSplit workgroups: `slot` then runs
 // over q_heads x kSplit, and part slot / q_heads owns features
@@ -1405,8 +1455,8 @@ __device__ __forceinline__ void handoff_raise(const Handoff& hs, int go) {
 // values), so no part waits for another; the parts' PV chains run on
 // different compute units.
 template <bool kHandoff = false, bool kFromQkv = false, int kSplit = 1>
-__device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int b, const Handoff* qkv_go = nullptr,
-                                                const uint16_t* v_new = nullptr) {
+__device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int b, const Handoff* hs = nullptr,
+                                                const Tagged* tg = nullptr) {
   static_assert(kSplit == 1 || kSplit == 2 || kSplit == 4, "a head splits into 1, 2 or 4 feature parts");
   __shared__ float qs[kHeadDim];
   __shared__ float ks[kHeadDim];
@@ -1486,20 +1536,25 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
   }
   float v_pos = 0.0f;  // the new value at `pos` of this lane's feature (kFromQkv)
   if constexpr (kFromQkv) {
+    // A lane of a head wave reads values lane and lane + 64 of its head row
+    // (words lane / 2 and 32 + lane / 2); a chain lane reads its feature's
+    // new value.  The waves that do neither go straight to the barrier.
     __builtin_amdgcn_sched_barrier(0);
-    handoff_wait(*qkv_go);
+    uint32_t* failure = handoff_line(*hs, hs->failure);
+    const int c = g * kHeadDim + f;
     if (wave < 2) {
-      const uint32_t* x32 = reinterpret_cast<const uint32_t*>(head_row);
-      const uint32_t wa = __hip_atomic_load(x32 + lane / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const uint32_t wb = __hip_atomic_load(x32 + 32 + lane / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      head.xa = (lane & 1) ? dl_bf16_hi(wa) : dl_bf16_lo(wa);
-      head.xb = (lane & 1) ? dl_bf16_hi(wb) : dl_bf16_lo(wb);
-    }
-    if (chain) {
-      const int c = g * kHeadDim + f;
-      const uint32_t wv =
-          __hip_atomic_load(reinterpret_cast<const uint32_t*>(v_new) + c / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      v_pos = (c & 1) ? dl_bf16_hi(wv) : dl_bf16_lo(wv);
+      const uint64_t* row = tg->words + (wave == 0 ? h * (kHeadDim / 2) : tg->k + g * (kHeadDim / 2)) + lane / 2;
+      const uint64_t* src[3] = {row, row + 32, chain ? tg->words + tg->v + c / 2 : row};
+      uint32_t x[3];
+      tagged_gather<3>(src, tg->tag, failure, x);
+      head.xa = (lane & 1) ? dl_bf16_hi(x[0]) : dl_bf16_lo(x[0]);
+      head.xb = (lane & 1) ? dl_bf16_hi(x[1]) : dl_bf16_lo(x[1]);
+      if (chain) v_pos = (c & 1) ? dl_bf16_hi(x[2]) : dl_bf16_lo(x[2]);
+    } else if (chain) {
+      const uint64_t* src[1] = {tg->words + tg->v + c / 2};
+      uint32_t x[1];
+      tagged_gather<1>(src, tg->tag, failure, x);
+      v_pos = (c & 1) ? dl_bf16_hi(x[0]) : dl_bf16_lo(x[0]);
     }
   }
 
@@ -1686,7 +1741,13 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
   }
   __syncthreads();
   uint16_t* att = a.att + static_cast<uint64_t>(b) * qw + h * kHeadDim + part * kPartFeatures;
-  if constexpr (kHandoff) {
+  if constexpr (kFromQkv) {
+    if (tid < kPartFeatures / 2) {
+      const uint32_t lo = bf16_bits(red[2 * tid] + red[2 * tid + kHeadDim]);
+      const uint32_t hi = bf16_bits(red[2 * tid + 1] + red[2 * tid + 1 + kHeadDim]);
+      tagged_put(tg->words + tg->att + (h * kHeadDim + part * kPartFeatures) / 2 + tid, lo | (hi << 16), tg->tag);
+    }
+  } else if constexpr (kHandoff) {
     if (tid < kPartFeatures / 2) {
       const uint32_t lo = bf16_bits(red[2 * tid] + red[2 * tid + kHeadDim]);
       const uint32_t hi = bf16_bits(red[2 * tid + 1] + red[2 * tid + 1 + kHeadDim]);
@@ -1908,9 +1969,12 @@ struct AttnOArgs {
   uint32_t* sync;
 };
 
-// The O workgroup `wg` of `o_workgroups`: waits on hs's go lines; the last
-// to finish zeroes lines [0, hs.exit].
-__device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int o_workgroups, const Handoff& hs) {
+// The O workgroup `wg` of `o_workgroups`: waits on hs's go lines (or, with
+// `tg`, reads the attention output as tagged words); the last to finish
+// zeroes lines [0, hs.exit] (and with `tg` advances the epoch word `epoch`).
+template <bool kTagged = false>
+__device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int o_workgroups, const Handoff& hs,
+                                             const Tagged* tg = nullptr, uint32_t* epoch = nullptr) {
   constexpr int P = 16, RW = 64 / P;
   // 16-byte aligned: the attention's static arrays come first, and the chain
   // reads the staged inputs 16 bytes at a time.
@@ -1924,17 +1988,24 @@ __device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int 
   for (int s = 0; s < kOChunks; ++s) w[s] = load_stream(src + s * 64);
   if (!a.ctl->active) return;
   const uint64_t pos = a.ctl->position;
-  handoff_wait(hs);
   // The attention output, read device-coherently (it was written in this
   // launch), staged as stage_rows does; all of a thread's loads are issued
   // before any is used.
   constexpr int kWords = kOChunks * 8 * P / 2 / kAttnThreads;
   static_assert(kWords * 2 * kAttnThreads == kOChunks * 8 * P, "the O input row splits evenly over the threads");
-  const uint32_t* x32 = reinterpret_cast<const uint32_t*>(a.x);
   uint32_t v[kWords];
+  if constexpr (kTagged) {
+    const uint64_t* src[kWords];
 #pragma unroll
-  for (int k = 0; k < kWords; ++k)
-    v[k] = __hip_atomic_load(x32 + threadIdx.x + k * kAttnThreads, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int k = 0; k < kWords; ++k) src[k] = tg->words + tg->att + threadIdx.x + k * kAttnThreads;
+    tagged_gather<kWords>(src, tg->tag, handoff_line(hs, hs.failure), v);
+  } else {
+    handoff_wait(hs);
+    const uint32_t* x32 = reinterpret_cast<const uint32_t*>(a.x);
+#pragma unroll
+    for (int k = 0; k < kWords; ++k)
+      v[k] = __hip_atomic_load(x32 + threadIdx.x + k * kAttnThreads, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 #pragma unroll
   for (int k = 0; k < kWords; ++k) {
     const int wi = threadIdx.x + k * kAttnThreads;
@@ -1955,8 +2026,17 @@ __device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int 
                                                  __HIP_MEMORY_SCOPE_AGENT);
     if (done == static_cast<uint32_t>(o_workgroups) - 1u) {
       // Every workgroup of this launch is past its wait: clear for the next.
-      for (int line = 0; line <= hs.exit; ++line)
-        __hip_atomic_store(handoff_line(hs, line), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if constexpr (kTagged) {
+        // Every tagged word was read (each is some O workgroup's input or
+        // was read by an attention workgroup whose output this one read),
+        // so every workgroup has read the epoch: the next launch may use
+        // the next tag.
+        __hip_atomic_store(handoff_line(hs, hs.exit), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(epoch, tg->tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        for (int line = 0; line <= hs.exit; ++line)
+          __hip_atomic_store(handoff_line(hs, line), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
 }
@@ -1988,31 +2068,34 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_o(AttnOArgs a) {
 // projection of a single row: workgroups [0, qkv_workgroups) own one QKV
 // tile per wavefront (held in registers, as k_qkv's batch-1 path), then the
 // attention workgroups (kAttnSplit per query head), then the O workgroups
-// (as in k_attn_o).  The QKV
-// workgroups write q and k with device-coherent stores, the new V values
-// both into the cache column (for later steps) and, device-coherently, into
-// `v_new` (for this launch's attention, which substitutes them at the
-// current position); each counts itself on the counter of its XCD (lines
-// 0-7), the last of each counter counts the counter done (line 8), and the
-// last counter done raises the QKV go lines (9-16).  The attention
-// workgroups issue their key and value prefetch, wait for those lines, then
-// run; they count themselves on line 17 and the last raises the attention go
-// lines (18-25) that the O workgroups wait on.
-constexpr int kQkvoQkvCount = 0, kQkvoQkvDone = 8, kQkvoQkvGo = 9, kQkvoAttnCount = 17;
-constexpr Handoff kQkvoLayout{nullptr, 18, 26, 27};
-constexpr int kQkvoSyncWords = 32 * 28;
+// (as in k_attn_o).  Every hand-off goes through tagged words (Tagged): the
+// QKV workgroups write q, k and the new V values as tagged words (the new V
+// values also into the cache column, for later steps) and exit; each
+// attention workgroup issues its key and value prefetch, then reads its own
+// head's q row, its group's k row and its features' new V values once they
+// carry this launch's tag, and writes its output as tagged words; each O
+// workgroup reads the whole attention output the same way.  So no role
+// waits for another's store acknowledgements, counters or go flags, and a
+// head starts as soon as its own rows are written.  Sync lines: O exit
+// count 0, failure 1, epoch 2.
+constexpr Handoff kQkvoLayout{nullptr, -1, 0, 1};
+constexpr int kQkvoEpoch = 2;
+constexpr int kQkvoSyncWords = 32 * 3;
 constexpr int kQkvWaves = kAttnThreads / 64;
+
+// Tagged words of one k_qkv_attn_o launch: q (QW / 2), k (KW / 2), the new
+// V values (KW / 2), the attention output (QW / 2).
+__host__ __device__ constexpr int qkvo_tagged_words(int QW, int KW) { return QW + KW; }
 
 struct QkvAttnOArgs {
   QkvArgs qkv;
   AttnArgs attn;
   ResidualArgs o;
-  uint16_t* v_new;
+  uint64_t* tagged;
   uint32_t* sync;
-  int qkv_workgroups;
 };
 
-__device__ __forceinline__ void qkv_phase(const QkvArgs& a, uint16_t* v_new, const Handoff& hs, int qkv_workgroups) {
+__device__ __forceinline__ void qkv_phase(const QkvArgs& a, const Tagged& tg) {
   constexpr int W = kQkvWaves;
   extern __shared__ __align__(16) float lds[];
   float* xs16 = lds;
@@ -2053,9 +2136,7 @@ __device__ __forceinline__ void qkv_phase(const QkvArgs& a, uint16_t* v_new, con
     // Lanes 0, 16, 32, 48 hold rows 4 t .. 4 t + 3: two words.
     const uint32_t y = bf16_bits(acc[0]);
     const uint32_t y1 = __shfl_down(y, 16, 64);
-    if (lane == 0 || lane == 32)
-      __hip_atomic_store(reinterpret_cast<uint32_t*>(a.q_out) + tile * 2 + lane / 32, y | (y1 << 16),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0 || lane == 32) tagged_put(tg.words + tile * 2 + lane / 32, y | (y1 << 16), tg.tag);
   } else {
     constexpr int P = 32, stride = kWholeTileInputs / P + kXsPad;
     const float* xt = xs32 + (lane % P) * stride;
@@ -2067,44 +2148,27 @@ __device__ __forceinline__ void qkv_phase(const QkvArgs& a, uint16_t* v_new, con
     const uint32_t y1 = __shfl_down(y, 32, 64);
     if (is_v && lane % P == 0)
       a.v_cache[static_cast<uint64_t>(kt * 2 + lane / P) * a.cap + a.ctl->position] = static_cast<uint16_t>(y);
-    if (lane == 0)
-      __hip_atomic_store(reinterpret_cast<uint32_t*>(is_v ? v_new : a.k_out) + kt, y | (y1 << 16), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __builtin_amdgcn_s_waitcnt(pv_vmcnt(0));  // this wavefront's outputs are written
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    // The last workgroup of a counter's share counts the counter done; the
-    // last counter done raises the QKV go lines.
-    const int x = blockIdx.x % 8;
-    const uint32_t share = static_cast<uint32_t>((qkv_workgroups - x + 7) / 8);
-    const uint32_t n = __hip_atomic_fetch_add(handoff_line(hs, kQkvoQkvCount + x), 1u, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-    if (n == share - 1u) {
-      const uint32_t c = __hip_atomic_fetch_add(handoff_line(hs, kQkvoQkvDone), 1u, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-      if (c == 7u) handoff_raise(hs, kQkvoQkvGo);
-    }
+    if (lane == 0) tagged_put(tg.words + (is_v ? tg.v : tg.k) + kt, y | (y1 << 16), tg.tag);
   }
 }
 
 __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_qkv_attn_o(QkvAttnOArgs a) {
-  const uint32_t heads = static_cast<uint32_t>(a.attn.q_heads) * kAttnSplit, nq = static_cast<uint32_t>(a.qkv_workgroups);
+  const uint32_t heads = static_cast<uint32_t>(a.attn.q_heads) * kAttnSplit;
+  const uint32_t nq = static_cast<uint32_t>(a.qkv.QW / 4 + a.qkv.KW) / kQkvWaves;
   Handoff hs = kQkvoLayout;
   hs.words = a.sync;
+  uint32_t* epoch = handoff_line(hs, kQkvoEpoch);
+  const Tagged tg{a.tagged, __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u, a.qkv.QW / 2,
+                  a.qkv.QW / 2 + a.qkv.KW / 2, a.qkv.QW / 2 + a.qkv.KW};
   if (blockIdx.x < nq) {
-    qkv_phase(a.qkv, a.v_new, hs, a.qkv_workgroups);
+    qkv_phase(a.qkv, tg);
     return;
   }
   if (blockIdx.x < nq + heads) {
-    Handoff qkv_go = hs;
-    qkv_go.go = kQkvoQkvGo;
-    if (!attn_fused_body<true, true, kAttnSplit>(a.attn, blockIdx.x - nq, 0, &qkv_go, a.v_new)) return;
-    __syncthreads();  // every output word of this workgroup has been written
-    handoff_signal(hs, kQkvoAttnCount, heads, hs.go);
+    attn_fused_body<true, true, kAttnSplit>(a.attn, blockIdx.x - nq, 0, &hs, &tg);
     return;
   }
-  o_prefetched(a.o, blockIdx.x - nq - heads, gridDim.x - nq - heads, hs);
+  o_prefetched<true>(a.o, blockIdx.x - nq - heads, gridDim.x - nq - heads, hs, &tg, epoch);
 }
 
 // ------------------------------------------------------------ gate/up GEMV
@@ -3160,7 +3224,7 @@ struct dl_plan {
   uint32_t* attn_sync = nullptr;
   // Hand-off words of the fused QKV + attention + O launch, and its new V row.
   uint32_t* qkvo_sync = nullptr;
-  uint16_t* v_new = nullptr;
+  uint64_t* qkvo_tagged = nullptr;
   uint64_t* partial_keys = nullptr;
   uint32_t *partial_flags = nullptr, *tokens = nullptr, *selected = nullptr, *out_tokens = nullptr;
   uint8_t* stop_mask = nullptr;
@@ -3532,7 +3596,7 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       const int o_workgroups = D / (64 / 16) / kOWaves;
       const size_t lds = (staged_floats(16, D) + staged_floats(32, D)) * sizeof(float);
       k_qkv_attn_o<<<qkv_workgroups + c.q_heads * kAttnSplit + o_workgroups, kAttnThreads, lds, s>>>(
-          QkvAttnOArgs{qa, aa, oa, p->v_new, p->qkvo_sync, qkv_workgroups});
+          QkvAttnOArgs{qa, aa, oa, p->qkvo_tagged, p->qkvo_sync});
       break;
     }
     case 10: {
@@ -3846,7 +3910,8 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
     dl::check_hip(hipMemsetAsync(p->attn_sync, 0, dl::kSyncWords * 4, queue->stream), "hand-off clear");
     p->qkvo_sync = p->alloc<uint32_t>(dl::kQkvoSyncWords);
     dl::check_hip(hipMemsetAsync(p->qkvo_sync, 0, dl::kQkvoSyncWords * 4, queue->stream), "hand-off clear");
-    p->v_new = p->alloc<uint16_t>(KW);
+    p->qkvo_tagged = p->alloc<uint64_t>(dl::qkvo_tagged_words(QW, KW));
+    dl::check_hip(hipMemsetAsync(p->qkvo_tagged, 0, dl::qkvo_tagged_words(QW, KW) * 8, queue->stream), "hand-off clear");
     p->partial_keys = p->alloc<uint64_t>(B * 1024);
     p->partial_flags = p->alloc<uint32_t>(B * 1024);
     p->tokens = p->alloc<uint32_t>(cap);
