@@ -43,6 +43,32 @@ __device__ __forceinline__ float row_down(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + kOff, 0xf, 0xf, true));
 }
 
+// row_down for an order-free reduction: a lane whose source lies past its
+// row keeps its own value (DPP with the lane disabled instead of reading 0).
+template <int kOff>
+__device__ __forceinline__ float row_down_keep(float v) {
+  static_assert(kOff >= 1 && kOff <= 15, "DPP row shifts within 16 lanes");
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x100 + kOff, 0xf, 0xf, false));
+}
+
+// The maximum over the 64 lanes of a wavefront, returned to every lane.
+// fmaxf is exact, so any tree gives the same value (a NaN input is ignored
+// by every tree alike): DPP steps within each 16-lane row, then the four row
+// maxima read from lanes 0, 16, 32 and 48.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, row_down_keep<1>(v));
+  v = fmaxf(v, row_down_keep<2>(v));
+  v = fmaxf(v, row_down_keep<4>(v));
+  v = fmaxf(v, row_down_keep<8>(v));
+  const int b = __float_as_int(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 // The adjacent-first tree over 32 lanes (offsets 1, 2, 4, 8, 16 as
 // __shfl_down(s, off, 32)); lane 0 of each 32-lane half holds the total.
 // Offsets below 16 stay in the row of the lanes that feed lane 0.

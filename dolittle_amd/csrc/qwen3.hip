@@ -1349,7 +1349,7 @@ constexpr int kFusedKeys = 1536;
 constexpr int kAttnThreads = 512;
 constexpr int kAttnKeysPerPass = kAttnThreads / 8;
 constexpr int kAttnKeyPasses = 8;     // key rows issued at kernel entry: 512 keys
-constexpr int kAttnValueBlocks = 8;  // 8-key V blocks per PV chain issued at entry (one 64-key block)
+constexpr int kAttnValueBlocks = 16;  // 8-key V blocks per PV chain issued at entry (two 64-key blocks)
 
 // The attention of query head slot `slot` (group-minor numbering) of row
 // `b`; false when the loop is stopped (nothing is written).  kHandoff writes
@@ -1622,8 +1622,7 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
   // 16..1, p = e / l (attention.cu:301-360).
   float m = -INFINITY;
   for (int j = tid; j < count; j += kAttnThreads) m = fmaxf(m, sc[j]);
-#pragma unroll
-  for (int off = 32; off; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  m = dl::wave_max(m);
   if (lane == 0) wave_max[wave] = m;
   __syncthreads();
   m = wave_max[0];
@@ -1633,7 +1632,8 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
   __syncthreads();
   if (tid < 32) {
     // The partial's additions in ascending key order, its LDS reads issued
-    // eight at a time.
+    // eight at a time (the last, partial batch too: reads past the keys are
+    // clamped and their additions skipped).
     float partial = 0.0f;
     int j = tid;
     for (; j + 7 * 32 < count; j += 8 * 32) {
@@ -1643,9 +1643,20 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
 #pragma unroll
       for (int k = 0; k < 8; ++k) partial = partial + e[k];
     }
-    for (; j < count; j += 32) partial = partial + sc[j];
+    if (j < count) {
+      float e[7];
 #pragma unroll
-    for (int off = 16; off; off >>= 1) partial = partial + __shfl_down(partial, off, 32);
+      for (int k = 0; k < 7; ++k) e[k] = sc[min(j + 32 * k, count - 1)];
+#pragma unroll
+      for (int k = 0; k < 7; ++k) partial = j + 32 * k < count ? partial + e[k] : partial;
+    }
+    // Offsets 16, 8, 4, 2, 1 as __shfl_down(partial, off, 32); below 16 the
+    // lanes that feed lane 0 read within their row (DPP).
+    partial = partial + __shfl_down(partial, 16, 32);
+    partial = partial + row_down<8>(partial);
+    partial = partial + row_down<4>(partial);
+    partial = partial + row_down<2>(partial);
+    partial = partial + row_down<1>(partial);
     if (tid == 0) denominator_shared = partial;
   }
   __syncthreads();
@@ -1721,10 +1732,22 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
       }
     };
     if (blocks > 0) {
+      // Blocks 0 and 1 come from the entry prefetch.
+      static_assert(kAttnValueBlocks == 16, "the entry prefetch holds two 64-key blocks");
       u32x4 va[8], vb[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) va[i] = vpre[i];
-      int x = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vb[i] = vpre[8 + i];
+      run(va, 0);
+      int x = 1;
+      if (blocks > 1) {
+        load(va, 2);
+        __builtin_amdgcn_sched_barrier(0);
+        run(vb, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        x = 2;
+      }
       for (; x + 2 <= blocks; x += 2) {
         load(vb, x + 1);
         __builtin_amdgcn_sched_barrier(0);
@@ -3462,6 +3485,7 @@ void launch_residual(dl_plan* p, hipStream_t s, int which, const dl::ResidualArg
   dl::k_residual<P, G, split><<<p->grid_for(which, a.D / (64 / P) * split, lds, dl::gemv_waves(G)),
                                 dl::gemv_waves(G) * 64, lds, s>>>(a);
 }
+
 template <int G>
 void launch_gateup(dl_plan* p, hipStream_t s, const dl::GateUpArgs& a) {
   dl::k_gateup<G><<<p->grid_for(5, a.F / 2, p16_lds(G, a.D), dl::gemv_waves(G)), dl::gemv_waves(G) * 64,
