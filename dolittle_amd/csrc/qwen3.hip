@@ -922,6 +922,37 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
         bf16_bits(acc + second);
 }
 
+// acc = fma(p_k, v[k], acc) for k = 0..15 in order, p_k taken from lane k
+// of the lane's 16-lane row of `p` (DPP row_newbcast): one VGPR carries the
+// probabilities of 16 keys, so a PV chain wave needs no LDS read per key.
+// v_fmac_f32 is the single-rounding FMA, the same operation as fma_rn.  The
+// s_nop covers the two wait states a DPP read needs after a VALU write of its
+// source.
+__device__ __forceinline__ float fma16_row_bcast(float acc, float p, const float (&v)[16]) {
+  asm volatile(
+      "s_nop 1\n"
+      "v_fmac_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf"
+      : "+v"(acc)
+      : "v"(p), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]), "v"(v[8]),
+        "v"(v[9]), "v"(v[10]), "v"(v[11]), "v"(v[12]), "v"(v[13]), "v"(v[14]), "v"(v[15]));
+  return acc;
+}
+
 // Several rows per launch (the chunked prompt pass): k_attn_pv's work in 64
 // workgroups per row, so that 8 rows still fit the GPU in one round.  Grid
 // (kv head * 8 feature blocks, row), 256 threads.  Waves 0 and 2 run the two
@@ -1351,37 +1382,6 @@ constexpr int kAttnKeysPerPass = kAttnThreads / 8;
 constexpr int kAttnKeyPasses = 8;     // key rows issued at kernel entry: 512 keys
 constexpr int kAttnValueBlocks = 16;  // 8-key V blocks per PV chain issued at entry (two 64-key blocks)
 
-// acc = fma(p_k, v[k], acc) for k = 0..15 in order, p_k taken from lane k
-// of the lane's 16-lane row of `p` (DPP row_newbcast): one VGPR carries the
-// probabilities of 16 keys, so a PV chain wave needs no LDS read per key.
-// v_fmac_f32 is the single-rounding FMA, the same operation as fma_rn.  The
-// s_nop covers the two wait states a DPP read needs after a VALU write of its
-// source.
-__device__ __forceinline__ float fma16_row_bcast(float acc, float p, const float (&v)[16]) {
-  asm volatile(
-      "s_nop 1\n"
-      "v_fmac_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
-      "v_fmac_f32_dpp %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf"
-      : "+v"(acc)
-      : "v"(p), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]), "v"(v[8]),
-        "v"(v[9]), "v"(v[10]), "v"(v[11]), "v"(v[12]), "v"(v[13]), "v"(v[14]), "v"(v[15]));
-  return acc;
-}
-
 // The attention of query head slot `slot` (group-minor numbering) of row
 // `b`; false when the loop is stopped (nothing is written).  kHandoff writes
 // the output with device-coherent stores and waits for them, for a reader
@@ -1719,11 +1719,12 @@ __device__ __forceinline__ bool attn_fused_body(const AttnArgs& a, int slot, int
       const int pi = static_cast<int>(pos) - jb;
       const bool patch = kFromQkv && pi >= lo && pi < hi;
       if (hi <= lo) return;
-      if (kSplit == 2 && lo == 0 && hi == 64 && !patch) {
+      if (kPartFeatures % 64 == 0 && lo == 0 && hi == 64 && !patch) {
         // A block wholly inside the chain: the 64 probabilities as four
         // VGPRs of 16 (lane l holds key jb + 16 q + l % 16), each FMA taking
         // its key's value by DPP broadcast.  Every lane of the wave is a
-        // chain lane here (two parts per head), as the broadcast needs.
+        // chain lane of one half here (one or two parts per head), as the
+        // broadcast needs.
         float pq[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) pq[q] = sc[jb + 16 * q + (lane & 15)];
