@@ -7,7 +7,9 @@
 // probability is rounded to BF16 (numerical-portability.md:8-10).
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "dl_device.h"
 #include "dl_internal.h"
@@ -50,11 +52,23 @@ __device__ __forceinline__ uint64_t packed_offset(int n, int P, int K, int kpos)
 
 // SiluMultiply on BF16-rounded operands (elementwise.cu:62-87), two-sided
 // as there, with the decode path's correctly rounded exponential, so an
-// activation row equals the exact chain's whenever its gate and up inputs do.
-__device__ __forceinline__ float silu_times(float a, float b) {
+// activation row equals the exact chain's whenever its gate and up inputs do:
+// the activation is silu_round(gate) * up.
+__device__ __forceinline__ float silu_round(float a) {
   const float e = dl_expf(a >= 0.0f ? -a : a);
   const float sigmoid = a >= 0.0f ? 1.0f / (1.0f + e) : e / (1.0f + e);
-  return dl_round_bf16(a * sigmoid) * b;
+  return dl_round_bf16(a * sigmoid);
+}
+
+// silu_round of every BF16 value, by bit pattern, built once per device
+// (k_silu_table): the GEMM epilogue looks its activations up instead of
+// evaluating the FP64-accurate exponential per element, with the same
+// values.  In a 256 x 256 gate/up tile the evaluation took ~20% of the launch.
+__device__ uint16_t g_silu_table[65536];
+
+__global__ void k_silu_table() {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  g_silu_table[i] = dl_f32_to_bf16(silu_round(dl_bf16_to_f32(static_cast<uint16_t>(i))));
 }
 
 // exp(x) for x <= 0 within about 2 ulp: 2^(x log2 e) with the product split
@@ -100,35 +114,75 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int m, int n, f
 // lane % 32, row 8 (r / 4) + 4 (lane / 32) + r % 4 for r < 16.  For the
 // gate/up epilogue the four lanes of a quad hold gate 2j, gate 2j+1, up 2j,
 // up 2j+1 of the same rows; the gate lanes finish rows r < 8 and the up lanes
-// rows r >= 8, each taking the other operand from the lane two over.
+// rows r >= 8, each taking the other operand from the lane two over, and
+// per row of MFMA tiles every SiLU is looked up before any activation is
+// stored (so the lookups are not ordered behind the stores).
 template <int EPI, int WM, int WN>
 __device__ __forceinline__ void gemm_tile_epilogue(const GemmArgs& a, const floatx16 (&acc)[WM][WN], int mb, int nb,
                                                    int lane) {
+  if constexpr (EPI == kResidual) {
+    // Per row of MFMA tiles, every residual value is loaded before any sum
+    // is stored: the stores may alias later loads as far as the compiler
+    // knows, so element by element each load would wait for a full memory
+    // round trip.
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const int rows = mb + 32 * i + 4 * (lane / 32);
+      uint16_t old[WN][16];
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          old[j][r] = a.out[static_cast<uint64_t>(rows + 8 * (r / 4) + r % 4) * a.N + nb + 32 * j + lane % 32];
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          a.out[static_cast<uint64_t>(rows + 8 * (r / 4) + r % 4) * a.N + nb + 32 * j + lane % 32] =
+              dl_f32_to_bf16(dl_bf16_to_f32(old[j][r]) + dl_round_bf16(acc[i][j][r]));
+    }
+    return;
+  }
+  if constexpr (EPI == kGateUp) {
+    const bool gate_lane = (lane & 3) < 2;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const int rows = mb + 32 * i + 4 * (lane / 32);
+      uint16_t silu[WN][8];
+      float other[WN][8];
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float send = gate_lane ? acc[i][j][8 + k] : acc[i][j][k];
+          const float recv = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0x4e, 0xf, 0xf, false));
+          const float gate = gate_lane ? acc[i][j][k] : recv;
+          other[j][k] = dl_round_bf16(gate_lane ? recv : acc[i][j][8 + k]);
+          silu[j][k] = g_silu_table[dl_f32_to_bf16(gate)];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        const int n = nb + 32 * j + lane % 32;
+        uint16_t* out = a.out + permuted(2 * (n / 4) + (lane & 1), 32);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int r = gate_lane ? k : 8 + k;
+          const int m = rows + 8 * (r / 4) + r % 4;
+          out[static_cast<uint64_t>(m) * (a.N / 2)] = dl_f32_to_bf16(dl_bf16_to_f32(silu[j][k]) * other[j][k]);
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < WM; ++i) {
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
       const int n = nb + 32 * j + lane % 32;
       const int rows = mb + 32 * i + 4 * (lane / 32);
-      if constexpr (EPI == kGateUp) {
-        const bool gate_lane = (lane & 3) < 2;
-        const uint32_t f = 2 * (n / 4) + (lane & 1);
-        uint16_t* out = a.out + permuted(f, 32);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const float send = gate_lane ? acc[i][j][8 + k] : acc[i][j][k];
-          const float recv = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0x4e, 0xf, 0xf, false));
-          const float gate = gate_lane ? acc[i][j][k] : recv;
-          const float up = gate_lane ? recv : acc[i][j][8 + k];
-          const int r = gate_lane ? k : 8 + k;
-          const int m = rows + 8 * (r / 4) + r % 4;
-          out[static_cast<uint64_t>(m) * (a.N / 2)] =
-              dl_f32_to_bf16(silu_times(dl_round_bf16(gate), dl_round_bf16(up)));
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) gemm_epilogue<EPI>(a, rows + 8 * (r / 4) + r % 4, n, acc[i][j][r]);
-      }
+      for (int r = 0; r < 16; ++r) gemm_epilogue<EPI>(a, rows + 8 * (r / 4) + r % 4, n, acc[i][j][r]);
     }
   }
 }
@@ -252,6 +306,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 // below are the only ones the loads need.
 constexpr int kDmaTK = 32;
 constexpr int kDmaTN = 256;
+constexpr int kGemmGroupM = 8;  // M tiles per group of the tile order
 constexpr int kDmaLoads = (kTileM + kDmaTN) * kDmaTK / 8 / kGemmThreads;  // 16-byte loads per thread per chunk
 
 __device__ __forceinline__ int dma_swizzle(int r) { return (r >> 2) & 3; }
@@ -268,7 +323,17 @@ template <int EPI>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_dma(GemmArgs a) {
   __shared__ __align__(1024) uint16_t A0[kTileM * kDmaTK], A1[kTileM * kDmaTK], A2[kTileM * kDmaTK];
   __shared__ __align__(1024) uint16_t B0[kDmaTN * kDmaTK], B1[kDmaTN * kDmaTK], B2[kDmaTN * kDmaTK];
-  const int n0 = blockIdx.x * kDmaTN, m0 = blockIdx.y * kTileM;
+  // Tile order.  Workgroups are dealt to the XCDs round-robin by linear id;
+  // XCD x takes the x-th eighth of a grouped raster (kGemmGroupM M tiles per
+  // group, walked N tile by N tile), so the ~64 workgroups resident on one
+  // XCD at a time cover a compact block of tiles and share their A rows and
+  // weight rows in that XCD's L2.
+  const int nN = gridDim.x, nM = gridDim.y, total = nN * nM;
+  const int id = blockIdx.x + blockIdx.y * nN;
+  const int v = total % kXcds == 0 ? (id % kXcds) * (total / kXcds) + id / kXcds : id;
+  const int group = v / (kGemmGroupM * nN), first_m = group * kGemmGroupM;
+  const int gm = min(nM - first_m, kGemmGroupM), rest = v - group * kGemmGroupM * nN;
+  const int n0 = (rest / gm) * kDmaTN, m0 = (first_m + rest % gm) * kTileM;
   const bool alt = n0 >= a.n_split;
   const uint16_t* A = alt ? a.a_alt : a.a;
   const uint16_t* W = alt ? a.w_alt : a.w;
@@ -386,6 +451,173 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // no load outlives the wave
 #undef DL_DMA_STEP
   gemm_tile_epilogue<EPI, 2, 4>(a, acc, m0 + 64 * wm, n0 + 128 * wn, lane);
+}
+
+// 256 x 256 tiles for the wide GEMMs (gate/up, O, down): four waves of
+// 128 x 128 (4 x 4 MFMA tiles, 256 FP32 accumulators per lane), so a
+// 16-deep K step reads 8 operand fragments from LDS for 16 products (0.5
+// per product, against 0.75 for k_gemm_dma's 64 x 128 waves) and a
+// workgroup brings 64 KB per 32 K positions for twice k_gemm_dma's work.
+// K chunks of 32 positions go through a ring of four 32 KB LDS stages by
+// direct global-to-LDS loads, three chunks ahead.  Per chunk, each wave
+//   - reads the second K step's fragments (F1) of chunk c,
+//   - issues chunk c + 3 into the stage chunk c - 1 left, between the
+//     products of the first K step (F0, read in the previous chunk),
+//   - waits for its loads of chunk c + 1 and its fragment reads, then one
+//     workgroup barrier (every wave's chunk c + 1 is in LDS; every wave is
+//     done reading chunk c - 1's stage before any load into it is issued),
+//   - reads chunk c + 1's F0 while the products of F1 run,
+// so the matrix cores see no fragment-read latency and one barrier per 32
+// products.  Stage rows use k_gemm_dma's 64-byte swizzled rows.
+constexpr int kBigM = 256;
+constexpr int kBigStageElems = (kBigM + kDmaTN) * kDmaTK;  // A rows then W rows
+constexpr int kBigLoads = kBigStageElems / 8 / kGemmThreads;  // 16-byte loads per thread per chunk: 8
+
+// s_waitcnt immediate: at most n vector-memory operations outstanding and no
+// LDS operation outstanding (lgkmcnt 0; expcnt at its no-wait maximum).
+constexpr unsigned vm_lds_wait(unsigned n) { return 0x0070u | (n & 0xfu) | ((n >> 4) << 14); }
+
+struct BigFrags {
+  bf16x8 a[4], b[4];
+};
+
+template <int EPI>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1))) void k_gemm_big(GemmArgs a) {
+  __shared__ __align__(1024) uint16_t S0[kBigStageElems], S1[kBigStageElems], S2[kBigStageElems],
+      S3[kBigStageElems];
+  // Tile order as k_gemm_dma (XCD-contiguous eighths of a grouped raster).
+  const int nN = gridDim.x, nM = gridDim.y, total = nN * nM;
+  const int id = blockIdx.x + blockIdx.y * nN;
+  const int v = total % kXcds == 0 ? (id % kXcds) * (total / kXcds) + id / kXcds : id;
+  constexpr int kGroup = kGemmGroupM / 2;
+  const int group = v / (kGroup * nN), first_m = group * kGroup;
+  const int gm = min(nM - first_m, kGroup), rest = v - group * kGroup * nN;
+  const int n0 = (rest / gm) * kDmaTN, m0 = (first_m + rest % gm) * kBigM;
+  const bool alt = n0 >= a.n_split;
+  const uint16_t* A = alt ? a.a_alt : a.a;
+  const uint16_t* W = alt ? a.w_alt : a.w;
+  const int P = alt ? a.P_alt : a.P;
+  const int nb = alt ? n0 - a.n_split : n0;
+  const int K = a.K, chunks = K / kDmaTK;
+  const int tid = threadIdx.x, lane = tid % 64;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // Load j of this wave fills stage rows 16 (4 j + wave) .. + 15 of A
+  // (j < 4) or of W (j >= 4); lane L brings row + L / 4, physical piece L % 4.
+  const int lr = lane / 4, lp = lane % 4;
+  const uint16_t* src[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 16 * (4 * j + wave) + lr;
+    src[j] = A + static_cast<uint64_t>(m0 + r) * K + 8 * (lp ^ dma_swizzle(r));
+    src[4 + j] = W + packed_offset(nb + r, P, K, 0) + 8 * (lp ^ dma_swizzle(r));
+  }
+  const int block_shift = __builtin_ctz(8 * P), block_mask = 8 * P - 1;
+  auto issue = [&](int c, uint16_t* S) {
+    const int kp = c * kDmaTK;
+    const uint64_t woff = (static_cast<uint64_t>(kp >> block_shift) << 9) + (kp & block_mask);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds((const global_void*)(src[j] + kp), (lds_void*)(S + 16 * (4 * j + wave) * kDmaTK),
+                                       16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds((const global_void*)(src[4 + j] + woff),
+                                       (lds_void*)(S + (kBigM + 16 * (4 * j + wave)) * kDmaTK), 16, 0, 0);
+  };
+  const int sw = dma_swizzle(lane % 32);
+  int frag[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) frag[ks] = (lane % 32) * kDmaTK + 8 * ((2 * ks + lane / 32) ^ sw);
+  auto read = [&](const uint16_t* S, int ks, BigFrags& f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      f.a[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&S[(128 * wm + 32 * i) * kDmaTK + frag[ks]]));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      f.b[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(&S[(kBigM + 128 * wn + 32 * j) * kDmaTK + frag[ks]]));
+  };
+  floatx16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  auto products = [&](const BigFrags& f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+  };
+
+  // First K step: F1's 8 fragment reads spread over the first 8 products
+  // (after the first two, so the wait for F0's reads, long landed, does not
+  // also wait for F1's), then the other 8 products with the next loads
+  // between them.  Second: F0's reads of the next chunk spread over the
+  // first 8 products.
+  auto big_first_schedule = [] {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS reads
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global-to-LDS load
+    }
+  };
+  auto big_second_schedule = [] {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+  };
+  issue(0, S0);
+  issue(min(1, chunks - 1), S1);
+  issue(min(2, chunks - 1), S2);
+  __builtin_amdgcn_s_waitcnt(vm_lds_wait(2 * kBigLoads));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  BigFrags f0, f1;
+  read(S0, 0, f0);
+  int c = 0;
+  // One chunk: Sc holds chunk c, Sn chunk c + 1, Sf is free for chunk c + 3.
+  // Past the last chunk the loads repeat it into the free stage, so every
+  // chunk issues and waits with the same counts (and the last chunk's F0
+  // read of "chunk c + 1" reads such a landed repeat, never used).
+#define DL_BIG_STEP(Sc, Sn, Sf)                                            \
+  do {                                                                     \
+    read(Sc, 1, f1);                                                       \
+    issue(min(c + 3, chunks - 1), Sf);                                     \
+    products(f0);                                                          \
+    big_first_schedule();                                                  \
+    __builtin_amdgcn_sched_barrier(0);                                     \
+    __builtin_amdgcn_s_waitcnt(vm_lds_wait(2 * kBigLoads));               \
+    __builtin_amdgcn_s_barrier();                                          \
+    __builtin_amdgcn_sched_barrier(0);                                     \
+    read(Sn, 0, f0);                                                       \
+    products(f1);                                                          \
+    big_second_schedule();                                                 \
+    __builtin_amdgcn_sched_barrier(0);                                     \
+    ++c;                                                                   \
+  } while (0)
+  for (; c + 4 <= chunks;) {
+    DL_BIG_STEP(S0, S1, S3);
+    DL_BIG_STEP(S1, S2, S0);
+    DL_BIG_STEP(S2, S3, S1);
+    DL_BIG_STEP(S3, S0, S2);
+  }
+  if (c < chunks) DL_BIG_STEP(S0, S1, S3);
+  if (c < chunks) DL_BIG_STEP(S1, S2, S0);
+  if (c < chunks) DL_BIG_STEP(S2, S3, S1);
+#undef DL_BIG_STEP
+  __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // no load outlives the wave
+  gemm_tile_epilogue<EPI, 4, 4>(a, acc, m0 + 128 * wm, n0 + 128 * wn, lane);
 }
 
 // ------------------------------------------------------------- row norms
@@ -736,7 +968,36 @@ void launch_permute(hipStream_t stream, const uint16_t* x, uint16_t* out, uint64
   hipLaunchKernelGGL(k_permute, dim3(grid), dim3(256), 0, stream, x, out, rows, width, P);
 }
 
+// Builds g_silu_table on the current device before its first gate/up GEMM
+// (and waits for it, so a GEMM on any other stream of the device finds it).
+void ensure_silu_table(hipStream_t stream) {
+  static std::mutex mu;
+  static std::vector<bool> built;
+  int device = 0;
+  check_hip(hipGetDevice(&device), "current device");
+  std::lock_guard<std::mutex> lock(mu);
+  if (built.size() <= static_cast<size_t>(device)) built.resize(device + 1, false);
+  if (built[device]) return;
+  hipLaunchKernelGGL(k_silu_table, dim3(65536 / 256), dim3(256), 0, stream);
+  check_hip(hipGetLastError(), "SiLU table");
+  check_hip(hipStreamSynchronize(stream), "SiLU table");
+  built[device] = true;
+}
+
 void launch_gemm(hipStream_t stream, const GemmArgs& a) {
+  if (a.epilogue == kGateUp) ensure_silu_table(stream);
+  // 256 x 256 tiles where they fill the GPU in whole rounds (gate/up, O,
+  // down at 4096 rows); the QKV epilogue keeps the 128 x 256 tiles.
+  if (a.N % 256 == 0 && a.n_split % 256 == 0 && a.M % kBigM == 0 && a.epilogue != kStoreQkv &&
+      (a.N / 256) * (a.M / kBigM) >= 256) {
+    const dim3 grid(a.N / kDmaTN, a.M / kBigM);
+    switch (a.epilogue) {
+      case kStore: hipLaunchKernelGGL((k_gemm_big<kStore>), grid, dim3(kGemmThreads), 0, stream, a); break;
+      case kResidual: hipLaunchKernelGGL((k_gemm_big<kResidual>), grid, dim3(kGemmThreads), 0, stream, a); break;
+      default: hipLaunchKernelGGL((k_gemm_big<kGateUp>), grid, dim3(kGemmThreads), 0, stream, a); break;
+    }
+    return;
+  }
   // The 256-wide tile needs whole tiles on both sides of the Q | K/V split.
   if (a.N % 256 == 0 && a.n_split % 256 == 0) {
     const dim3 grid(a.N / kDmaTN, a.M / kTileM);

@@ -25,8 +25,11 @@ def bf16_ulp(x):
     return 2.0 ** (e - 7)
 
 
+# (4096, 4096, 4096) has 256 output tiles of 256 x 256: the 256 x 256 tile
+# GEMM; the smaller shapes run the 128 x 256 and 128 x 128 tile GEMMs.
 @pytest.mark.parametrize("rows,in_w,out_w", [(256, 4096, 4096), (128, 4096, 1024), (128, 12288, 4096),
-                                             (384, 4096, 6144), (512, 12288, 4096), (512, 4096, 6144)])
+                                             (384, 4096, 6144), (512, 12288, 4096), (512, 4096, 6144),
+                                             (4096, 4096, 4096)])
 def test_prefill_projection_within_one_ulp(device, queue, oracle, rows, in_w, out_w):
     from dolittle_amd import _lib
     x = oracle.normal_bf16(rows * in_w, SEED, 1, 1.0)
