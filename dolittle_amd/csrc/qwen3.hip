@@ -452,6 +452,14 @@ __global__ __launch_bounds__(qkv_waves(B, Part) * 64) __attribute__((amdgpu_wave
   }
 }
 
+// Orders one wavefront's LDS writes before its own later LDS reads (and the
+// reads before the next writes) when lanes exchange values through LDS.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ------------------------------------------------------------- attention
 struct AttnArgs {
   const Control* ctl;
@@ -706,6 +714,59 @@ __global__ __launch_bounds__(kSoftmaxThreads) void k_attn_softmax(AttnArgs a) {
   __syncthreads();
   const float l = denominator_shared;
   for (int j = tid; j < count; j += kSoftmaxThreads) a.probs[row + j] = es[j] / l;
+}
+
+// k_attn_softmax for many rows (the chunked prompt pass, batched decode):
+// one wavefront per (query head, row), grid (query head, row), so that a
+// short row is not spread over 1024 threads and three workgroup barriers.
+// The same arithmetic: m = max (order-free), e = exp(s - m) kept in the
+// wavefront's LDS, the 32 partials owning j mod 32 in ascending key order
+// (lanes 0-31, reads eight at a time), merged at offsets 16..1, p = e / l
+// (attention.cu:301-330).
+__global__ __launch_bounds__(64) void k_attn_softmax_rows(AttnArgs a) {
+  extern __shared__ float es[];
+  if (!a.ctl->active) return;
+  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const int count = static_cast<int>(a.ctl->position + static_cast<uint64_t>(b) * a.pos_step) + 1;
+  const uint64_t row = (static_cast<uint64_t>(b) * a.q_heads + h) * a.cap;
+  const float* sc = a.scores + row;
+  float m = -INFINITY;
+  for (int base = 0; base < count; base += 64 * kSoftmaxLoads) {
+    float s[kSoftmaxLoads];
+#pragma unroll
+    for (int i = 0; i < kSoftmaxLoads; ++i) s[i] = sc[min(base + lane + 64 * i, count - 1)];
+#pragma unroll
+    for (int i = 0; i < kSoftmaxLoads; ++i) {
+      m = fmaxf(m, s[i]);
+      const int j = base + lane + 64 * i;
+      if (j < count) es[j] = s[i];
+    }
+  }
+  m = dl::wave_max(m);
+  wave_lds_sync();
+  for (int j = lane; j < count; j += 64) es[j] = dl_expf(es[j] - m);
+  wave_lds_sync();
+  float partial = 0.0f;
+  if (lane < 32) {
+    int j = lane;
+    for (; j + 7 * 32 < count; j += 8 * 32) {
+      float e[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) e[k] = es[j + 32 * k];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) partial = partial + e[k];
+    }
+    for (; j < count; j += 32) partial = partial + es[j];
+  }
+  // Offsets 16, 8, 4, 2, 1 as __shfl_down(partial, off, 32); below 16 the
+  // lanes that feed lane 0 read within their row (DPP).
+  partial = partial + __shfl_down(partial, 16, 32);
+  partial = partial + row_down<8>(partial);
+  partial = partial + row_down<4>(partial);
+  partial = partial + row_down<2>(partial);
+  partial = partial + row_down<1>(partial);
+  const float l = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(partial), 0));
+  for (int j = lane; j < count; j += 64) a.probs[row + j] = es[j] / l;
 }
 
 // Grid (kv head * 32 feature blocks, sequence), 192 threads.  Wave 0 runs
@@ -1857,13 +1918,6 @@ struct ResidualArgs {
   int same_sequence, sequence;
 };
 
-// Orders one wavefront's LDS writes before its own later LDS reads (and the
-// reads before the next writes) when lanes exchange values through LDS.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Residual epilogue of one tile: output row tile * RW + i of sequence row b
 // is h = round(h + round(y)), then the optional steering and capture.  With
@@ -3509,6 +3563,7 @@ void prepare_kernels_all(dl_plan* p) {
   allow_lds(k_lm_head<4>, p16_lds(4, D));
   allow_lds(k_lm_head<8>, p16_lds(8, D));
   allow_lds(k_attn_softmax, size_t(p->cap) * sizeof(float));
+  allow_lds(k_attn_softmax_rows, size_t(p->cap) * sizeof(float));
 }
 
 // Row groups per tile for launches with one tile per wavefront (O and the
@@ -3643,7 +3698,13 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       else
         k_attn_qk<<<dim3(c.kv_heads, p->cap / 64, B), kBlock, 0, s>>>(aa);
       break;
-    case 2: k_attn_softmax<<<dim3(c.q_heads, B), kSoftmaxThreads, size_t(p->cap) * sizeof(float), s>>>(aa); break;
+    case 2:
+      // Several rows: one wavefront per (query head, row).
+      if (B > 1)
+        k_attn_softmax_rows<<<dim3(c.q_heads, B), 64, size_t(p->cap) * sizeof(float), s>>>(aa);
+      else
+        k_attn_softmax<<<dim3(c.q_heads, B), kSoftmaxThreads, size_t(p->cap) * sizeof(float), s>>>(aa);
+      break;
     case 3:
       if (B == 1)
         k_attn_pv<<<dim3(c.kv_heads * (kHeadDim / kPvFeatures), 1), kPvThreads, kPvLds, s>>>(aa);
