@@ -93,6 +93,7 @@ def other_configs(device, queue, model, cfg, seed, pplan, long_prompt):
         # Config 3: greedy decode of 512 tokens after the exact prompt pass
         # of a 4096-id prompt; visible keys grow from 4097 to 4607.
         n, max_new = len(long_prompt), 512
+        pplan.prefill(long_prompt)  # warm: allocates the exact pass's chunk buffers
         ea, eb = Event(device), Event(device)
         queue.drain()
         ea.record(queue)
