@@ -58,6 +58,50 @@ def test_prefill_projection_within_one_ulp(device, queue, oracle, rows, in_w, ou
     assert np.mean(err <= bf16_ulp(exact)) > 0.9999
 
 
+def permuted_np(k, P):
+    """Position of input k in the P-permuted order (prefill.h `permuted`)."""
+    block = 8 * P
+    return (k // block) * block + (k % P) * 8 + (k % block) // P
+
+
+def test_prefill_gate_up_silu_of_every_bf16_gate(device, queue, oracle):
+    """The gate/up GEMM's SiLU * up against the oracle's SiluMultiply for
+    every BF16 gate value that is +0 or finite and normal (65,025 bit
+    patterns).  Rows of x carry the patterns in inputs 0-127 and 1.0 in input
+    128; gate row f selects input f % 128 and up row f input 128, each with
+    weight 1.0, so every MFMA sum is exact and act[m][f] = SiLU(x[m][f % 128])
+    rounded as the contract rounds it.  512 rows x 65,536 gate/up columns is
+    512 tiles of 256 x 256: the 256 x 256 tile kernel, whose SiLU comes from
+    the table built per device, and its P32-permuted activation order."""
+    from dolittle_amd import _lib
+    K, F, rows = 256, 32768, 512
+    patterns = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    exponent = (patterns >> 7) & 0xFF
+    # -0 is left out: a dot product adds +0 terms to it, so its gate is +0.
+    usable = ((exponent != 0) | ((patterns & 0x7F) == 0)) & (exponent != 0xFF) & (patterns != 0x8000)
+    x = np.zeros((rows, K), np.uint16)
+    x[:, :128] = np.where(usable, patterns, 0).reshape(rows, 128)
+    x[:, 128] = 0x3F80
+    f = np.arange(F)
+    w = np.zeros((2 * F, K), np.uint16)
+    w[4 * (f // 2) + f % 2, f % 128] = 0x3F80       # gate rows: g 2j, g 2j+1
+    w[4 * (f // 2) + 2 + f % 2, 128] = 0x3F80       # up rows: u 2j, u 2j+1
+    bx, bw = device.upload_array(queue, x.reshape(-1)), device.upload_array(queue, w.reshape(-1))
+    nbytes = C.c_uint64()
+    _lib.call("dl_projection_packed_bytes", 2 * F, K, C.byref(nbytes))
+    packed = device.allocate(nbytes.value)
+    _lib.call("dl_projection_pack", queue.handle, bw.ptr(), packed.ptr(), 2 * F, K)
+    out, work = device.allocate(rows * F * 2), device.allocate(rows * K * 2)
+    _lib.call("dl_prefill_gate_up", queue.handle, bx.ptr(), packed.ptr(), out.ptr(), work.ptr(), rows, K, F)
+    queue.drain()
+    act = queue.read(out, np.uint16, rows * F).reshape(rows, F)[:, permuted_np(f, 32)]
+    gate = x[:, f % 128]
+    want = oracle.silu_multiply(gate.reshape(-1), np.full(gate.size, 0x3F80, np.uint16)).reshape(rows, F)
+    check = usable.reshape(rows, 128)[:, f % 128]
+    assert int(usable.sum()) == 65536 - 256 - 254 - 1 and int(check.sum()) == int(usable.sum()) * (F // 128)
+    assert np.array_equal(act[check], want[check])
+
+
 def test_prefill_projection_rejects_ragged_shapes(device, queue):
     from dolittle_amd import InvalidArgument, _lib
     buf = device.allocate(1 << 20)
