@@ -409,8 +409,8 @@ __device__ __forceinline__ bool norm_stage_pass(const uint16_t* __restrict__ h, 
   return true;
 }
 
-// norm_stage_pass over B rows, R G at a time (R = 2 rows per group, 1 for
-// a single row) (scratch is reused between
+// norm_stage_pass over B rows, R G at a time (R = 1 row per group while the
+// G groups cover the B rows in one pass, else 2) (scratch is reused between
 // passes behind a barrier); G = threads / 128 of the calling workgroup.
 // Rows have width kNormWidth.  Returns false, before any math, when the
 // loop word `active` (read in the first pass, as in stage_rows) is zero.
@@ -418,7 +418,7 @@ template <int B, bool S16, bool S32, int G, class Issue>
 __device__ __forceinline__ bool norm_stage(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
                                            float eps, float* xs16, float* xs32, float* scratch, Issue&& issue,
                                            const uint32_t* active = nullptr) {
-  constexpr int R = B == 1 ? 1 : 2;
+  constexpr int R = B <= G ? 1 : 2;
   auto none = [] {};
 #pragma unroll
   for (int b0 = 0; b0 < B; b0 += R * G) {

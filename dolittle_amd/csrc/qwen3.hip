@@ -1497,6 +1497,7 @@ struct Tagged {
   uint64_t* words;
   uint32_t tag;
   int k, v, att;  // word offsets of the k row, the new v row and the attention output (q at 0)
+  int row;        // words per row (row b's words start at words + b * row)
 };
 
 __device__ __forceinline__ void tagged_put(uint64_t* w, uint32_t data, uint32_t tag) {
@@ -2101,14 +2102,15 @@ struct AttnOArgs {
 // The O workgroup `wg` of `o_workgroups`: waits on hs's go lines (or, with
 // `tg`, reads the attention output as tagged words); the last to finish
 // zeroes lines [0, hs.exit] (and with `tg` advances the epoch word `epoch`).
-template <bool kTagged = false>
+template <bool kTagged = false, int B = 1>
 __device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int o_workgroups, const Handoff& hs,
                                              const Tagged* tg = nullptr, uint32_t* epoch = nullptr) {
+  static_assert(B == 1 || kTagged, "several rows come as tagged words");
   constexpr int P = 16, RW = 64 / P;
   // 16-byte aligned: the attention's static arrays come first, and the chain
   // reads the staged inputs 16 bytes at a time.
   extern __shared__ __align__(16) float xs[];
-  __shared__ float epi[kOWaves * RW];
+  __shared__ float epi[kOWaves * RW * B];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int tile = wg * kOWaves + wave;
   const u32x4* src = a.w + static_cast<uint64_t>(tile) * (kOChunks * 64) + lane;
@@ -2122,12 +2124,17 @@ __device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int 
   // before any is used.
   constexpr int kWords = kOChunks * 8 * P / 2 / kAttnThreads;
   static_assert(kWords * 2 * kAttnThreads == kOChunks * 8 * P, "the O input row splits evenly over the threads");
-  uint32_t v[kWords];
+  // Row b's words follow row 0's at b * qkvo_tagged_words (the per-row
+  // stride `tg->row`).
+  uint32_t v[B * kWords];
   if constexpr (kTagged) {
-    const uint64_t* src[kWords];
+    const uint64_t* src[B * kWords];
 #pragma unroll
-    for (int k = 0; k < kWords; ++k) src[k] = tg->words + tg->att + threadIdx.x + k * kAttnThreads;
-    tagged_gather<kWords>(src, tg->tag, handoff_line(hs, hs.failure), v);
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+      for (int k = 0; k < kWords; ++k)
+        src[b * kWords + k] = tg->words + b * tg->row + tg->att + threadIdx.x + k * kAttnThreads;
+    tagged_gather<B * kWords>(src, tg->tag, handoff_line(hs, hs.failure), v);
   } else {
     handoff_wait(hs);
     const uint32_t* x32 = reinterpret_cast<const uint32_t*>(a.x);
@@ -2136,19 +2143,23 @@ __device__ __forceinline__ void o_prefetched(const ResidualArgs& a, int wg, int 
       v[k] = __hip_atomic_load(x32 + threadIdx.x + k * kAttnThreads, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 #pragma unroll
-  for (int k = 0; k < kWords; ++k) {
-    const int wi = threadIdx.x + k * kAttnThreads;
-    stage_put<P>(xs, a.I, 0, 2 * wi, dl_bf16_lo(v[k]));
-    stage_put<P>(xs, a.I, 0, 2 * wi + 1, dl_bf16_hi(v[k]));
-  }
+  for (int b = 0; b < B; ++b)
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) {
+      const int wi = threadIdx.x + k * kAttnThreads;
+      stage_put<P>(xs, a.I, b, 2 * wi, dl_bf16_lo(v[b * kWords + k]));
+      stage_put<P>(xs, a.I, b, 2 * wi + 1, dl_bf16_hi(v[b * kWords + k]));
+    }
   __syncthreads();
   const int L = a.I / P, stride = L + kXsPad, bstride = P * stride;
   const float* xt = xs + (lane % P) * stride;
-  float acc[1] = {0.0f};
+  float acc[B];
 #pragma unroll
-  for (int s = 0; s < kOChunks; ++s) chain_step<1>(w[s], xt, bstride, s, acc);
-  chain_merge<P, 1>(acc);
-  residual_outputs<P, 1>(a, acc, tile, lane, epi + wave * RW, pos, false, false, 0u);
+  for (int b = 0; b < B; ++b) acc[b] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kOChunks; ++s) chain_step<B>(w[s], xt, bstride, s, acc);
+  chain_merge<P, B>(acc);
+  residual_outputs<P, B>(a, acc, tile, lane, epi + wave * RW * B, pos, false, false, 0u);
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t done = __hip_atomic_fetch_add(handoff_line(hs, hs.exit), 1u, __ATOMIC_RELAXED,
@@ -2224,11 +2235,12 @@ struct QkvAttnOArgs {
   uint32_t* sync;
 };
 
+template <int B>
 __device__ __forceinline__ void qkv_phase(const QkvArgs& a, const Tagged& tg) {
   constexpr int W = kQkvWaves;
   extern __shared__ __align__(16) float lds[];
   float* xs16 = lds;
-  float* xs32 = lds + staged_floats(16, kWholeTileInputs);
+  float* xs32 = lds + B * staged_floats(16, kWholeTileInputs);
   __shared__ float scratch[W * 40];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int q_tiles = a.QW / 4, k_tiles = a.KW / 2;
@@ -2242,7 +2254,7 @@ __device__ __forceinline__ void qkv_phase(const QkvArgs& a, const Tagged& tg) {
                            : a.w + q_tiles * q_chunks + (is_v ? k_tiles : 0) * k_chunks + kt * k_chunks) + lane;
   constexpr int SQ = kWholeTileInputs / 128, SK = kWholeTileInputs / 256;
   u32x4 w[SQ];
-  if (!norm_stage<1, true, true, W / 2>(
+  if (!norm_stage<B, true, true, W / 2>(
           a.h, a.norm, a.eps, xs16, xs32, scratch,
           [&] {
 #pragma unroll
@@ -2255,49 +2267,64 @@ __device__ __forceinline__ void qkv_phase(const QkvArgs& a, const Tagged& tg) {
     for (int s = SK; s < SQ; ++s) w[s] = load_stream(src + s * 64);
   }
   __syncthreads();
-  float acc[1] = {0.0f};
+  float acc[B];
+#pragma unroll
+  for (int b = 0; b < B; ++b) acc[b] = 0.0f;
   if (is_q) {
     constexpr int P = 16, stride = kWholeTileInputs / P + kXsPad;
     const float* xt = xs16 + (lane % P) * stride;
 #pragma unroll
-    for (int s = 0; s < SQ; ++s) chain_step<1>(w[s], xt, P * stride, s, acc);
-    chain_merge<P, 1>(acc);
-    // Lanes 0, 16, 32, 48 hold rows 4 t .. 4 t + 3: two words.
-    const uint32_t y = bf16_bits(acc[0]);
-    const uint32_t y1 = __shfl_down(y, 16, 64);
-    if (lane == 0 || lane == 32) tagged_put(tg.words + tile * 2 + lane / 32, y | (y1 << 16), tg.tag);
+    for (int s = 0; s < SQ; ++s) chain_step<B>(w[s], xt, P * stride, s, acc);
+    chain_merge<P, B>(acc);
+    // Lanes 0, 16, 32, 48 hold rows 4 t .. 4 t + 3: two words per row.
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const uint32_t y = bf16_bits(acc[b]);
+      const uint32_t y1 = __shfl_down(y, 16, 64);
+      if (lane == 0 || lane == 32) tagged_put(tg.words + b * tg.row + tile * 2 + lane / 32, y | (y1 << 16), tg.tag);
+    }
   } else {
     constexpr int P = 32, stride = kWholeTileInputs / P + kXsPad;
     const float* xt = xs32 + (lane % P) * stride;
 #pragma unroll
-    for (int s = 0; s < SK; ++s) chain_step<1>(w[s], xt, P * stride, s, acc);
-    chain_merge<P, 1>(acc);
-    // Lanes 0 and 32 hold rows 2 kt and 2 kt + 1: one word.
-    const uint32_t y = bf16_bits(acc[0]);
-    const uint32_t y1 = __shfl_down(y, 32, 64);
-    if (is_v && lane % P == 0)
-      a.v_cache[static_cast<uint64_t>(kt * 2 + lane / P) * a.cap + a.ctl->position] = static_cast<uint16_t>(y);
-    if (lane == 0) tagged_put(tg.words + (is_v ? tg.v : tg.k) + kt, y | (y1 << 16), tg.tag);
+    for (int s = 0; s < SK; ++s) chain_step<B>(w[s], xt, P * stride, s, acc);
+    chain_merge<P, B>(acc);
+    // Lanes 0 and 32 hold rows 2 kt and 2 kt + 1: one word per row.  Row b's
+    // new V values go to its cache column as k_qkv writes them.
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const uint32_t y = bf16_bits(acc[b]);
+      const uint32_t y1 = __shfl_down(y, 32, 64);
+      if (is_v && lane % P == 0)
+        a.v_cache[b * a.cache_seq_stride + static_cast<uint64_t>(kt * 2 + lane / P) * a.cap + a.ctl->position] =
+            static_cast<uint16_t>(y);
+      if (lane == 0) tagged_put(tg.words + b * tg.row + (is_v ? tg.v : tg.k) + kt, y | (y1 << 16), tg.tag);
+    }
   }
 }
 
+template <int B>
 __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_qkv_attn_o(QkvAttnOArgs a) {
   const uint32_t heads = static_cast<uint32_t>(a.attn.q_heads) * kAttnSplit;
   const uint32_t nq = static_cast<uint32_t>(a.qkv.QW / 4 + a.qkv.KW) / kQkvWaves;
   Handoff hs = kQkvoLayout;
   hs.words = a.sync;
   uint32_t* epoch = handoff_line(hs, kQkvoEpoch);
-  const Tagged tg{a.tagged, __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u, a.qkv.QW / 2,
-                  a.qkv.QW / 2 + a.qkv.KW / 2, a.qkv.QW / 2 + a.qkv.KW};
+  Tagged tg{a.tagged, __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u, a.qkv.QW / 2,
+            a.qkv.QW / 2 + a.qkv.KW / 2, a.qkv.QW / 2 + a.qkv.KW, qkvo_tagged_words(a.qkv.QW, a.qkv.KW)};
   if (blockIdx.x < nq) {
-    qkv_phase(a.qkv, tg);
+    qkv_phase<B>(a.qkv, tg);
     return;
   }
-  if (blockIdx.x < nq + heads) {
-    attn_fused_body<true, true, kAttnSplit>(a.attn, blockIdx.x - nq, 0, &hs, &tg);
+  if (blockIdx.x < nq + B * heads) {
+    // Row-major over (row, head slot): row b's heads read and write row b's
+    // tagged words.
+    const uint32_t i = blockIdx.x - nq, b = i / heads;
+    tg.words += b * tg.row;
+    attn_fused_body<true, true, kAttnSplit>(a.attn, i % heads, b, &hs, &tg);
     return;
   }
-  o_prefetched<true>(a.o, blockIdx.x - nq - heads, gridDim.x - nq - heads, hs, &tg, epoch);
+  o_prefetched<true, B>(a.o, blockIdx.x - nq - B * heads, gridDim.x - nq - B * heads, hs, &tg, epoch);
 }
 
 // ------------------------------------------------------------ gate/up GEMV
@@ -3564,6 +3591,7 @@ void prepare_kernels_all(dl_plan* p) {
   allow_lds(k_lm_head<8>, p16_lds(8, D));
   allow_lds(k_attn_softmax, size_t(p->cap) * sizeof(float));
   allow_lds(k_attn_softmax_rows, size_t(p->cap) * sizeof(float));
+  allow_lds(k_qkv_attn_o<2>, qkv_lds(2, D));
 }
 
 // Row groups per tile for launches with one tile per wavefront (O and the
@@ -3723,17 +3751,21 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
         k_attn_fused<1><<<dim3(c.q_heads, B), kAttnThreads, 0, s>>>(aa);
       break;
     case 12: {
-      // QKV + attention + O of one row (fused_qkv_attention_o decides when it
-      // applies).
+      // QKV + attention + O of one or two rows (fused_qkv_attention_o decides
+      // when it applies).
       QkvArgs qa{ctl, r.h, m->input_norm[l], reinterpret_cast<const u32x4*>(m->qkv[l]), r.q_raw, r.k_raw, vc,
                  r.v_append_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps};
       ResidualArgs oa{ctl, r.att, reinterpret_cast<const u32x4*>(m->o[l]), r.h, nullptr, nullptr, QW, D,
                       static_cast<int>(p->cap), static_cast<int>(l), 0, r.same_sequence, r.sequence};
       const int qkv_workgroups = (QW / 4 + KW) / kQkvWaves;
       const int o_workgroups = D / (64 / 16) / kOWaves;
-      const size_t lds = (staged_floats(16, D) + staged_floats(32, D)) * sizeof(float);
-      k_qkv_attn_o<<<qkv_workgroups + c.q_heads * kAttnSplit + o_workgroups, kAttnThreads, lds, s>>>(
-          QkvAttnOArgs{qa, aa, oa, p->qkvo_tagged, p->qkvo_sync});
+      const int grid = qkv_workgroups + static_cast<int>(B) * c.q_heads * kAttnSplit + o_workgroups;
+      const size_t lds = qkv_lds(static_cast<int>(B), D);
+      const QkvAttnOArgs args{qa, aa, oa, p->qkvo_tagged, p->qkvo_sync};
+      if (B == 1)
+        k_qkv_attn_o<1><<<grid, kAttnThreads, lds, s>>>(args);
+      else
+        k_qkv_attn_o<2><<<grid, kAttnThreads, lds, s>>>(args);
       break;
     }
     case 10: {
@@ -3839,13 +3871,15 @@ bool fused_attention_o(const dl_plan* p) {
   return p->batch == 1 && QW / (8 * 16) == dl::kOChunks && tiles % dl::kOWaves == 0;
 }
 
-// Whether a short-context step also folds the QKV projection into that
-// launch (k_qkv_attn_o): the QKV tile shapes of the batch-1 whole-tile path
-// (hidden width kWholeTileInputs) in whole workgroups.
+// Whether a short-context step runs QKV, attention and O as one launch
+// (k_qkv_attn_o): one or two rows, the O tile shape of k_attn_o and the QKV
+// tile shapes of the batch-1 whole-tile path (hidden width
+// kWholeTileInputs) in whole workgroups.
 bool fused_qkv_attention_o(const dl_plan* p) {
   const auto& c = p->model->cfg;
-  const int QW = c.q_heads * c.head_dim, KW = c.kv_heads * c.head_dim;
-  return fused_attention_o(p) && c.hidden == dl::kWholeTileInputs && (QW / 4 + KW) % dl::kQkvWaves == 0;
+  const int QW = c.q_heads * c.head_dim, KW = c.kv_heads * c.head_dim, tiles = c.hidden / (64 / 16);
+  return (p->batch == 1 || p->batch == 2) && QW / (8 * 16) == dl::kOChunks && tiles % dl::kOWaves == 0 &&
+         c.hidden == dl::kWholeTileInputs && (QW / 4 + KW) % dl::kQkvWaves == 0;
 }
 
 // Records one decode step.  `short_context` selects the fused attention
@@ -4047,8 +4081,9 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
     dl::check_hip(hipMemsetAsync(p->attn_sync, 0, dl::kSyncWords * 4, queue->stream), "hand-off clear");
     p->qkvo_sync = p->alloc<uint32_t>(dl::kQkvoSyncWords);
     dl::check_hip(hipMemsetAsync(p->qkvo_sync, 0, dl::kQkvoSyncWords * 4, queue->stream), "hand-off clear");
-    p->qkvo_tagged = p->alloc<uint64_t>(dl::qkvo_tagged_words(QW, KW));
-    dl::check_hip(hipMemsetAsync(p->qkvo_tagged, 0, dl::qkvo_tagged_words(QW, KW) * 8, queue->stream), "hand-off clear");
+    p->qkvo_tagged = p->alloc<uint64_t>(B * dl::qkvo_tagged_words(QW, KW));
+    dl::check_hip(hipMemsetAsync(p->qkvo_tagged, 0, B * dl::qkvo_tagged_words(QW, KW) * 8, queue->stream),
+                  "hand-off clear");
     p->partial_keys = p->alloc<uint64_t>(B * 1024);
     p->partial_flags = p->alloc<uint32_t>(B * 1024);
     p->tokens = p->alloc<uint32_t>(cap);
