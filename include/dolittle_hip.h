@@ -503,7 +503,9 @@ int dl_plan_decode_steps(dl_plan* plan, uint32_t steps);
  * snapshots the live control block into a separate always-active one;
  * launch_kernel then enqueues `count` instances of one decode-step kernel
  * (0 QKV, 1 attention scores, 2 softmax, 3 PV, 4 O + residual, 5 gate/up,
- * 6 down + residual, 7 LM head, 8 short-context fused attention), cycling
+ * 6 down + residual, 7 LM head, 8 short-context fused attention, 10
+ * attention + O of one row, 12 QKV + attention + O of one or two rows),
+ * cycling
  * through layers from `first_layer`
  * so repeated launches stream distinct weights, on the plan's queue. */
 int dl_plan_bench_prepare(dl_plan* plan);

@@ -78,6 +78,46 @@ def test_capture_and_steering_full_size(full_model):
     assert not np.array_equal(plain_capture, steered_capture)
 
 
+def test_capture_and_steering_two_rows_past_1k_keys(full_model):
+    """The same semantics at 1100-1106 keys, where a step of one or two rows
+    runs QKV, attention and O as one launch (below 1536 keys) and each
+    attention workgroup reads its own row's cache over several 64-key
+    blocks: batch 2 with sequence 1 steered at block 24 equals the two
+    batch-1 runs (tokens, last logits, every captured block-24 row)."""
+    from dolittle_amd.qwen3 import Plan
+    p, new, layer = prompt(11, 1100), 6, 24
+    rng = np.random.default_rng(12)
+    v = rng.standard_normal(4096).astype(np.float32)
+    v = (v / np.float32(np.linalg.norm(v.astype(np.float64)))).astype(np.float32) * np.float32(8.0)
+    consumed, cap = len(p) + new, len(p) + new + 1
+
+    def run(batch, steer_seq):
+        plan = Plan(full_model, batch=batch, capacity=cap)
+        plan.set_capture(layer)
+        if steer_seq is not None:
+            plan.set_steering(steer_seq, layer, v)
+        plan.prefill(p)
+        plan.generate(p, new)
+        tokens, results = plan.collect()
+        assert all(r["generated"] == new and r["status"] == 0 for r in results)
+        return plan, tokens
+
+    plain, plain_tokens = run(1, None)
+    plain_capture, plain_logits = plain.read_capture(0, 0, consumed), plain.logits(0)
+    del plain
+    steered, steered_tokens = run(1, 0)
+    steered_capture, steered_logits = steered.read_capture(0, 0, consumed), steered.logits(0)
+    del steered
+    both, tokens = run(2, 1)
+    assert tokens[0].tolist() == plain_tokens[0].tolist()
+    assert tokens[1].tolist() == steered_tokens[0].tolist()
+    assert np.array_equal(both.logits(0), plain_logits)
+    assert np.array_equal(both.logits(1), steered_logits)
+    assert np.array_equal(both.read_capture(0, 0, consumed), plain_capture)
+    assert np.array_equal(both.read_capture(1, 0, consumed), steered_capture)
+    assert not np.array_equal(plain_capture, steered_capture)
+
+
 def test_exact_prefill_equals_token_loop_full_size(full_model):
     from dolittle_amd.qwen3 import Plan
     p, new = prompt(4, 600), 6
