@@ -312,7 +312,7 @@ struct QkvArgs {
 
 // Part: kQkvAll projects Q, K and V; at eight rows both staged layouts do
 // not fit in LDS together, so kQkvQ (Q rows, P = 16 layout) and kQkvKV (K
-// and V rows, P = 32 layout) run as two launches.
+// and V rows, P = 32 layout) run in separate workgroups (k_qkv_roles).
 enum QkvPart : int { kQkvAll = 0, kQkvQ = 1, kQkvKV = 2 };
 // Input width of the batch-1 GEMV paths that hold a wavefront's whole weight
 // tile in registers (Qwen3-8B's hidden width).
@@ -323,10 +323,11 @@ constexpr int qkv_waves(int rows, int part) { return part == kQkvAll ? kWaves : 
 // rows (the same tile's weights, read by Split wavefronts): with one tile
 // per wavefront the chain length per wavefront, not the CU count, bounds
 // these launches at eight rows.
-template <int B, int Part = kQkvAll, int Split = 1>
-// Two wavefronts per SIMD at least: the batch-1 whole-tile path holds 128
-// weight VGPRs, and a grid of one tile per wavefront must be resident at once.
-__global__ __launch_bounds__(qkv_waves(B, Part) * 64) __attribute__((amdgpu_waves_per_eu(2))) void k_qkv(QkvArgs a) {
+// `block` of `blocks` is the workgroup's place among the launch's
+// workgroups of this part (k_qkv_roles runs the Q and K/V parts of eight
+// rows in one launch).
+template <int B, int Part, int Split>
+__device__ __forceinline__ void qkv_rows(const QkvArgs& a, int block, int blocks) {
   constexpr int W = qkv_waves(B, Part);
   constexpr int BR = B / Split;
   static_assert(B % Split == 0, "rows split evenly");
@@ -349,9 +350,9 @@ __global__ __launch_bounds__(qkv_waves(B, Part) * 64) __attribute__((amdgpu_wave
   };
   const int tile_begin = Part == kQkvKV ? q_tiles : 0, tile_end = Part == kQkvQ ? q_tiles : total;
   const int items = (tile_end - tile_begin) * Split;
-  const int first = blockIdx.x * W + wave;
+  const int first = block * W + wave;
   if constexpr (B == 1 && Part == kQkvAll && Split == 1) {
-    if (gridDim.x * W >= static_cast<unsigned>(items) && a.D == kWholeTileInputs) {
+    if (blocks * W >= items && a.D == kWholeTileInputs) {
       // One tile per wavefront, held in registers (32 chunks per lane for a
       // Q tile, 16 for K or V): the first 16 chunks are issued before the
       // prologue, the rest right after it, and the chains run from
@@ -419,14 +420,14 @@ __global__ __launch_bounds__(qkv_waves(B, Part) * 64) __attribute__((amdgpu_wave
     return;
   __syncthreads();
   const uint64_t pos = a.ctl->position;
-  for (int item = first; item < items; item += gridDim.x * W) {
+  for (int item = first; item < items; item += blocks * W) {
     const int tile = tile_begin + item / Split, b0 = (item % Split) * BR;
     const bool is_q = tile < q_tiles;
     int kt = tile - q_tiles;
     const bool is_v = !is_q && kt >= k_tiles;
     if (is_v) kt -= k_tiles;
     const u32x4* src = tile_src(tile);
-    const int next = item + gridDim.x * W;
+    const int next = item + blocks * W;
     const u32x4* next_src = next < items ? tile_src(tile_begin + next / Split) : nullptr;
     float acc[BR];
     if (Part == kQkvQ || (Part == kQkvAll && is_q)) {
@@ -450,6 +451,27 @@ __global__ __launch_bounds__(qkv_waves(B, Part) * 64) __attribute__((amdgpu_wave
       }
     }
   }
+}
+
+// Two wavefronts per SIMD at least: the batch-1 whole-tile path holds 128
+// weight VGPRs, and a grid of one tile per wavefront must be resident at once.
+template <int B, int Part = kQkvAll, int Split = 1>
+__global__ __launch_bounds__(qkv_waves(B, Part) * 64) __attribute__((amdgpu_waves_per_eu(2))) void k_qkv(QkvArgs a) {
+  qkv_rows<B, Part, Split>(a, blockIdx.x, gridDim.x);
+}
+
+// The Q part (workgroups [0, q_blocks)) and the K/V part (the rest) of B
+// rows in one launch: a compute unit whose Q workgroup is done takes a K/V
+// workgroup without waiting for the whole Q grid.  Each workgroup stages only
+// its part's layout, so both fit the LDS that one of them takes.
+template <int B, int Split>
+__global__ __launch_bounds__(qkv_waves(B, kQkvQ) * 64) __attribute__((amdgpu_waves_per_eu(2))) void k_qkv_roles(
+    QkvArgs a, int q_blocks) {
+  static_assert(qkv_waves(B, kQkvQ) == qkv_waves(B, kQkvKV), "both parts use the same workgroup shape");
+  if (static_cast<int>(blockIdx.x) < q_blocks)
+    qkv_rows<B, kQkvQ, Split>(a, blockIdx.x, q_blocks);
+  else
+    qkv_rows<B, kQkvKV, Split>(a, blockIdx.x - q_blocks, gridDim.x - q_blocks);
 }
 
 // Orders one wavefront's LDS writes before its own later LDS reads (and the
@@ -3571,8 +3593,7 @@ void prepare_kernels_all(dl_plan* p) {
   allow_lds(k_qkv<1>, qkv_lds(1, D));
   allow_lds(k_qkv<2>, qkv_lds(2, D));
   allow_lds(k_qkv<4>, qkv_lds(4, D));
-  allow_lds(k_qkv<8, kQkvQ, 2>, qkv_lds(8, D, kQkvQ));
-  allow_lds(k_qkv<8, kQkvKV, 2>, qkv_lds(8, D, kQkvKV));
+  allow_lds(k_qkv_roles<8, 2>, std::max(qkv_lds(8, D, kQkvQ), qkv_lds(8, D, kQkvKV)));
   allow_lds(k_residual_chunked<32, 4>, p32_lds(4, kChunkInputs));
   allow_lds(k_residual_chunked<32, 8>, p32_lds(8, kChunkInputs));
   allow_lds(k_residual<16, 1>, p16_lds(1, QW));
@@ -3606,6 +3627,17 @@ void launch_qkv(dl_plan* p, hipStream_t s, const dl::QkvArgs& a) {
   constexpr int waves = dl::qkv_waves(G, Part);
   constexpr int split = kRowSplit(G, Part == dl::kQkvAll ? 0 : 1);
   dl::k_qkv<G, Part, split><<<p->grid_for(0, tiles * split, lds, waves), waves * 64, lds, s>>>(a);
+}
+// The Q and K/V parts of G rows as one launch (k_qkv_roles), each part with
+// the grid launch_qkv gives it.
+template <int G>
+void launch_qkv_roles(dl_plan* p, hipStream_t s, const dl::QkvArgs& a) {
+  constexpr int waves = dl::qkv_waves(G, dl::kQkvQ);
+  constexpr int split = kRowSplit(G, 1);
+  const unsigned q_blocks = p->grid_for(0, uint64_t(a.QW / 4) * split, qkv_lds(G, a.D, dl::kQkvQ), waves);
+  const unsigned kv_blocks = p->grid_for(0, uint64_t(a.KW) * split, qkv_lds(G, a.D, dl::kQkvKV), waves);
+  const size_t lds = std::max(qkv_lds(G, a.D, dl::kQkvQ), qkv_lds(G, a.D, dl::kQkvKV));
+  dl::k_qkv_roles<G, split><<<q_blocks + kv_blocks, waves * 64, lds, s>>>(a, static_cast<int>(q_blocks));
 }
 template <int G>
 void launch_down_chunked(dl_plan* p, hipStream_t s, const dl::ResidualArgs& a) {
@@ -3706,8 +3738,7 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
                    r.q_raw + uint64_t(r0) * QW, r.k_raw + uint64_t(r0) * KW, vc + r0 * r.v_append_stride,
                    r.v_append_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps};
         if (g == 8) {
-          launch_qkv<8, kQkvQ>(p, s, qa);
-          launch_qkv<8, kQkvKV>(p, s, qa);
+          launch_qkv_roles<8>(p, s, qa);
         } else if (g == 4) {
           launch_qkv<4>(p, s, qa);
         } else if (g == 2) {
