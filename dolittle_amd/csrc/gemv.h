@@ -222,10 +222,15 @@ __device__ __forceinline__ void chain_tile_pipelined(const u32x4* __restrict__ s
     for (int j = 0; j < kBatch; ++j) chain_step<B>(wa[j], xt, bstride, k * kBatch + j, acc);
     __builtin_amdgcn_sched_barrier(0);
     // Past the tile's last batch: the next tile's first batch, or (no next
-    // tile) the batch just loaded again, which L2 still holds; a select, not
-    // a branch, so both register sets stay in place.
-    load(wa, k + 2 < batches ? src + (k + 2) * kBatch * 64
-                             : (has_next ? next_src : src + (k + 1) * kBatch * 64));
+    // tile) at one row nothing; at several rows the batch just loaded again,
+    // which L2 still holds: a select, not a branch, so both register sets
+    // stay in place (a branch there spills).
+    if constexpr (B == 1) {
+      if (k + 2 < batches || has_next) load(wa, k + 2 < batches ? src + (k + 2) * kBatch * 64 : next_src);
+    } else {
+      load(wa, k + 2 < batches ? src + (k + 2) * kBatch * 64
+                               : (has_next ? next_src : src + (k + 1) * kBatch * 64));
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) chain_step<B>(wb[j], xt, bstride, (k + 1) * kBatch + j, acc);
