@@ -67,13 +67,15 @@ __device__ __forceinline__ void stage_put(float* xs, int I, int b, int i, float 
 // after the vector loads are in flight, so a live step waits no longer.
 template <int P, class Issue>
 __device__ __forceinline__ bool stage_rows(const uint16_t* __restrict__ x, int I, int rows, float* xs,
-                                           Issue&& issue, int row_stride = 0, const uint32_t* active = nullptr) {
+                                           Issue&& issue, int row_stride = 0, const uint32_t* active = nullptr,
+                                           int valid = 1 << 30) {
   constexpr int kMaxChunks = 8;
   const int chunks = I / 8;
   const uint64_t stride = row_stride ? row_stride : I;
   const uint32_t live = active ? *active : 1u;
   for (int b = 0; b < rows; ++b) {
-    const u32x4* src = reinterpret_cast<const u32x4*>(x + static_cast<uint64_t>(b) * stride);
+    // Rows from `valid` on do not exist: their slots repeat the last row.
+    const u32x4* src = reinterpret_cast<const u32x4*>(x + static_cast<uint64_t>(b < valid ? b : valid - 1) * stride);
     u32x4 v[kMaxChunks];
 #pragma unroll
     for (int j = 0; j < kMaxChunks; ++j) {
@@ -111,10 +113,11 @@ __device__ __forceinline__ bool stage_rows(const uint16_t* __restrict__ x, int I
 // into the P-partial layout with a compile-time shape: each of the T
 // threads moves I / (8 T) 16-byte chunks per row, all B rows' loads issued
 // before any is converted.  `issue` runs after the loads (loads retire in
-// order).  Requires I % (8 T) == 0.
+// order).  Requires I % (8 T) == 0.  Only the first `rows` rows exist: the
+// others' slots are staged from the last of them and never stored from.
 template <int P, int B, int I, int T, class Issue>
 __device__ __forceinline__ void stage_block(const uint16_t* __restrict__ x, uint64_t row_stride, float* xs,
-                                            Issue&& issue) {
+                                            Issue&& issue, int rows = B) {
   constexpr int J = I / (8 * T);
   static_assert(J >= 1 && I % (8 * T) == 0, "block width must be a multiple of 8 per thread");
   u32x4 v[B][J];
@@ -122,7 +125,7 @@ __device__ __forceinline__ void stage_block(const uint16_t* __restrict__ x, uint
   for (int b = 0; b < B; ++b) {
 #pragma unroll
     for (int j = 0; j < J; ++j)
-      v[b][j] = reinterpret_cast<const u32x4*>(x + b * row_stride)[threadIdx.x + j * T];
+      v[b][j] = reinterpret_cast<const u32x4*>(x + (b < rows ? b : rows - 1) * row_stride)[threadIdx.x + j * T];
   }
   __builtin_amdgcn_sched_barrier(0);
   issue();
@@ -419,18 +422,20 @@ __device__ __forceinline__ bool norm_stage_pass(const uint16_t* __restrict__ h, 
 // passes behind a barrier); G = threads / 128 of the calling workgroup.
 // Rows have width kNormWidth.  Returns false, before any math, when the
 // loop word `active` (read in the first pass, as in stage_rows) is zero.
+// Only the first `rows` (at most B) rows exist and are read and staged; the
+// staged slots of the others are left as they are.
 template <int B, bool S16, bool S32, int G, class Issue>
 __device__ __forceinline__ bool norm_stage(const uint16_t* __restrict__ h, const uint16_t* __restrict__ gain,
                                            float eps, float* xs16, float* xs32, float* scratch, Issue&& issue,
-                                           const uint32_t* active = nullptr) {
+                                           const uint32_t* active = nullptr, int rows = B) {
   constexpr int R = B <= G ? 1 : 2;
   auto none = [] {};
 #pragma unroll
   for (int b0 = 0; b0 < B; b0 += R * G) {
     if (b0) {
       __syncthreads();
-      norm_stage_pass<R, S16, S32, G>(h, gain, eps, xs16, xs32, scratch, b0, B, none, nullptr);
-    } else if (!norm_stage_pass<R, S16, S32, G>(h, gain, eps, xs16, xs32, scratch, b0, B, issue, active)) {
+      norm_stage_pass<R, S16, S32, G>(h, gain, eps, xs16, xs32, scratch, b0, rows, none, nullptr);
+    } else if (!norm_stage_pass<R, S16, S32, G>(h, gain, eps, xs16, xs32, scratch, b0, rows, issue, active)) {
       return false;
     }
   }

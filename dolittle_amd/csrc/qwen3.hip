@@ -308,7 +308,23 @@ struct QkvArgs {
   uint64_t cache_seq_stride; // elements
   int D, QW, KW, cap;
   float eps;
+  // Rows of the launch that exist (a launch of a larger row template for
+  // fewer rows reads and writes only these; see live_rows).
+  int rows = 1 << 30;
 };
+
+// Rows that exist in a launch of the B-row kernels given the launch's `rows`
+// field.  Only the 4- and 8-row kernels run for fewer rows (the host takes
+// one or two rows with kernels of that size), so for B <= 2 this is B and
+// the row guards compile away.
+template <int B>
+__device__ __forceinline__ int live_rows(int rows) {
+  if constexpr (B <= 2) {
+    return B;
+  } else {
+    return rows < B ? rows : B;
+  }
+}
 
 // Part: kQkvAll projects Q, K and V; at eight rows both staged layouts do
 // not fit in LDS together, so kQkvQ (Q rows, P = 16 layout) and kQkvKV (K
@@ -411,12 +427,13 @@ __device__ __forceinline__ void qkv_rows(const QkvArgs& a, int block, int blocks
   FirstBatch fb{};
   // The prologue returns, after issuing its loads, when the loop is stopped
   // (grid-uniform flag).
+  const int rows = live_rows<B>(a.rows);
   if (!norm_stage<B, Part != kQkvKV, Part != kQkvQ, W / 2>(
           a.h, a.norm, a.eps, xs16, xs32, scratch,
           [&] {
             if (first < items) issue_first(tile_src(tile_begin + first / Split), lane, fb);
           },
-          &a.ctl->active))
+          &a.ctl->active, rows))
     return;
   __syncthreads();
   const uint64_t pos = a.ctl->position;
@@ -435,7 +452,8 @@ __device__ __forceinline__ void qkv_rows(const QkvArgs& a, int block, int blocks
       if (lane % 16 == 0) {
         const int row = tile * 4 + lane / 16;
 #pragma unroll
-        for (int b = 0; b < BR; ++b) a.q_out[(b0 + b) * a.QW + row] = bf16_bits(acc[b]);
+        for (int b = 0; b < BR; ++b)
+          if (b0 + b < rows) a.q_out[(b0 + b) * a.QW + row] = bf16_bits(acc[b]);
       }
     } else {
       chain_tile<32, BR>(src, xs32 + b0 * staged_floats(32, a.D), a.D, lane, acc, &fb, next_src);
@@ -443,6 +461,7 @@ __device__ __forceinline__ void qkv_rows(const QkvArgs& a, int block, int blocks
         const int row = kt * 2 + lane / 32;
 #pragma unroll
         for (int b = 0; b < BR; ++b) {
+          if (b0 + b >= rows) break;
           if (is_v)
             a.v_cache[(b0 + b) * a.cache_seq_stride + static_cast<uint64_t>(row) * a.cap + pos] = bf16_bits(acc[b]);
           else
@@ -1939,6 +1958,9 @@ struct ResidualArgs {
   // with same_sequence, consecutive positions of sequence `sequence`
   // (row r at ctl->position + r; chunked prompt pass).
   int same_sequence, sequence;
+  // Rows from row0 that exist (a launch of a larger row template for fewer
+  // rows reads and writes only these).
+  int rows = 1 << 30;
 };
 
 
@@ -1979,7 +2001,7 @@ __device__ __forceinline__ void residual_outputs(const ResidualArgs& a, const fl
       for (int b = 0; b < B; ++b) ep[(lane / P) * B + b] = acc[b];
     }
     wave_lds_sync();
-    if (lane < RW * B) finish(lane / B, lane % B, ep[lane]);
+    if (lane < RW * B && lane % B < live_rows<B>(a.rows)) finish(lane / B, lane % B, ep[lane]);
     wave_lds_sync();
   }
 }
@@ -2009,7 +2031,7 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual(ResidualArgs a)
           [&] {
             if (first < items) issue_first(a.w + (first / Split) * chunks, lane, fb);
           },
-          0, &a.ctl->active))
+          0, &a.ctl->active, live_rows<B>(a.rows)))
     return;
   __syncthreads();
   const uint64_t pos = a.ctl->position;
@@ -2029,6 +2051,7 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual(ResidualArgs a)
     } else {
       ResidualArgs part = a;
       part.row0 += b0;
+      part.rows -= b0;
       residual_outputs<P, BR>(part, acc, tile, lane, epi + wave * RW * BR, pos, steer, capture, steer_mask);
     }
   }
@@ -2072,7 +2095,8 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_residual_chunked(Residua
       stage_block<P, B, kChunkInputs, W * 64>(a.x + static_cast<uint64_t>(a.row0) * a.I + c * kChunkInputs, a.I, xs,
                                              [&] {
                                                if (c == 0 && active) issue_first(src, lane, fb);
-                                             });
+                                             },
+                                             live_rows<B>(a.rows));
       __syncthreads();
       if (active) {
         // The block width is passed as a run-time value (a.I / blocks): a
@@ -2358,6 +2382,7 @@ struct GateUpArgs {
   uint16_t* act;         // [B][F]
   int D, F;
   float eps;
+  int rows = 1 << 30;    // rows that exist (see QkvArgs::rows)
 };
 
 template <int B>
@@ -2379,7 +2404,7 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_gateup(GateUpArgs a) {
           [&] {
             if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
           },
-          &a.ctl->active))
+          &a.ctl->active, live_rows<B>(a.rows)))
     return;
   __syncthreads();
   (void)S;
@@ -2401,7 +2426,7 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_gateup(GateUpArgs a) {
         for (int b = 0; b < B; ++b) ep[(lane / 16) * B + b] = acc[b];
       }
       wave_lds_sync();
-      if (lane < 2 * B) {
+      if (lane < 2 * B && lane % B < live_rows<B>(a.rows)) {
         const int o = lane / B, b = lane % B;
         a.act[static_cast<uint64_t>(b) * a.F + tile * 2 + o] =
             bf16_bits(silu_times(rbf(ep[o * B + b]), rbf(ep[(2 + o) * B + b])));
@@ -2640,6 +2665,7 @@ struct HeadArgs {
   uint32_t V;
   float eps;
   int row0;                // first sequence of this launch's row group
+  int rows = 1 << 30;      // rows from row0 that exist (see QkvArgs::rows)
 };
 
 // Orders BF16 logits: key = (ordered value << 32) | ~id, so the maximum key
@@ -2685,10 +2711,11 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_lm_head(HeadArgs a) {
   const int first = blockIdx.x * W + wave;
   (void)S;
   FirstBatch fb{};
+  const int rows = live_rows<B>(a.rows);
   norm_stage<B, true, false, W / 2>(a.h + static_cast<uint64_t>(a.row0) * a.D, a.norm, a.eps, xs, nullptr, scratch,
                                     [&] {
     if (first < tiles) issue_first(a.w + first * chunks, lane, fb);
-  });
+  }, nullptr, rows);
   __syncthreads();
   uint64_t best[B];
   uint32_t flags[B];
@@ -2705,6 +2732,7 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_lm_head(HeadArgs a) {
       const uint32_t row = static_cast<uint32_t>(tile * 4 + lane / 16);
 #pragma unroll
       for (int b = 0; b < B; ++b) {
+        if (b >= rows) break;
         const uint16_t bits = bf16_bits(acc[b]);
         a.logits[static_cast<uint64_t>(a.row0 + b) * a.V + row] = bits;
         logit_key(bits, row, &best[b], &flags[b]);
@@ -2723,7 +2751,7 @@ __global__ __launch_bounds__(gemv_waves(B) * 64) void k_lm_head(HeadArgs a) {
     }
   }
   __syncthreads();
-  if (threadIdx.x < B) {
+  if (static_cast<int>(threadIdx.x) < rows) {
     const int b = threadIdx.x;
     uint64_t k = 0;
     uint32_t f = 0;
@@ -3563,17 +3591,21 @@ size_t qkv_lds(int rows, int D, int part = dl::kQkvAll) {
 size_t p16_lds(int rows, int I) { return size_t(rows) * dl::staged_floats(16, I) * 4; }
 size_t p32_lds(int rows, int I) { return size_t(rows) * dl::staged_floats(32, I) * 4; }
 
-// Calls f(row0, rows) over row groups of templated sizes 8, 4, 2, 1 not
-// above `limit`.
+// Calls f(row0, g, rows) over row groups: `limit` rows at a time, then the
+// remaining rows as one launch of the smallest templated size g (1, 2, 4
+// or 8, at most `limit`) that holds them, whose kernels read and write only
+// its `rows` rows.  So every group streams the weights once: 3 rows run the
+// 4-row kernels, 5 to 7 rows the 8-row kernels.
 template <class F>
 void for_row_groups(uint32_t batch, int limit, F&& f) {
   uint32_t row0 = 0;
-  for (int g = 8; g >= 1; g /= 2) {
-    if (g > limit) continue;
-    while (batch - row0 >= static_cast<uint32_t>(g)) {
-      f(row0, g);
-      row0 += g;
-    }
+  while (row0 < batch) {
+    const uint32_t rest = batch - row0;
+    int g = 1;
+    while (static_cast<uint32_t>(g) < rest && g < limit) g *= 2;
+    const uint32_t rows = rest < static_cast<uint32_t>(g) ? rest : static_cast<uint32_t>(g);
+    f(row0, g, static_cast<int>(rows));
+    row0 += rows;
   }
 }
 
@@ -3733,10 +3765,10 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
         launch_xgemm<32, kXgKV>(s, kva);
         break;
       }
-      for_row_groups(B, kQkvRows, [&](uint32_t r0, int g) {
+      for_row_groups(B, kQkvRows, [&](uint32_t r0, int g, int rows) {
         QkvArgs qa{ctl, r.h + uint64_t(r0) * D, m->input_norm[l], reinterpret_cast<const u32x4*>(m->qkv[l]),
                    r.q_raw + uint64_t(r0) * QW, r.k_raw + uint64_t(r0) * KW, vc + r0 * r.v_append_stride,
-                   r.v_append_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps};
+                   r.v_append_stride, D, QW, KW, static_cast<int>(p->cap), c.rms_eps, rows};
         if (g == 8) {
           launch_qkv_roles<8>(p, s, qa);
         } else if (g == 4) {
@@ -3817,10 +3849,10 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
             s, XgemmArgs{ctl, r.att, oa.w, static_cast<int>(B), D, QW, 0, nullptr, nullptr, 0, 0, 0, oa});
         break;
       }
-      for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
+      for_row_groups(B, kWideRows, [&](uint32_t r0, int g, int rows) {
         ResidualArgs oa{ctl, r.att, reinterpret_cast<const u32x4*>(m->o[l]), r.h, nullptr, nullptr, QW, D,
                         static_cast<int>(p->cap), static_cast<int>(l), static_cast<int>(r0), r.same_sequence,
-                        r.sequence};
+                        r.sequence, rows};
         if (g == 8) launch_residual<16, 8>(p, s, 4, oa);
         else if (g == 4) launch_residual<16, 4>(p, s, 4, oa);
         else if (g == 2) launch_residual<16, 2>(p, s, 4, oa);
@@ -3836,9 +3868,9 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
                                                  static_cast<int>(B), 2 * F, D, 1, r.act, nullptr, 0, 0, 0, {}});
         break;
       }
-      for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
+      for_row_groups(B, kWideRows, [&](uint32_t r0, int g, int rows) {
         GateUpArgs ga{ctl, r.h + uint64_t(r0) * D, m->post_norm[l], reinterpret_cast<const u32x4*>(m->gu[l]),
-                      r.act + uint64_t(r0) * F, D, F, c.rms_eps};
+                      r.act + uint64_t(r0) * F, D, F, c.rms_eps, rows};
         if (g == 8) launch_gateup<8>(p, s, ga);
         else if (g == 4) launch_gateup<4>(p, s, ga);
         else if (g == 2) launch_gateup<2>(p, s, ga);
@@ -3855,10 +3887,10 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       }
       // Staging in blocks needs whole blocks of inputs; other widths keep
       // two-row launches.
-      for_row_groups(B, F % kChunkInputs == 0 ? kDownRows : 2, [&](uint32_t r0, int g) {
+      for_row_groups(B, F % kChunkInputs == 0 ? kDownRows : 2, [&](uint32_t r0, int g, int rows) {
         ResidualArgs da{ctl, r.act, reinterpret_cast<const u32x4*>(m->down[l]), r.h, p->capture, p->steer, F, D,
                         static_cast<int>(p->cap), static_cast<int>(l), static_cast<int>(r0), r.same_sequence,
-                        r.sequence};
+                        r.sequence, rows};
         if (g == 8) launch_down_chunked<8>(p, s, da);
         else if (g == 4) launch_down_chunked<4>(p, s, da);
         else if (g == 2) launch_residual<32, 2>(p, s, 6, da);
@@ -3866,9 +3898,9 @@ void launch_step_kernel(dl_plan* p, hipStream_t s, int which, uint32_t l, dl::Co
       });
       break;
     case 7:
-      for_row_groups(B, kWideRows, [&](uint32_t r0, int g) {
+      for_row_groups(B, kWideRows, [&](uint32_t r0, int g, int rows) {
         HeadArgs ha{ctl, r.h, m->final_norm, reinterpret_cast<const u32x4*>(m->lm_head), p->logits,
-                    p->partial_keys, p->partial_flags, D, V, c.rms_eps, static_cast<int>(r0)};
+                    p->partial_keys, p->partial_flags, D, V, c.rms_eps, static_cast<int>(r0), rows};
         if (g == 8) launch_head<8>(p, s, ha);
         else if (g == 4) launch_head<4>(p, s, ha);
         else if (g == 2) launch_head<2>(p, s, ha);

@@ -273,13 +273,14 @@ def test_batch_eight_equals_batch_one(small_model):
         assert np.array_equal(p8.logits(b), l1), b
 
 
-@pytest.mark.parametrize("batch", [3, 4, 5, 8])
+@pytest.mark.parametrize("batch", [3, 4, 5, 6, 7, 8])
 def test_batched_rows_follow_their_own_sequences(small_model, batch):
     """Each sequence of a batched plan samples with its own MT19937-64 seed,
     so the rows diverge; every row's token stream and last logits equal a
-    batch-1 run with that seed.  Covers the row groups of odd batches (3 = 2
-    + 1, 5 = 4 + 1) and the 4- and 8-row kernels, where a row read from or
-    written to the wrong sequence would show."""
+    batch-1 run with that seed.  Covers the 4- and 8-row kernels over all
+    their rows and over fewer rows (3 rows on the 4-row kernels, 5 to 7 on
+    the 8-row kernels, which read and write only the rows that exist),
+    where a row read from or written to the wrong sequence would show."""
     from dolittle_amd.qwen3 import Plan, SamplingSettings
     prompt = [11, 4242, 90000, 7]
     settings = SamplingSettings("categorical", 1.0, 0, 0.95)
