@@ -3459,13 +3459,20 @@ struct dl_plan {
   // Workgroups per decode-step kernel (0: one tile per wavefront).
   // Defaults from the workgroup sweep on MI355X (grid-stride over tiles).
   uint32_t grid_override[8] = {512, 0, 0, 0, 256, 768, 512, 0};
-  // Workgroups of `waves` wavefronts for `tiles` tiles: the tuned override
-  // (or one tile per wavefront), capped at what stays resident at once when the
-  // staged rows' LDS limits residency, so no workgroup repeats the staging
-  // prologue in a second round.
-  unsigned grid_for(int which, uint64_t tiles, size_t lds = 0, int waves = dl::kWaves) const {
+  // The same for launches of two to four rows where the sweep differs (0:
+  // as grid_override): gate/up at 2 and 4 rows streams faster from 192
+  // workgroups than from one or three per compute unit (at 8 rows, one per
+  // compute unit, the LDS-resident count, is faster).
+  uint32_t grid_override_rows[8] = {0, 0, 0, 0, 0, 192, 0, 0};
+  // Workgroups of `waves` wavefronts for `tiles` tiles of a `rows`-row
+  // launch: the tuned override (or one tile per wavefront), capped at what
+  // stays resident at once when the staged rows' LDS limits residency, so no
+  // workgroup repeats the staging prologue in a second round.
+  unsigned grid_for(int which, uint64_t tiles, size_t lds = 0, int waves = dl::kWaves, int rows = 1) const {
     const uint64_t full = dl::ceil_div(tiles, static_cast<uint64_t>(waves));
-    uint64_t g = grid_override[which] ? grid_override[which] : full;
+    const bool few = rows >= 2 && rows <= 4;
+    const uint32_t tuned = few && grid_override_rows[which] ? grid_override_rows[which] : grid_override[which];
+    uint64_t g = tuned ? tuned : full;
     if (lds > 0) {
       const uint64_t resident = std::max<uint64_t>(1, dl::kLdsPerCu / (lds + 1024));
       g = std::min<uint64_t>(g, resident * compute_units);
@@ -3687,7 +3694,7 @@ void launch_residual(dl_plan* p, hipStream_t s, int which, const dl::ResidualArg
 
 template <int G>
 void launch_gateup(dl_plan* p, hipStream_t s, const dl::GateUpArgs& a) {
-  dl::k_gateup<G><<<p->grid_for(5, a.F / 2, p16_lds(G, a.D), dl::gemv_waves(G)), dl::gemv_waves(G) * 64,
+  dl::k_gateup<G><<<p->grid_for(5, a.F / 2, p16_lds(G, a.D), dl::gemv_waves(G), G), dl::gemv_waves(G) * 64,
                      p16_lds(G, a.D), s>>>(a);
 }
 template <int G>
@@ -4236,6 +4243,7 @@ int dl_plan_set_grid(dl_plan* plan, uint32_t which, uint32_t blocks) {
       plan->head_blocks = static_cast<int>(blocks);
     } else {
       plan->grid_override[which] = blocks;
+      plan->grid_override_rows[which] = 0;  // the value set applies at every row count
     }
     dl::check_hip(hipStreamSynchronize(plan->queue->stream), "set grid wait");
     plan->capture_step();

@@ -510,7 +510,7 @@ int dl_plan_decode_steps(dl_plan* plan, uint32_t steps);
  * so repeated launches stream distinct weights, on the plan's queue. */
 int dl_plan_bench_prepare(dl_plan* plan);
 int dl_plan_launch_kernel(dl_plan* plan, uint32_t which, uint32_t first_layer, uint32_t count);
-/* Workgroup count of one decode-step kernel (0 restores the default of one
+/* Workgroup count of one decode-step kernel at every row count (0: one
  * weight tile per wavefront); re-records the step graph. */
 int dl_plan_set_grid(dl_plan* plan, uint32_t which, uint32_t blocks);
 /* Waits for the enqueued loop and copies each sequence's generated ids
