@@ -3416,6 +3416,8 @@ struct dl_plan {
   dl_qwen3* model = nullptr;
   dl_queue* queue = nullptr;
   uint32_t batch = 1, capacity = 0, cap = 0;  // cap: padded to 64
+  // LM head workgroups (also the argmax partials per row): 256, or 192 for
+  // plans of 2 to 4 rows (MI355X sweep: 20 us per batch-2 step faster).
   int head_blocks = 256;
   uint64_t compute_units = 256;  // queried at creation
   std::vector<void*> allocations;
@@ -4134,6 +4136,7 @@ int dl_plan_create(dl_qwen3* model, dl_queue* queue, uint32_t batch, uint32_t ca
       dl::check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device), "compute units");
       p->compute_units = static_cast<uint64_t>(std::max(cus, 1));
     }
+    if (batch >= 2 && batch <= 4) p->head_blocks = 192;
     const auto& c = model->cfg;
     const uint64_t B = batch, D = c.hidden, QW = uint64_t(c.q_heads) * c.head_dim,
                    KW = uint64_t(c.kv_heads) * c.head_dim, F = c.ffn, V = c.vocab, L = c.layers, cap = p->cap;
