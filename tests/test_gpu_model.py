@@ -300,6 +300,35 @@ def test_batched_rows_follow_their_own_sequences(small_model, batch):
     assert len(streams) > 1  # the rows really differ
 
 
+@pytest.mark.parametrize("batch,grids", [
+    (2, [(5, 768), (7, 256), (6, 256)]),   # gate/up, LM head and down off their 2-row defaults
+    (3, [(5, 96), (4, 512)]),              # 3 rows on the 4-row kernels
+    (8, [(0, 96), (6, 128), (7, 320)]),    # the 8-row Q and K/V parts on fewer workgroups
+])
+def test_workgroup_counts_do_not_change_results(small_model, batch, grids):
+    """Every output is the same FMA chain whichever workgroup runs its tile,
+    so a plan whose decode kernels are launched with other workgroup counts
+    (dl_plan_set_grid) produces the same tokens and logits as one with the
+    defaults."""
+    from dolittle_amd import _lib
+    from dolittle_amd.qwen3 import Plan, SamplingSettings
+    prompt = [5, 17, 91000, 4242, 7]
+    settings = SamplingSettings("categorical", 1.0, 0, 0.95)
+    seeds = [300 + 11 * b for b in range(batch)]
+    runs = []
+    for custom in (False, True):
+        plan = Plan(small_model, batch=batch, capacity=24)
+        if custom:
+            for which, blocks in grids:
+                _lib.call("dl_plan_set_grid", plan.handle, which, blocks)
+        plan.generate(prompt, 10, settings, seeds)
+        tokens, _ = plan.collect()
+        runs.append((tokens, [plan.logits(b) for b in range(batch)]))
+    assert np.array_equal(runs[0][0], runs[1][0])
+    for b in range(batch):
+        assert np.array_equal(runs[0][1][b], runs[1][1][b]), b
+
+
 def _categorical_run(plan, prompt, max_new, settings, seeds, override=None, stop_ids=None):
     """Drives the loop one step at a time; returns the per-step logits rows
     and the emitted tokens of every sequence."""
