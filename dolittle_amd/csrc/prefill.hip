@@ -453,13 +453,15 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   gemm_tile_epilogue<EPI, 2, 4>(a, acc, m0 + 64 * wm, n0 + 128 * wn, lane);
 }
 
-// 256 x 256 tiles for the wide GEMMs (gate/up, O, down): four waves of
-// 128 x 128 (4 x 4 MFMA tiles, 256 FP32 accumulators per lane), so a
-// 16-deep K step reads 8 operand fragments from LDS for 16 products (0.5
-// per product, against 0.75 for k_gemm_dma's 64 x 128 waves) and a
-// workgroup brings 64 KB per 32 K positions for twice k_gemm_dma's work.
-// K chunks of 32 positions go through a ring of four 32 KB LDS stages by
-// direct global-to-LDS loads, three chunks ahead.  Per chunk, each wave
+// 256 x 256 tiles for the wide GEMMs (gate/up, O, down): eight waves of
+// 64 x 128 (2 x 4 MFMA tiles, 128 FP32 accumulators per lane), two per
+// SIMD, so one wave's barrier and fragment waits overlap the other's
+// products (four waves of 128 x 128, one per SIMD, took 77.4 against 75.7
+// ms for the 4096-id prompt, the same outputs); a 16-deep K step reads 6
+// operand fragments from LDS for 8 products, and a workgroup brings 64 KB
+// per 32 K positions for twice k_gemm_dma's work.  K chunks of 32
+// positions go through a ring of four 32 KB LDS stages by direct
+// global-to-LDS loads, three chunks ahead.  Per chunk, each wave
 //   - reads the second K step's fragments (F1) of chunk c,
 //   - issues chunk c + 3 into the stage chunk c - 1 left, between the
 //     products of the first K step (F0, read in the previous chunk),
@@ -471,21 +473,22 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 // products.  Stage rows use k_gemm_dma's 64-byte swizzled rows.
 constexpr int kBigM = 256;
 constexpr int kBigStageElems = (kBigM + kDmaTN) * kDmaTK;  // A rows then W rows
-constexpr int kBigLoads = kBigStageElems / 8 / kGemmThreads;  // 16-byte loads per thread per chunk: 8
 
 // s_waitcnt immediate: at most n vector-memory operations outstanding and no
 // LDS operation outstanding (lgkmcnt 0; expcnt at its no-wait maximum).
 constexpr unsigned vm_lds_wait(unsigned n) { return 0x0070u | (n & 0xfu) | ((n >> 4) << 14); }
 
+constexpr int kBigThreads = 512;
+constexpr int kBigLoads = kBigStageElems / 8 / kBigThreads;  // 16-byte loads per thread per chunk: 4
+
 struct BigFrags {
-  bf16x8 a[4], b[4];
+  bf16x8 a[2], b[4];
 };
 
 template <int EPI>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1))) void k_gemm_big(GemmArgs a) {
+__global__ __launch_bounds__(kBigThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_big(GemmArgs a) {
   __shared__ __align__(1024) uint16_t S0[kBigStageElems], S1[kBigStageElems], S2[kBigStageElems],
       S3[kBigStageElems];
-  // Tile order as k_gemm_dma (XCD-contiguous eighths of a grouped raster).
   const int nN = gridDim.x, nM = gridDim.y, total = nN * nM;
   const int id = blockIdx.x + blockIdx.y * nN;
   const int v = total % kXcds == 0 ? (id % kXcds) * (total / kXcds) + id / kXcds : id;
@@ -502,29 +505,28 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1)
   const int tid = threadIdx.x, lane = tid % 64;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
   const int wm = wave >> 1, wn = wave & 1;
-
-  // Load j of this wave fills stage rows 16 (4 j + wave) .. + 15 of A
-  // (j < 4) or of W (j >= 4); lane L brings row + L / 4, physical piece L % 4.
+  // Load j of this wave fills stage rows 16 (8 j + wave) .. + 15 of A (j < 2)
+  // or of W (j >= 2).
   const int lr = lane / 4, lp = lane % 4;
-  const uint16_t* src[8];
+  const uint16_t* src[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = 16 * (4 * j + wave) + lr;
+  for (int j = 0; j < 2; ++j) {
+    const int r = 16 * (8 * j + wave) + lr;
     src[j] = A + static_cast<uint64_t>(m0 + r) * K + 8 * (lp ^ dma_swizzle(r));
-    src[4 + j] = W + packed_offset(nb + r, P, K, 0) + 8 * (lp ^ dma_swizzle(r));
+    src[2 + j] = W + packed_offset(nb + r, P, K, 0) + 8 * (lp ^ dma_swizzle(r));
   }
   const int block_shift = __builtin_ctz(8 * P), block_mask = 8 * P - 1;
   auto issue = [&](int c, uint16_t* S) {
     const int kp = c * kDmaTK;
     const uint64_t woff = (static_cast<uint64_t>(kp >> block_shift) << 9) + (kp & block_mask);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_global_load_lds((const global_void*)(src[j] + kp), (lds_void*)(S + 16 * (4 * j + wave) * kDmaTK),
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds((const global_void*)(src[j] + kp), (lds_void*)(S + 16 * (8 * j + wave) * kDmaTK),
                                        16, 0, 0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_global_load_lds((const global_void*)(src[4 + j] + woff),
-                                       (lds_void*)(S + (kBigM + 16 * (4 * j + wave)) * kDmaTK), 16, 0, 0);
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds((const global_void*)(src[2 + j] + woff),
+                                       (lds_void*)(S + (kBigM + 16 * (8 * j + wave)) * kDmaTK), 16, 0, 0);
   };
   const int sw = dma_swizzle(lane % 32);
   int frag[2];
@@ -532,50 +534,45 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1)
   for (int ks = 0; ks < 2; ++ks) frag[ks] = (lane % 32) * kDmaTK + 8 * ((2 * ks + lane / 32) ^ sw);
   auto read = [&](const uint16_t* S, int ks, BigFrags& f) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      f.a[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&S[(128 * wm + 32 * i) * kDmaTK + frag[ks]]));
+    for (int i = 0; i < 2; ++i)
+      f.a[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(&S[(64 * wm + 32 * i) * kDmaTK + frag[ks]]));
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       f.b[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(&S[(kBigM + 128 * wn + 32 * j) * kDmaTK + frag[ks]]));
   };
-  floatx16 acc[4][4];
+  floatx16 acc[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   auto products = [&](const BigFrags& f) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
   };
-
-  // First K step: F1's 8 fragment reads spread over the first 8 products
-  // (after the first two, so the wait for F0's reads, long landed, does not
-  // also wait for F1's), then the other 8 products with the next loads
-  // between them.  Second: F0's reads of the next chunk spread over the
-  // first 8 products.
-  auto big_first_schedule = [] {
+  auto first_schedule = [] {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+    for (int t = 0; t < 3; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS reads
     }
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < 4; ++t) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global-to-LDS load
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
   };
-  auto big_second_schedule = [] {
+  auto second_schedule = [] {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    for (int t = 0; t < 3; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 5, 0);
   };
   issue(0, S0);
   issue(min(1, chunks - 1), S1);
@@ -586,23 +583,19 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1)
   BigFrags f0, f1;
   read(S0, 0, f0);
   int c = 0;
-  // One chunk: Sc holds chunk c, Sn chunk c + 1, Sf is free for chunk c + 3.
-  // Past the last chunk the loads repeat it into the free stage, so every
-  // chunk issues and waits with the same counts (and the last chunk's F0
-  // read of "chunk c + 1" reads such a landed repeat, never used).
-#define DL_BIG_STEP(Sc, Sn, Sf)                                            \
+#define DL_BIG_STEP(Sc, Sn, Sf)                                           \
   do {                                                                     \
     read(Sc, 1, f1);                                                       \
     issue(min(c + 3, chunks - 1), Sf);                                     \
     products(f0);                                                          \
-    big_first_schedule();                                                  \
+    first_schedule();                                                      \
     __builtin_amdgcn_sched_barrier(0);                                     \
-    __builtin_amdgcn_s_waitcnt(vm_lds_wait(2 * kBigLoads));               \
+    __builtin_amdgcn_s_waitcnt(vm_lds_wait(2 * kBigLoads));              \
     __builtin_amdgcn_s_barrier();                                          \
     __builtin_amdgcn_sched_barrier(0);                                     \
     read(Sn, 0, f0);                                                       \
     products(f1);                                                          \
-    big_second_schedule();                                                 \
+    second_schedule();                                                     \
     __builtin_amdgcn_sched_barrier(0);                                     \
     ++c;                                                                   \
   } while (0)
@@ -617,7 +610,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1)
   if (c < chunks) DL_BIG_STEP(S2, S3, S1);
 #undef DL_BIG_STEP
   __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));  // no load outlives the wave
-  gemm_tile_epilogue<EPI, 4, 4>(a, acc, m0 + 128 * wm, n0 + 128 * wn, lane);
+  gemm_tile_epilogue<EPI, 2, 4>(a, acc, m0 + 64 * wm, n0 + 128 * wn, lane);
 }
 
 // ------------------------------------------------------------- row norms
@@ -992,9 +985,9 @@ void launch_gemm(hipStream_t stream, const GemmArgs& a) {
       (a.N / 256) * (a.M / kBigM) >= 256) {
     const dim3 grid(a.N / kDmaTN, a.M / kBigM);
     switch (a.epilogue) {
-      case kStore: hipLaunchKernelGGL((k_gemm_big<kStore>), grid, dim3(kGemmThreads), 0, stream, a); break;
-      case kResidual: hipLaunchKernelGGL((k_gemm_big<kResidual>), grid, dim3(kGemmThreads), 0, stream, a); break;
-      default: hipLaunchKernelGGL((k_gemm_big<kGateUp>), grid, dim3(kGemmThreads), 0, stream, a); break;
+      case kStore: hipLaunchKernelGGL((k_gemm_big<kStore>), grid, dim3(kBigThreads), 0, stream, a); break;
+      case kResidual: hipLaunchKernelGGL((k_gemm_big<kResidual>), grid, dim3(kBigThreads), 0, stream, a); break;
+      default: hipLaunchKernelGGL((k_gemm_big<kGateUp>), grid, dim3(kBigThreads), 0, stream, a); break;
     }
     return;
   }
