@@ -818,8 +818,10 @@ __global__ __launch_bounds__(64) void k_attn_softmax_rows(AttnArgs a) {
 // time is one wave's chain however the waves are placed on SIMDs.
 //
 // A wave issues at most one instruction per issue cycle of its SIMD, so the
-// chain wave's time is its instruction count per key: one FMA, a quarter of
-// a 16-byte LDS read for V and one for the probabilities, and its waits.
+// chain wave's time is its instruction count per key: one FMA (its
+// probability broadcast within the lane's quad by DPP), a quarter of a
+// 16-byte LDS read for V, a sixteenth of one for the probabilities, and its
+// waits.
 // The other two waves keep everything else off it:
 // - wave 1 copies: each chunk's 8 V rows (BF16, both ranges) and 8
 //   probability rows (FP32) go from global memory straight into a
@@ -857,6 +859,36 @@ constexpr unsigned pv_vmcnt(unsigned n) { return 0x0f70u | (n & 0xfu) | ((n >> 4
 // s_waitcnt immediate waiting until no LDS operation of this wave is
 // outstanding (lgkmcnt bits 11:8 zero; vmcnt and expcnt at their maxima).
 constexpr unsigned kPvLdsDone = 0xc07fu;
+
+// acc = fma(p_key, v[key], acc) for key = 4k + j, k and j = 0..3 ascending:
+// p component j of quad lane k (DPP quad_perm broadcast), v[k] component j.
+// v_fmac_f32 is the single-rounding FMA (fma_rn); the s_nop covers the two
+// wait states a DPP read needs after a VALU write of its source.
+__device__ __forceinline__ float fma16_quad_bcast(float acc, const float4& p, const float4 (&v)[4]) {
+  asm volatile(
+      "s_nop 1\n"
+      "v_fmac_f32_dpp %0, %1, %5 quad_perm:[0,0,0,0] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %2, %6 quad_perm:[0,0,0,0] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %3, %7 quad_perm:[0,0,0,0] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %4, %8 quad_perm:[0,0,0,0] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %9 quad_perm:[1,1,1,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %2, %10 quad_perm:[1,1,1,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %3, %11 quad_perm:[1,1,1,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %4, %12 quad_perm:[1,1,1,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %13 quad_perm:[2,2,2,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %2, %14 quad_perm:[2,2,2,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %3, %15 quad_perm:[2,2,2,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %4, %16 quad_perm:[2,2,2,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %1, %17 quad_perm:[3,3,3,3] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %2, %18 quad_perm:[3,3,3,3] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %3, %19 quad_perm:[3,3,3,3] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %4, %20 quad_perm:[3,3,3,3] row_mask:0xf bank_mask:0xf\n"
+      : "+v"(acc)
+      : "v"(p.x), "v"(p.y), "v"(p.z), "v"(p.w), "v"(v[0].x), "v"(v[0].y), "v"(v[0].z), "v"(v[0].w), "v"(v[1].x),
+        "v"(v[1].y), "v"(v[1].z), "v"(v[1].w), "v"(v[2].x), "v"(v[2].y), "v"(v[2].z), "v"(v[2].w), "v"(v[3].x),
+        "v"(v[3].y), "v"(v[3].z), "v"(v[3].w));
+  return acc;
+}
 
 __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
   extern __shared__ __align__(16) uint8_t pv_lds[];
@@ -967,29 +999,29 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnArgs a) {
       const int cs0 = kPvChunk * c, cs1 = jb0_1 + kPvChunk * c;
       const bool full = cs0 + kPvChunk <= end0 && begin1 <= cs1 && cs1 + kPvChunk <= end1;
       if (full) {
-        // The reads of group q + kAhead are issued before the FMAs of group
-        // q (the order is pinned with scheduling barriers), so the LDS
-        // latency hides behind the chain and the waits stay partial (at most
-        // 4 kAhead reads are outstanding; the wait counter has 4 bits).
-        constexpr int kGroups = kPvChunk / 8, kAhead = 3;
-        float4 va[kGroups], vc[kGroups], pa[kGroups], pc[kGroups];
-        auto read = [&](int q) {
-          va[q] = *reinterpret_cast<const float4*>(vb + 32 * q);
-          vc[q] = *reinterpret_cast<const float4*>(vb + 32 * q + 16);
-          pa[q] = *reinterpret_cast<const float4*>(pb + 32 * (2 * q));
-          pc[q] = *reinterpret_cast<const float4*>(pb + 32 * (2 * q + 1));
+        // 16-key groups m: four 16-byte reads of the lane's widened V row
+        // and one of its head's probabilities, keys 16 m + 4 f .. + 3 (the
+        // lanes of a quad share the head, so each quad holds the 16 keys'
+        // probabilities and fma16_quad_bcast broadcasts them).  The reads
+        // of group m + kAhead are issued before the FMAs of group m (the
+        // order is pinned with scheduling barriers), so the LDS latency
+        // hides behind the chain and the waits stay partial (at most
+        // 5 kAhead reads are outstanding; the wait counter has 4 bits).
+        constexpr int kGroups = kPvChunk / 16, kAhead = 2;
+        float4 v4[kGroups][4], p4[kGroups];
+        auto read = [&](int m) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v4[m][i] = *reinterpret_cast<const float4*>(vb + 64 * m + 16 * i);
+          p4[m] = *reinterpret_cast<const float4*>(pb + 128 * m + 32 * f);
         };
 #pragma unroll
-        for (int q = 0; q < kAhead; ++q) read(q);
+        for (int m = 0; m < kAhead; ++m) read(m);
 #pragma unroll
-        for (int q = 0; q < kGroups; ++q) {
+        for (int m = 0; m < kGroups; ++m) {
           __builtin_amdgcn_sched_barrier(0);
-          if (q + kAhead < kGroups) read(q + kAhead);
+          if (m + kAhead < kGroups) read(m + kAhead);
           __builtin_amdgcn_sched_barrier(0);
-          const float vv[8] = {va[q].x, va[q].y, va[q].z, va[q].w, vc[q].x, vc[q].y, vc[q].z, vc[q].w};
-          const float pp[8] = {pa[q].x, pa[q].y, pa[q].z, pa[q].w, pc[q].x, pc[q].y, pc[q].z, pc[q].w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc = fma_rn(pp[e], vv[e], acc);
+          acc = fma16_quad_bcast(acc, p4[m], v4[m]);
         }
       } else {
         // Keys [lo, hi) of this lane's range in the chunk (empty once the
